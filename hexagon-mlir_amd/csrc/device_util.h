@@ -1,0 +1,72 @@
+// Device-side helpers for gfx950 kernels: 16-byte vector types, element
+// conversions and 64-lane wave reductions built from DPP row operations plus
+// cross-row readlanes (the GPU analogue of the hvx.vror rotate-and-fold
+// butterfly, qcom_hexagon_backend/lib/Conversion/LinalgToLLVM/
+// VectorRowReducePass.cpp:10-31).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace hxm {
+
+typedef int32_t v4i32 __attribute__((ext_vector_type(4)));
+typedef int32_t v16i32 __attribute__((ext_vector_type(16)));
+typedef float v4f32 __attribute__((ext_vector_type(4)));
+typedef float v16f32 __attribute__((ext_vector_type(16)));
+typedef _Float16 v8f16 __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf16 __attribute__((ext_vector_type(8)));
+typedef _Float16 v2f16 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float tof(_Float16 v) { return static_cast<float>(v); }
+__device__ __forceinline__ float tof(__bf16 v) { return static_cast<float>(v); }
+__device__ __forceinline__ float tof(float v) { return v; }
+
+template <typename T>
+__device__ __forceinline__ T fromf(float v) { return static_cast<T>(v); }
+
+// DPP controls (GCN/CDNA encoding).
+constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                         0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+struct OpMax {
+  __device__ __forceinline__ float operator()(float a, float b) const {
+    return fmaxf(a, b);
+  }
+};
+struct OpSum {
+  __device__ __forceinline__ float operator()(float a, float b) const {
+    return a + b;
+  }
+};
+
+// Reduces v over all 64 lanes; the result is wave-uniform.  Inside each
+// 16-lane row: xor-1, xor-2, half-mirror, mirror (every lane ends with its
+// row's total); across rows: four readlanes folded pairwise.
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+  v = op(v, dpp<kDppQuadXor1>(v));
+  v = op(v, dpp<kDppQuadXor2>(v));
+  v = op(v, dpp<kDppRowHalfMirror>(v));
+  v = op(v, dpp<kDppRowMirror>(v));
+  float a = op(readlane(v, 0), readlane(v, 16));
+  float b = op(readlane(v, 32), readlane(v, 48));
+  return op(a, b);
+}
+
+}  // namespace hxm

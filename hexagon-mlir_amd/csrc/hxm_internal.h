@@ -1,0 +1,62 @@
+// Internal helpers shared by the HIP translation units of libhxm: status and
+// reason reporting, dtype sizes, launch checks and the library-owned
+// per-stream workspace.  Nothing here is part of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/hxm.h"
+
+namespace hxm {
+
+// Records `reason` as this thread's last error and returns `st`.  Reasons
+// start with the manifest vocabulary word ("tile-alignment", ...) so that a
+// caller can switch on the prefix.
+hxm_status fail(hxm_status st, const char* fmt, ...)
+    __attribute__((format(printf, 2, 3)));
+// Clears the thread's last error and returns HXM_OK.
+hxm_status ok();
+
+inline int64_t dtype_bytes(int32_t dt) {
+  switch (dt) {
+    case HXM_F16:
+    case HXM_BF16: return 2;
+    case HXM_F32:
+    case HXM_I32: return 4;
+    case HXM_I8: return 1;
+    default: return 0;
+  }
+}
+
+inline bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// Checks the launch that was just enqueued.
+hxm_status check_launch(const char* what);
+
+// Current device's gfx950 check (cached per device).  Returns HXM_OK or
+// HXM_NO_DEVICE with a reason.
+hxm_status require_device(int* device_out);
+
+// Library-owned scratch for one (device, stream) pair, grown on demand and
+// kept until hxm_release_cache().  Calls on the same stream are ordered, so
+// one buffer per stream never races with itself.
+hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace hxm
+
+#define HXM_HIP_TRY(expr)                                                    \
+  do {                                                                       \
+    hipError_t _e = (expr);                                                  \
+    if (_e != hipSuccess)                                                    \
+      return ::hxm::fail(HXM_HIP_ERROR, "hip-error: %s failed: %s", #expr,   \
+                         hipGetErrorString(_e));                             \
+  } while (0)

@@ -1,0 +1,392 @@
+// Row reductions on gfx950: softmax, RMSNorm, LayerNorm.
+//
+// Reference semantics: test/python/triton/test_softmax.py:41-69 (max-subtract,
+// exp in fp32, sum, divide), test_rms_norm.py:34-60 (x / sqrt(mean(x^2)+eps)
+// * g), test_layer_norm.py:39-79 (mean, biased variance, rstd, affine, mean and
+// rstd written per row), as lowered on the HVX path by
+// lib/Conversion/LinalgToLLVM/VectorRowReducePass.cpp:10-31 (vector fold +
+// rotate butterfly) and SplitReduceGenericPass.cpp:62-93.
+//
+// Design: one wave per row, four rows per 256-thread workgroup.  A row of up to
+// 64 lanes x 16 vectors x 16 bytes is loaded ONCE into registers with 128-bit
+// coalesced loads (consecutive lanes read consecutive 16-byte chunks), reduced
+// across the wave with DPP + readlane (no LDS, no barriers) and written back
+// from registers: one HBM read and one HBM write per element.  Longer rows use
+// the streaming variant (VPL = 0) that re-reads the row per pass.
+#include "device_util.h"
+#include "hxm_internal.h"
+
+namespace hxm {
+
+enum RowOp { kSoftmax = 0, kRmsNorm = 1, kLayerNorm = 2 };
+
+constexpr int kRowWaves = 4;  // rows (waves) per workgroup
+
+template <typename T>
+struct RowVec {
+  static constexpr int N = 16 / sizeof(T);  // elements per 16-byte vector
+};
+
+// Loads the 16-byte vector starting at column c0 into f[], padding columns
+// >= cols with `fill`.  ALIGNED means the row base is 16-byte aligned, so a
+// full in-bounds vector is one dwordx4 load.
+template <typename T, bool ALIGNED>
+__device__ __forceinline__ void load_vec(const T* __restrict__ row, int64_t c0,
+                                         int64_t cols, float fill,
+                                         float (&f)[RowVec<T>::N]) {
+  constexpr int N = RowVec<T>::N;
+  if (ALIGNED && c0 + N <= cols) {
+    typedef T vt __attribute__((ext_vector_type(N)));
+    vt v = *reinterpret_cast<const vt*>(row + c0);
+#pragma unroll
+    for (int j = 0; j < N; ++j) f[j] = tof(v[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) f[j] = (c0 + j < cols) ? tof(row[c0 + j]) : fill;
+  }
+}
+
+template <typename T, bool ALIGNED>
+__device__ __forceinline__ void store_vec(T* __restrict__ row, int64_t c0,
+                                          int64_t cols,
+                                          const float (&f)[RowVec<T>::N]) {
+  constexpr int N = RowVec<T>::N;
+  if (ALIGNED && c0 + N <= cols) {
+    typedef T vt __attribute__((ext_vector_type(N)));
+    vt v;
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = fromf<T>(f[j]);
+    *reinterpret_cast<vt*>(row + c0) = v;
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (c0 + j < cols) row[c0 + j] = fromf<T>(f[j]);
+  }
+}
+
+// exp(x) for x <= 0 via the hardware exp2 (v_exp_f32): exp(x) = 2^(x*log2 e).
+__device__ __forceinline__ float exp_f32(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
+struct RowArgs {
+  const void* x;
+  int64_t ldx;
+  void* y;
+  int64_t ldy;
+  const void* gamma;
+  const void* beta;
+  float* mean_out;
+  float* rstd_out;
+  int64_t rows;
+  int64_t cols;
+  float eps;
+};
+
+// Register-resident kernel: each lane holds VPL vectors of the row.
+template <typename T, int OP, int VPL, bool ALIGNED>
+__global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
+  constexpr int N = RowVec<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * kRowWaves + (threadIdx.x >> 6);
+  if (r >= a.rows) return;  // whole wave leaves; no barriers below
+  const T* __restrict__ xr = static_cast<const T*>(a.x) + r * a.ldx;
+  T* __restrict__ yr = static_cast<T*>(a.y) + r * a.ldy;
+  const int64_t cols = a.cols;
+
+  float v[VPL][N];
+  const float fill = (OP == kSoftmax) ? -__builtin_huge_valf() : 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i)
+    load_vec<T, ALIGNED>(xr, (static_cast<int64_t>(i) * 64 + lane) * N, cols, fill, v[i]);
+
+  if constexpr (OP == kSoftmax) {
+    float m = -__builtin_huge_valf();
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int j = 0; j < N; ++j) m = fmaxf(m, v[i][j]);
+    m = wave_reduce(m, OpMax());
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        v[i][j] = exp_f32(v[i][j] - m);  // padded -inf -> 0
+        s += v[i][j];
+      }
+    s = wave_reduce(s, OpSum());
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int j = 0; j < N; ++j) v[i][j] *= inv;
+  } else if constexpr (OP == kRmsNorm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int j = 0; j < N; ++j) ss += v[i][j] * v[i][j];
+    ss = wave_reduce(ss, OpSum());
+    const float rstd = 1.0f / sqrtf(ss / static_cast<float>(cols) + a.eps);
+    const T* __restrict__ g = static_cast<const T*>(a.gamma);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int64_t c0 = (static_cast<int64_t>(i) * 64 + lane) * N;
+      float gv[N];
+      if (g) load_vec<T, ALIGNED>(g, c0, cols, 0.0f, gv);
+#pragma unroll
+      for (int j = 0; j < N; ++j) v[i][j] = (v[i][j] * rstd) * (g ? gv[j] : 1.0f);
+    }
+  } else {  // kLayerNorm
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int j = 0; j < N; ++j) s += v[i][j];
+    const float mean = wave_reduce(s, OpSum()) / static_cast<float>(cols);
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int64_t c0 = (static_cast<int64_t>(i) * 64 + lane) * N;
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        const float d = (c0 + j < cols) ? v[i][j] - mean : 0.0f;
+        q += d * d;
+      }
+    }
+    const float var = wave_reduce(q, OpSum()) / static_cast<float>(cols);
+    const float rstd = 1.0f / sqrtf(var + a.eps);
+    if (lane == 0) {
+      if (a.mean_out) a.mean_out[r] = mean;
+      if (a.rstd_out) a.rstd_out[r] = rstd;
+    }
+    const T* __restrict__ g = static_cast<const T*>(a.gamma);
+    const T* __restrict__ b = static_cast<const T*>(a.beta);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int64_t c0 = (static_cast<int64_t>(i) * 64 + lane) * N;
+      float gv[N], bv[N];
+      if (g) load_vec<T, ALIGNED>(g, c0, cols, 0.0f, gv);
+      if (b) load_vec<T, ALIGNED>(b, c0, cols, 0.0f, bv);
+#pragma unroll
+      for (int j = 0; j < N; ++j)
+        v[i][j] = (v[i][j] - mean) * rstd * (g ? gv[j] : 1.0f) + (b ? bv[j] : 0.0f);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < VPL; ++i)
+    store_vec<T, ALIGNED>(yr, (static_cast<int64_t>(i) * 64 + lane) * N, cols, v[i]);
+}
+
+// Streaming kernel for rows longer than the register budget: the row is
+// re-read per pass (softmax keeps an online max/sum so it needs 2 passes,
+// RMSNorm 2, LayerNorm 3).
+template <typename T, int OP, bool ALIGNED>
+__global__ __launch_bounds__(256) void row_kernel_stream(RowArgs a) {
+  constexpr int N = RowVec<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * kRowWaves + (threadIdx.x >> 6);
+  if (r >= a.rows) return;
+  const T* __restrict__ xr = static_cast<const T*>(a.x) + r * a.ldx;
+  T* __restrict__ yr = static_cast<T*>(a.y) + r * a.ldy;
+  const int64_t cols = a.cols;
+  const int64_t step = 64 * N;
+  const T* __restrict__ g = static_cast<const T*>(a.gamma);
+  const T* __restrict__ b = static_cast<const T*>(a.beta);
+
+  float scale = 1.0f, shift = 0.0f;  // y = (x - shift) * scale [* g + b]
+  float m = 0.0f;
+  if constexpr (OP == kSoftmax) {
+    float lm = -__builtin_huge_valf(), ls = 0.0f;
+    for (int64_t c0 = lane * N; c0 < cols; c0 += step) {
+      float f[N];
+      load_vec<T, ALIGNED>(xr, c0, cols, -__builtin_huge_valf(), f);
+      float cm = lm;
+#pragma unroll
+      for (int j = 0; j < N; ++j) cm = fmaxf(cm, f[j]);
+      if (cm > lm) {
+        ls = (lm == -__builtin_huge_valf()) ? 0.0f : ls * exp_f32(lm - cm);
+        lm = cm;
+      }
+      if (lm != -__builtin_huge_valf())
+#pragma unroll
+        for (int j = 0; j < N; ++j) ls += exp_f32(f[j] - lm);
+    }
+    m = wave_reduce(lm, OpMax());
+    float part = (lm == -__builtin_huge_valf()) ? 0.0f : ls * exp_f32(lm - m);
+    const float s = wave_reduce(part, OpSum());
+    scale = 1.0f / s;
+  } else if constexpr (OP == kRmsNorm) {
+    float ss = 0.0f;
+    for (int64_t c0 = lane * N; c0 < cols; c0 += step) {
+      float f[N];
+      load_vec<T, ALIGNED>(xr, c0, cols, 0.0f, f);
+#pragma unroll
+      for (int j = 0; j < N; ++j) ss += f[j] * f[j];
+    }
+    ss = wave_reduce(ss, OpSum());
+    scale = 1.0f / sqrtf(ss / static_cast<float>(cols) + a.eps);
+  } else {
+    float s = 0.0f;
+    for (int64_t c0 = lane * N; c0 < cols; c0 += step) {
+      float f[N];
+      load_vec<T, ALIGNED>(xr, c0, cols, 0.0f, f);
+#pragma unroll
+      for (int j = 0; j < N; ++j) s += f[j];
+    }
+    const float mean = wave_reduce(s, OpSum()) / static_cast<float>(cols);
+    float q = 0.0f;
+    for (int64_t c0 = lane * N; c0 < cols; c0 += step) {
+      float f[N];
+      load_vec<T, ALIGNED>(xr, c0, cols, 0.0f, f);
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        const float d = (c0 + j < cols) ? f[j] - mean : 0.0f;
+        q += d * d;
+      }
+    }
+    const float var = wave_reduce(q, OpSum()) / static_cast<float>(cols);
+    shift = mean;
+    scale = 1.0f / sqrtf(var + a.eps);
+    if (lane == 0) {
+      if (a.mean_out) a.mean_out[r] = mean;
+      if (a.rstd_out) a.rstd_out[r] = scale;
+    }
+  }
+
+  for (int64_t c0 = lane * N; c0 < cols; c0 += step) {
+    float f[N];
+    load_vec<T, ALIGNED>(xr, c0, cols, 0.0f, f);
+    if constexpr (OP == kSoftmax) {
+#pragma unroll
+      for (int j = 0; j < N; ++j) f[j] = exp_f32(f[j] - m) * scale;
+    } else if constexpr (OP == kRmsNorm) {
+      float gv[N];
+      if (g) load_vec<T, ALIGNED>(g, c0, cols, 0.0f, gv);
+#pragma unroll
+      for (int j = 0; j < N; ++j) f[j] = (f[j] * scale) * (g ? gv[j] : 1.0f);
+    } else {
+      float gv[N], bv[N];
+      if (g) load_vec<T, ALIGNED>(g, c0, cols, 0.0f, gv);
+      if (b) load_vec<T, ALIGNED>(b, c0, cols, 0.0f, bv);
+#pragma unroll
+      for (int j = 0; j < N; ++j)
+        f[j] = (f[j] - shift) * scale * (g ? gv[j] : 1.0f) + (b ? bv[j] : 0.0f);
+    }
+    store_vec<T, ALIGNED>(yr, c0, cols, f);
+  }
+}
+
+namespace {
+
+template <typename T, int OP, bool ALIGNED>
+hxm_status launch_rows_t(const RowArgs& a, hipStream_t stream) {
+  constexpr int N = RowVec<T>::N;
+  const int64_t vpl = (a.cols + 64 * N - 1) / (64 * N);
+  const dim3 grid(static_cast<unsigned>((a.rows + kRowWaves - 1) / kRowWaves));
+  const dim3 block(64 * kRowWaves);
+  if (vpl <= 1)
+    row_kernel<T, OP, 1, ALIGNED><<<grid, block, 0, stream>>>(a);
+  else if (vpl <= 2)
+    row_kernel<T, OP, 2, ALIGNED><<<grid, block, 0, stream>>>(a);
+  else if (vpl <= 4)
+    row_kernel<T, OP, 4, ALIGNED><<<grid, block, 0, stream>>>(a);
+  else if (vpl <= 8)
+    row_kernel<T, OP, 8, ALIGNED><<<grid, block, 0, stream>>>(a);
+  else if (vpl <= 16)
+    row_kernel<T, OP, 16, ALIGNED><<<grid, block, 0, stream>>>(a);
+  else
+    row_kernel_stream<T, OP, ALIGNED><<<grid, block, 0, stream>>>(a);
+  return check_launch("row kernel");
+}
+
+template <int OP>
+hxm_status launch_rows(const RowArgs& a, int32_t dtype, hipStream_t stream) {
+  const int64_t eb = dtype_bytes(dtype);
+  bool al = aligned16(a.x) && aligned16(a.y) && (a.ldx * eb) % 16 == 0 &&
+            (a.ldy * eb) % 16 == 0 && (!a.gamma || aligned16(a.gamma)) &&
+            (!a.beta || aligned16(a.beta));
+  switch (dtype) {
+    case HXM_F16:
+      return al ? launch_rows_t<_Float16, OP, true>(a, stream)
+                : launch_rows_t<_Float16, OP, false>(a, stream);
+    case HXM_BF16:
+      return al ? launch_rows_t<__bf16, OP, true>(a, stream)
+                : launch_rows_t<__bf16, OP, false>(a, stream);
+    default:
+      return al ? launch_rows_t<float, OP, true>(a, stream)
+                : launch_rows_t<float, OP, false>(a, stream);
+  }
+}
+
+hxm_status validate_rows(const char* op, const void* x, int64_t ldx,
+                         const void* y, int64_t ldy, int64_t rows,
+                         int64_t cols, int32_t dtype) {
+  if (dtype != HXM_F16 && dtype != HXM_BF16 && dtype != HXM_F32)
+    return fail(HXM_UNSUPPORTED_DTYPE,
+                "unsupported-dtype: %s takes f16, bf16 or f32 (got %d)", op,
+                dtype);
+  if (rows < 0 || cols < 1)
+    return fail(HXM_INVALID_ARG, "invalid-argument: %s rows=%lld cols=%lld",
+                op, (long long)rows, (long long)cols);
+  if (rows > 0 && (!x || !y))
+    return fail(HXM_INVALID_ARG, "invalid-argument: %s null x or y", op);
+  if (ldx < cols || ldy < cols)
+    return fail(HXM_INVALID_ARG,
+                "invalid-argument: %s ldx=%lld ldy=%lld < cols=%lld", op,
+                (long long)ldx, (long long)ldy, (long long)cols);
+  if (rows > (int64_t(1) << 33))
+    return fail(HXM_UNSUPPORTED_SHAPE, "tile-alignment: %s rows=%lld too many",
+                op, (long long)rows);
+  return HXM_OK;
+}
+
+}  // namespace
+}  // namespace hxm
+
+using namespace hxm;
+
+extern "C" {
+
+hxm_status hxm_softmax_rows(const void* x, int64_t ldx, void* y, int64_t ldy,
+                            int64_t rows, int64_t cols, int32_t dtype,
+                            void* stream) {
+  hxm_status st = validate_rows("softmax", x, ldx, y, ldy, rows, cols, dtype);
+  if (st != HXM_OK) return st;
+  if ((st = require_device(nullptr)) != HXM_OK) return st;
+  if (rows == 0) return ok();
+  RowArgs a{x, ldx, y, ldy, nullptr, nullptr, nullptr, nullptr, rows, cols, 0.0f};
+  return launch_rows<kSoftmax>(a, dtype, as_stream(stream));
+}
+
+hxm_status hxm_rmsnorm_rows(const void* x, int64_t ldx, const void* gamma,
+                            void* y, int64_t ldy, int64_t rows, int64_t cols,
+                            float eps, int32_t dtype, void* stream) {
+  hxm_status st = validate_rows("rmsnorm", x, ldx, y, ldy, rows, cols, dtype);
+  if (st != HXM_OK) return st;
+  if (!(eps >= 0.0f))
+    return fail(HXM_INVALID_ARG, "invalid-argument: rmsnorm eps must be >= 0");
+  if ((st = require_device(nullptr)) != HXM_OK) return st;
+  if (rows == 0) return ok();
+  RowArgs a{x, ldx, y, ldy, gamma, nullptr, nullptr, nullptr, rows, cols, eps};
+  return launch_rows<kRmsNorm>(a, dtype, as_stream(stream));
+}
+
+hxm_status hxm_layernorm_rows(const void* x, int64_t ldx, const void* gamma,
+                              const void* beta, void* y, int64_t ldy,
+                              float* mean_out, float* rstd_out, int64_t rows,
+                              int64_t cols, float eps, int32_t dtype,
+                              void* stream) {
+  hxm_status st = validate_rows("layernorm", x, ldx, y, ldy, rows, cols, dtype);
+  if (st != HXM_OK) return st;
+  if (!(eps >= 0.0f))
+    return fail(HXM_INVALID_ARG, "invalid-argument: layernorm eps must be >= 0");
+  if ((st = require_device(nullptr)) != HXM_OK) return st;
+  if (rows == 0) return ok();
+  RowArgs a{x, ldx, y, ldy, gamma, beta, mean_out, rstd_out, rows, cols, eps};
+  return launch_rows<kLayerNorm>(a, dtype, as_stream(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,150 @@
+// Library runtime: status strings, the per-thread reason record, device
+// admission and the per-stream workspace (the library-owned counterpart of
+// the reference's VTCM pool, bin/runtime/include/HexagonCAPI.h:26-57 --
+// allocated once, kept for the process until released).
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "hxm_internal.h"
+
+namespace hxm {
+
+namespace {
+thread_local std::string g_last_error;
+
+struct Workspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+// key: (device << 48) ^ stream pointer
+std::unordered_map<uint64_t, Workspace> g_ws;
+
+std::mutex g_dev_mu;
+std::vector<int8_t> g_dev_ok;  // -1 unknown, 0 not gfx950, 1 ok
+}  // namespace
+
+hxm_status fail(hxm_status st, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return st;
+}
+
+hxm_status ok() {
+  g_last_error.clear();
+  return HXM_OK;
+}
+
+hxm_status check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail(HXM_HIP_ERROR, "hip-error: launch of %s failed: %s", what,
+                hipGetErrorString(e));
+  return ok();
+}
+
+hxm_status require_device(int* device_out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(HXM_NO_DEVICE, "no-device: hipGetDevice failed: %s",
+                hipGetErrorString(e));
+  std::lock_guard<std::mutex> lk(g_dev_mu);
+  if ((int)g_dev_ok.size() <= dev) g_dev_ok.resize(dev + 1, -1);
+  if (g_dev_ok[dev] < 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess)
+      return fail(HXM_NO_DEVICE, "no-device: hipGetDeviceProperties failed");
+    g_dev_ok[dev] = (std::string(prop.gcnArchName).rfind("gfx950", 0) == 0) ? 1 : 0;
+  }
+  if (!g_dev_ok[dev])
+    return fail(HXM_NO_DEVICE, "no-device: device %d is not gfx950", dev);
+  if (device_out) *device_out = dev;
+  return HXM_OK;
+}
+
+hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out) {
+  int dev = 0;
+  HXM_HIP_TRY(hipGetDevice(&dev));
+  const uint64_t key = (static_cast<uint64_t>(dev) << 48) ^
+                       reinterpret_cast<uint64_t>(stream);
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  Workspace& w = g_ws[key];
+  if (w.bytes < bytes) {
+    if (w.ptr) {
+      // The old buffer may still be read by work queued on this stream.
+      HXM_HIP_TRY(hipStreamSynchronize(stream));
+      HXM_HIP_TRY(hipFree(w.ptr));
+      w.ptr = nullptr;
+      w.bytes = 0;
+    }
+    size_t grow = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+    if (hipMalloc(&w.ptr, grow) != hipSuccess) {
+      w.ptr = nullptr;
+      return fail(HXM_OUT_OF_MEMORY, "out-of-memory: workspace of %zu bytes",
+                  grow);
+    }
+    w.bytes = grow;
+  }
+  *out = w.ptr;
+  return HXM_OK;
+}
+
+}  // namespace hxm
+
+extern "C" {
+
+const char* hxm_status_string(int32_t status) {
+  switch (status) {
+    case HXM_OK: return "ok";
+    case HXM_INVALID_ARG: return "invalid-argument";
+    case HXM_UNSUPPORTED_DTYPE: return "unsupported-dtype";
+    case HXM_UNSUPPORTED_SHAPE: return "unsupported-shape";
+    case HXM_HIP_ERROR: return "hip-error";
+    case HXM_OUT_OF_MEMORY: return "out-of-memory";
+    case HXM_NO_DEVICE: return "no-device";
+    default: return "unknown-status";
+  }
+}
+
+const char* hxm_last_error(void) { return hxm::g_last_error.c_str(); }
+
+const char* hxm_version(void) { return "hxm 0.1.0 gfx950"; }
+
+int32_t hxm_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  int count = 0;
+  for (int d = 0; d < n; ++d) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, d) == hipSuccess &&
+        std::string(prop.gcnArchName).rfind("gfx950", 0) == 0)
+      ++count;
+  }
+  return count;
+}
+
+hxm_status hxm_release_cache(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return hxm::ok();
+  std::lock_guard<std::mutex> lk(hxm::g_ws_mu);
+  for (auto it = hxm::g_ws.begin(); it != hxm::g_ws.end();) {
+    if ((it->first >> 48) == static_cast<uint64_t>(dev)) {
+      if (it->second.ptr) {
+        HXM_HIP_TRY(hipDeviceSynchronize());
+        HXM_HIP_TRY(hipFree(it->second.ptr));
+      }
+      it = hxm::g_ws.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  return hxm::ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,121 @@
+"""ctypes binding of libhxm.so (the C ABI declared in include/hxm.h).
+
+The library is built in-tree by ``hexagon-mlir_amd/csrc/Makefile`` into this
+directory.  There is no fallback: if the library is missing, importing
+``hxm`` raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libhxm.so")
+
+HXM_OK = 0
+HXM_INVALID_ARG = 1
+HXM_UNSUPPORTED_DTYPE = 2
+HXM_UNSUPPORTED_SHAPE = 3
+HXM_HIP_ERROR = 4
+HXM_OUT_OF_MEMORY = 5
+HXM_NO_DEVICE = 6
+
+F16, BF16, F32, I8, I32 = 1, 2, 3, 4, 5
+B_KN, B_NK = 0, 1
+
+
+class HxmError(RuntimeError):
+    """A non-OK hxm_status, carrying the library's reason string."""
+
+    def __init__(self, status: int, reason: str, fn: str):
+        self.status = status
+        self.reason = reason
+        super().__init__(f"{fn}: {status_string(status)} ({reason})")
+
+
+class GemmConfig(ctypes.Structure):
+    _fields_ = [("bm", ctypes.c_int32), ("bn", ctypes.c_int32), ("bk", ctypes.c_int32),
+                ("waves_m", ctypes.c_int32), ("waves_n", ctypes.c_int32),
+                ("split_k", ctypes.c_int32)]
+
+    def as_tuple(self):
+        return (self.bm, self.bn, self.bk, self.waves_m, self.waves_n, self.split_k)
+
+    def __repr__(self):
+        return "GemmConfig(bm=%d, bn=%d, bk=%d, waves=%dx%d, split_k=%d)" % self.as_tuple()
+
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+_f64 = ctypes.c_double
+_st = ctypes.c_int  # hxm_status
+_cfgp = ctypes.POINTER(GemmConfig)
+
+# name -> (restype, argtypes); the exact list of include/hxm.h.
+SIGNATURES = {
+    "hxm_status_string": (ctypes.c_char_p, [_i32]),
+    "hxm_last_error": (ctypes.c_char_p, []),
+    "hxm_version": (ctypes.c_char_p, []),
+    "hxm_device_count": (_i32, []),
+    "hxm_release_cache": (_st, []),
+    "hxm_query_contraction": (_st, [_i64, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(_i32)]),
+    "hxm_matmul": (_st, [_p, _i64, _p, _i64, _i32, _p, _i64, _i64, _i64, _i64, _i32, _i32,
+                         _i32, _cfgp, _p]),
+    "hxm_gemm_i8": (_st, [_p, _i64, _p, _i64, _i32, _p, _i64, _i64, _i64, _i64, _i32, _cfgp, _p]),
+    "hxm_gemm_i8_dequant": (_st, [_p, _i64, _p, _i64, _i32, _p, _p, _p, _i64, _i64, _i64,
+                                  _i64, _cfgp, _p]),
+    "hxm_prepack_weight": (_st, [_p, _i64, _p, _i64, _i64, _i64, _i32, _p]),
+    "hxm_gemv_w8a16": (_st, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p]),
+    "hxm_softmax_rows": (_st, [_p, _i64, _p, _i64, _i64, _i64, _i32, _p]),
+    "hxm_rmsnorm_rows": (_st, [_p, _i64, _p, _p, _i64, _i64, _i64, _f32, _i32, _p]),
+    "hxm_layernorm_rows": (_st, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i64, _i64, _f32, _i32,
+                                 _p]),
+    "hxm_reason_string": (ctypes.c_char_p, [_i32]),
+    "hxm_tile_ladder": (_i32, [_i64, ctypes.POINTER(_i64), _i32]),
+    "hxm_hmx_tile_verdict": (_i32, [_i64, _i64, _i64, _i64]),
+    "hxm_gpu_tile_verdict": (_i32, [_cfgp, _i32, _i64]),
+    "hxm_gemm_configs": (_i32, [_i32, _cfgp, _i32]),
+    "hxm_champion_gate": (_f64, [_f64]),
+    "hxm_quantile_spread_cv": (_f64, [_f64, _f64, _f64]),
+    "hxm_quantile": (_f64, [ctypes.POINTER(_f64), _i32, _f64]),
+    "hxm_calibration_iters": (_i32, [_f64, _f64, _i32, _i32]),
+    "hxm_champion_walk": (_i32, [ctypes.POINTER(_f64), ctypes.POINTER(_f64),
+                                 ctypes.POINTER(_f64), _i32, _i32, ctypes.POINTER(_i32),
+                                 ctypes.POINTER(_f64), ctypes.POINTER(_f64)]),
+    "hxm_canary_status": (_i32, [_i32, _f64, _f64, _f64, _f64, ctypes.POINTER(_f64),
+                                 ctypes.POINTER(_f64)]),
+    "hxm_tune_gemm": (_st, [_i32, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _cfgp,
+                            ctypes.c_char_p, _i64, _p]),
+    "hxm_tune_cache_clear": (None, []),
+}
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"libhxm.so not found at {LIB_PATH}: build it first "
+            "(python -c 'import __graft_entry__ as g; g.build()' or make -C "
+            "hexagon-mlir_amd/csrc)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def status_string(st: int) -> str:
+    return lib.hxm_status_string(int(st)).decode()
+
+
+def last_error() -> str:
+    return lib.hxm_last_error().decode()
+
+
+def check(st: int, fn: str) -> None:
+    if st != HXM_OK:
+        raise HxmError(st, last_error(), fn)

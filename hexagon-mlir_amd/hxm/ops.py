@@ -1,0 +1,246 @@
+"""Torch-facing host mirror of the reference's operator surface for this path.
+
+The reference launches Triton kernels whose meaning is ``linalg.matmul`` /
+row reductions and checks them against torch (``torch.matmul``,
+``F.softmax``, ``F.rms_norm``, ``F.layer_norm``: test/python/triton/
+test_matmul.py:86-88, test_softmax.py:91, test_rms_norm.py:84,
+test_layer_norm.py).  These functions keep those names and argument meanings
+and run the gfx950 kernels through the C ABI.  Tensors must already live on
+the GPU; a CPU tensor is an error, never a silent fallback.
+"""
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import torch
+
+from ._lib import (B_KN, B_NK, BF16, F16, F32, I8, I32, GemmConfig, check, lib)
+
+_DT = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32,
+       torch.int8: I8, torch.int32: I32}
+
+
+def _code(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}") from None
+
+
+def _stream(stream=None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _mat(t: torch.Tensor, name: str) -> torch.Tensor:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (got {t.device})")
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D (got {tuple(t.shape)})")
+    if t.stride(1) != 1:
+        raise ValueError(f"{name} must have a contiguous last dimension")
+    return t
+
+
+def _ld(t: torch.Tensor) -> int:
+    return t.stride(0) if t.shape[0] > 1 else max(t.shape[1], t.stride(0))
+
+
+def _cfg(config) -> Optional[GemmConfig]:
+    if config is None:
+        return None
+    if isinstance(config, GemmConfig):
+        return config
+    return GemmConfig(*config)
+
+
+def _ptr_or_none(cfg):
+    import ctypes
+    return None if cfg is None else ctypes.byref(cfg)
+
+
+def matmul(A: torch.Tensor, B: torch.Tensor, out: Optional[torch.Tensor] = None, *,
+           b_layout: str = "kn", accumulate: bool = False,
+           out_dtype: Optional[torch.dtype] = None, config=None, stream=None) -> torch.Tensor:
+    """C = [C +] A @ B on f16/bf16 with fp32 accumulation (linalg.matmul).
+
+    ``b_layout="kn"``: B is [K, N] (packed per call); ``"nk"``: B is the
+    resident [N, K] image from :func:`prepack_weight`."""
+    _mat(A, "A"), _mat(B, "B")
+    M, K = A.shape
+    N = B.shape[1] if b_layout == "kn" else B.shape[0]
+    if (B.shape[0] if b_layout == "kn" else B.shape[1]) != K:
+        raise ValueError(f"shape mismatch A{tuple(A.shape)} B{tuple(B.shape)} ({b_layout})")
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate=True needs out")
+        out = torch.empty((M, N), dtype=out_dtype or A.dtype, device=A.device)
+    _mat(out, "out")
+    cfg = _cfg(config)
+    st = lib.hxm_matmul(A.data_ptr(), _ld(A), B.data_ptr(), _ld(B),
+                        B_KN if b_layout == "kn" else B_NK, out.data_ptr(), _ld(out),
+                        M, N, K, _code(A), _code(out), int(accumulate), _ptr_or_none(cfg),
+                        _stream(stream))
+    check(st, "hxm_matmul")
+    return out
+
+
+def gemm_i8(A: torch.Tensor, B: torch.Tensor, out: Optional[torch.Tensor] = None, *,
+            b_layout: str = "kn", accumulate: bool = False, config=None,
+            stream=None) -> torch.Tensor:
+    """int32 C = [C +] A @ B, exact (the reference's int8 linalg.matmul)."""
+    _mat(A, "A"), _mat(B, "B")
+    M, K = A.shape
+    N = B.shape[1] if b_layout == "kn" else B.shape[0]
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate=True needs out")
+        out = torch.empty((M, N), dtype=torch.int32, device=A.device)
+    _mat(out, "out")
+    cfg = _cfg(config)
+    st = lib.hxm_gemm_i8(A.data_ptr(), _ld(A), B.data_ptr(), _ld(B),
+                         B_KN if b_layout == "kn" else B_NK, out.data_ptr(), _ld(out),
+                         M, N, K, int(accumulate), _ptr_or_none(cfg), _stream(stream))
+    check(st, "hxm_gemm_i8")
+    return out
+
+
+def gemm_i8_dequant(A: torch.Tensor, B: torch.Tensor, row_scale: torch.Tensor,
+                    col_scale: torch.Tensor, out: Optional[torch.Tensor] = None, *,
+                    b_layout: str = "kn", config=None, stream=None) -> torch.Tensor:
+    """f16 C = f16(((float)(A @ B) * row_scale[:,None]) * col_scale[None,:])."""
+    _mat(A, "A"), _mat(B, "B")
+    M, K = A.shape
+    N = B.shape[1] if b_layout == "kn" else B.shape[0]
+    if row_scale.dtype != torch.float32 or col_scale.dtype != torch.float32:
+        raise TypeError("scales must be float32")
+    if row_scale.numel() != M or col_scale.numel() != N:
+        raise ValueError("scale lengths must be M and N")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=A.device)
+    _mat(out, "out")
+    cfg = _cfg(config)
+    st = lib.hxm_gemm_i8_dequant(A.data_ptr(), _ld(A), B.data_ptr(), _ld(B),
+                                 B_KN if b_layout == "kn" else B_NK,
+                                 row_scale.contiguous().data_ptr(),
+                                 col_scale.contiguous().data_ptr(), out.data_ptr(), _ld(out),
+                                 M, N, K, _ptr_or_none(cfg), _stream(stream))
+    check(st, "hxm_gemm_i8_dequant")
+    return out
+
+
+def prepack_weight(B: torch.Tensor, out: Optional[torch.Tensor] = None, *,
+                   stream=None) -> torch.Tensor:
+    """[K, N] -> resident [N, K] image (hmx_weight_prepack's role)."""
+    _mat(B, "B")
+    K, N = B.shape
+    if out is None:
+        out = torch.empty((N, K), dtype=B.dtype, device=B.device)
+    _mat(out, "out")
+    st = lib.hxm_prepack_weight(B.data_ptr(), _ld(B), out.data_ptr(), _ld(out), K, N,
+                                _code(B), _stream(stream))
+    check(st, "hxm_prepack_weight")
+    return out
+
+
+def gemv_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor,
+               out: Optional[torch.Tensor] = None, *, stream=None) -> torch.Tensor:
+    """y = f16((x @ W.T in fp32) * scale) for int8 W [N, K], f16 x [M, K]."""
+    _mat(x, "x"), _mat(W, "W")
+    M, K = x.shape
+    N = W.shape[0]
+    if W.shape[1] != K:
+        raise ValueError("W must be [N, K]")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    _mat(out, "out")
+    st = lib.hxm_gemv_w8a16(x.data_ptr(), _ld(x), W.data_ptr(), _ld(W),
+                            scale.contiguous().data_ptr(), out.data_ptr(), _ld(out), M, N, K,
+                            _stream(stream))
+    check(st, "hxm_gemv_w8a16")
+    return out
+
+
+def _rows(x: torch.Tensor):
+    if not x.is_cuda:
+        raise ValueError(f"x must be a GPU tensor (got {x.device})")
+    if x.stride(-1) != 1:
+        raise ValueError("x must have a contiguous last dimension")
+    cols = x.shape[-1]
+    x2 = x.reshape(-1, cols)
+    return x2, x2.shape[0], cols
+
+
+def softmax(x: torch.Tensor, dim: int = -1, out: Optional[torch.Tensor] = None, *,
+            stream=None) -> torch.Tensor:
+    """Row softmax over the last dimension (F.softmax(x, dim=-1))."""
+    if dim not in (-1, x.dim() - 1):
+        raise ValueError("only the last dimension is supported")
+    x2, rows, cols = _rows(x)
+    if out is None:
+        out = torch.empty_like(x)
+    o2 = out.reshape(-1, cols)
+    st = lib.hxm_softmax_rows(x2.data_ptr(), _ld(x2), o2.data_ptr(), _ld(o2), rows, cols,
+                              _code(x), _stream(stream))
+    check(st, "hxm_softmax_rows")
+    return out
+
+
+def rms_norm(x: torch.Tensor, normalized_shape: Sequence[int],
+             weight: Optional[torch.Tensor] = None, eps: Optional[float] = None,
+             out: Optional[torch.Tensor] = None, *, stream=None) -> torch.Tensor:
+    """F.rms_norm over the last dimension."""
+    x2, rows, cols = _rows(x)
+    if tuple(normalized_shape) != (cols,):
+        raise ValueError("normalized_shape must be (x.shape[-1],)")
+    if eps is None:
+        eps = torch.finfo(x.dtype).eps
+    if out is None:
+        out = torch.empty_like(x)
+    o2 = out.reshape(-1, cols)
+    g = 0 if weight is None else weight.contiguous().data_ptr()
+    st = lib.hxm_rmsnorm_rows(x2.data_ptr(), _ld(x2), g or None, o2.data_ptr(), _ld(o2),
+                              rows, cols, float(eps), _code(x), _stream(stream))
+    check(st, "hxm_rmsnorm_rows")
+    return out
+
+
+def layer_norm(x: torch.Tensor, normalized_shape: Sequence[int],
+               weight: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
+               eps: float = 1e-5, out: Optional[torch.Tensor] = None, *,
+               return_stats: bool = False, stream=None):
+    """F.layer_norm over the last dimension; optionally returns (y, mean, rstd)."""
+    x2, rows, cols = _rows(x)
+    if tuple(normalized_shape) != (cols,):
+        raise ValueError("normalized_shape must be (x.shape[-1],)")
+    if out is None:
+        out = torch.empty_like(x)
+    o2 = out.reshape(-1, cols)
+    mean = rstd = None
+    if return_stats:
+        mean = torch.empty(rows, dtype=torch.float32, device=x.device)
+        rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
+    st = lib.hxm_layernorm_rows(
+        x2.data_ptr(), _ld(x2), None if weight is None else weight.contiguous().data_ptr(),
+        None if bias is None else bias.contiguous().data_ptr(), o2.data_ptr(), _ld(o2),
+        None if mean is None else mean.data_ptr(), None if rstd is None else rstd.data_ptr(),
+        rows, cols, float(eps), _code(x), _stream(stream))
+    check(st, "hxm_layernorm_rows")
+    return (out, mean, rstd) if return_stats else out
+
+
+def tune_gemm(A: torch.Tensor, B_nk: torch.Tensor, out: torch.Tensor, *, reps: int = 5,
+              stream=None):
+    """Measured tile search on these operands; returns (GemmConfig, report dict)."""
+    import ctypes
+    import json
+    _mat(A, "A"), _mat(B_nk, "B"), _mat(out, "out")
+    M, K = A.shape
+    N = B_nk.shape[0]
+    best = GemmConfig()
+    buf = ctypes.create_string_buffer(1 << 16)
+    st = lib.hxm_tune_gemm(_code(A), A.data_ptr(), _ld(A), B_nk.data_ptr(), _ld(B_nk),
+                           out.data_ptr(), _ld(out), M, N, K, reps, ctypes.byref(best), buf,
+                           len(buf), _stream(stream))
+    check(st, "hxm_tune_gemm")
+    return best, json.loads(buf.value.decode())

@@ -1,0 +1,296 @@
+/*
+ * hxm.h - C ABI of the MI355X (gfx950) hot path: MFMA matmuls with resident
+ * (pre-packed) weights, W8A16 skinny GEMM/GEMV, single-pass row reductions
+ * (softmax / RMSNorm / LayerNorm) and the measured tile search.
+ *
+ * Boundary rules (every entry point):
+ *   - plain pointers, sizes and leading dimensions (in ELEMENTS); no torch or
+ *     HIP types.  `stream` is a hipStream_t passed as void* (NULL = default
+ *     stream).  Every compute call is asynchronous and stream-ordered.
+ *   - the caller owns every tensor; the library never frees caller memory.
+ *   - arguments are validated on the host BEFORE any launch.  A refusal
+ *     returns a status and leaves a reason string (hxm_last_error) whose
+ *     vocabulary follows the reference's manifest reasons
+ *     (qcom_hexagon_backend/include/hexagon/Dialect/Hmx/Transforms/
+ *      HmxManifest.h:81-100): "unsupported-dtype", "min-rows",
+ *     "tile-alignment", "lds-budget" (the VTCM budget's counterpart), plus
+ *     "invalid-argument".  There is no silent fallback: a refused call
+ *     computes nothing.
+ *   - numerics: fp16/bf16 products accumulate in fp32 and are rounded once
+ *     to the output dtype; int8 products accumulate exactly in int32.
+ *
+ * Reference interfaces replaced (paths relative to the reference root):
+ *   the compiled Triton kernel symbol launched by
+ *   qcom_hexagon_backend/backend/driver.py:150-237 with the memref-descriptor
+ *   ABI of qcom_hexagon_backend/backend/hexagon_launcher_base.py:60-75 and
+ *   test/utils/dsp/include/common.h:15-30 (sizes + strides -> here sizes +
+ *   leading dimensions), and below it the HMX leaves of
+ *   qcom_hexagon_backend/bin/runtime/hmx/include/HMXAPI.h:53-293.
+ */
+#ifndef HXM_H
+#define HXM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum hxm_status {
+  HXM_OK = 0,
+  HXM_INVALID_ARG = 1,       /* null pointer, negative size, bad ld, bad enum */
+  HXM_UNSUPPORTED_DTYPE = 2, /* reason "unsupported-dtype" */
+  HXM_UNSUPPORTED_SHAPE = 3, /* reason "tile-alignment" / "min-rows" / "lds-budget" */
+  HXM_HIP_ERROR = 4,         /* a HIP runtime call failed; reason has hipGetErrorString */
+  HXM_OUT_OF_MEMORY = 5,     /* library-owned workspace could not grow */
+  HXM_NO_DEVICE = 6          /* no gfx950 device visible */
+} hxm_status;
+
+typedef enum hxm_dtype {
+  HXM_F16 = 1,
+  HXM_BF16 = 2,
+  HXM_F32 = 3,
+  HXM_I8 = 4,
+  HXM_I32 = 5
+} hxm_dtype;
+
+/* Layout of the B (weight) operand of a matmul.
+ *   HXM_B_KN: B is [K,N] row-major with leading dimension ldb >= N -- the
+ *             plain linalg.matmul operand.  The library packs it per call
+ *             into a library-owned workspace (the reference's per-launch
+ *             hmx.pack_weight, HmxOps.td:229).
+ *   HXM_B_NK: B is already packed, [N,K] row-major (K contiguous), ldb >= K --
+ *             the resident image produced once by hxm_prepack_weight (the
+ *             reference's weight-resident path, WeightResidentPass.cpp:10-53,
+ *             backend/hmx_weight_prepack.py:171-183). */
+typedef enum hxm_b_layout { HXM_B_KN = 0, HXM_B_NK = 1 } hxm_b_layout;
+
+/* One GEMM kernel configuration: the tile search's variables
+ * (backend/hmx_search.py:295-312 searches BM,BN,BK; the GPU adds the wave
+ * grid and the K-split).  A zeroed struct means "library default for the
+ * shape" (the tuned winner when one is cached). */
+typedef struct hxm_gemm_config {
+  int32_t bm, bn, bk;    /* workgroup tile, bk in elements */
+  int32_t waves_m, waves_n; /* wave grid inside the workgroup */
+  int32_t split_k;       /* workgroups along K (1 = none) */
+} hxm_gemm_config;
+
+/* ---- status / library ------------------------------------------------- */
+
+/* Human-readable name of a status code. */
+const char* hxm_status_string(int32_t status);
+
+/* Reason string of the last non-OK status returned on this host thread
+ * ("" after success).  Mirrors the manifest's plan/reason record
+ * (HmxManifest.h:81-110). */
+const char* hxm_last_error(void);
+
+/* Library version string. */
+const char* hxm_version(void);
+
+/* Number of gfx950 devices visible (0 when none); touches the HIP runtime. */
+int32_t hxm_device_count(void);
+
+/* Frees every library-owned buffer (per-stream pack workspaces) on the
+ * current device.  Replaces the process-lifetime VTCM release of
+ * bin/runtime/include/HexagonCAPI.h:38-57. */
+hxm_status hxm_release_cache(void);
+
+/* ---- admission (HmxTarget::queryContraction, HmxTarget.h:195-218) ----- */
+
+/* Plans a matmul without launching.  plan_out receives 0 = "mfma-full"
+ * (every extent a multiple of the 32-wide MFMA edge), 1 = "mfma-tail"
+ * (handled with masked edge tiles), -1 = refused (status says why).
+ * Unlike the reference's engine the GPU path admits int8 and tails. */
+hxm_status hxm_query_contraction(int64_t M, int64_t N, int64_t K,
+                                 int32_t a_dtype, int32_t b_dtype,
+                                 int32_t c_dtype, int32_t* plan_out);
+
+/* ---- matmuls ------------------------------------------------------------ */
+
+/* linalg.matmul on f16/bf16 (reference: the hmx.matmul contract,
+ * HmxOps.td:47, MatmulToHmxPass.cpp:101-121 for the init semantics; leaves
+ * hmx_mma_f16 / hmx_acc_store_f16, HMXAPI.c:36-55).
+ *   C[M,N] = (accumulate ? C : 0) + A[M,K] . B
+ * A row-major (lda >= K), dtype ab_dtype in {F16, BF16}; B of the same
+ * dtype in layout b_layout; C row-major (ldc >= N), c_dtype in
+ * {F16, BF16, F32}.  Products accumulate in fp32 (with the prior C added
+ * in fp32 when accumulate != 0) and round once to c_dtype.
+ * K*sizeof(elem) must be a multiple of 16 bytes, lda/ldb likewise, and
+ * A/B 16-byte aligned ("tile-alignment" otherwise); M and N are free. */
+hxm_status hxm_matmul(const void* A, int64_t lda, const void* B, int64_t ldb,
+                      int32_t b_layout, void* C, int64_t ldc, int64_t M,
+                      int64_t N, int64_t K, int32_t ab_dtype, int32_t c_dtype,
+                      int32_t accumulate, const hxm_gemm_config* cfg,
+                      void* stream);
+
+/* int8 linalg.matmul with exact int32 accumulation (the reference refuses
+ * int8 on the engine, HmxTarget.h:198-200, and lowers it on the HVX
+ * generic path, LinalgToLLVMPass.cpp:364-365; its result is the exact
+ * integer product).  C_i32[M,N] = (accumulate ? C : 0) + A . B, wrapping
+ * int32 addition.  K, lda, ldb multiples of 16; A, B 16-byte aligned. */
+hxm_status hxm_gemm_i8(const int8_t* A, int64_t lda, const int8_t* B,
+                       int64_t ldb, int32_t b_layout, int32_t* C, int64_t ldc,
+                       int64_t M, int64_t N, int64_t K, int32_t accumulate,
+                       const hxm_gemm_config* cfg, void* stream);
+
+/* int8 GEMM with the fused dequant epilogue (the GPU counterpart of the
+ * fused read-out convert, HMXAPI.c:36-44, with per-channel scales):
+ *   C_f16[i,j] = rne_f16( ((float)acc_i32[i,j] * row_scale[i]) * col_scale[j] )
+ * evaluated in fp32 exactly in that order (two roundings, no FMA), so the
+ * result is bit-exact against any implementation of the same spelling.
+ * row_scale: fp32 [M]; col_scale: fp32 [N]. */
+hxm_status hxm_gemm_i8_dequant(const int8_t* A, int64_t lda, const int8_t* B,
+                               int64_t ldb, int32_t b_layout,
+                               const float* row_scale, const float* col_scale,
+                               void* C_f16, int64_t ldc, int64_t M, int64_t N,
+                               int64_t K, const hxm_gemm_config* cfg,
+                               void* stream);
+
+/* Weight pre-pack: the host half of weight residency
+ * (backend/hmx_weight_prepack.py:171-212, WeightPrepack._permute) done on
+ * the device.  Transposes B [K,N] (ldb >= N) into the resident image
+ * out [N,K] (ldo >= K), K contiguous -- the operand order every MFMA kernel
+ * here reads.  dtype in {I8, F16, BF16}.  Run once per weight; matmuls then
+ * take b_layout = HXM_B_NK. */
+hxm_status hxm_prepack_weight(const void* B, int64_t ldb, void* out,
+                              int64_t ldo, int64_t K, int64_t N, int32_t dtype,
+                              void* stream);
+
+/* W8A16 weight-resident skinny GEMM / GEMV (the
+ * reference's int8 matmul on the HVX path, ScheduleMatmulForHVXPass.cpp:44-80):
+ *   y[m,n] = rne_f16( (sum_k f32(x[m,k]) * f32(W[n,k])) * f32(w_scale[n]) )
+ * x fp16 [M,K] (ldx >= K); W int8 [N,K] (ldw >= K, output-channel major);
+ * w_scale fp16 [N]; y fp16 [M,N] (ldy >= N).  fp32 accumulation in any
+ * order (tolerance rtol 1e-2 / atol 1e-3 against the fp32 restatement).
+ * Any M >= 1: M <= 16 streams W once through the GEMV kernel, larger M
+ * runs the W8A16 MFMA GEMM.  K, ldx, ldw multiples of 16. */
+hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W,
+                          int64_t ldw, const void* w_scale, void* y,
+                          int64_t ldy, int64_t M, int64_t N, int64_t K,
+                          void* stream);
+
+/* ---- row reductions (test/python/triton/test_softmax.py:41-69,
+ *      test_rms_norm.py:34-60, test_layer_norm.py:39-79, as lowered by
+ *      VectorRowReducePass.cpp:10-31 / SplitReduceGenericPass.cpp:62-93) -- */
+
+/* y[r,:] = exp(x[r,:] - max_r) / sum(exp(x[r,:] - max_r)), computed in fp32
+ * (max-subtract, fp32 sum), rounded once to dtype.  dtype in {F16, BF16,
+ * F32}; x and y may alias.  cols >= 1. */
+hxm_status hxm_softmax_rows(const void* x, int64_t ldx, void* y, int64_t ldy,
+                            int64_t rows, int64_t cols, int32_t dtype,
+                            void* stream);
+
+/* y[r,c] = x[r,c] * rsqrt(mean_c(x[r,:]^2) + eps) * gamma[c], fp32 inside,
+ * one rounding to dtype.  gamma (same dtype, [cols]) may be NULL (= 1). */
+hxm_status hxm_rmsnorm_rows(const void* x, int64_t ldx, const void* gamma,
+                            void* y, int64_t ldy, int64_t rows, int64_t cols,
+                            float eps, int32_t dtype, void* stream);
+
+/* y = (x - mean) * rstd * gamma + beta with rstd = 1/sqrt(var + eps)
+ * (biased variance), fp32 inside.  gamma/beta may be NULL (1 / 0).
+ * mean_out / rstd_out: fp32 [rows] or NULL (the reference kernel writes
+ * them for the backward pass, test_layer_norm.py:67-69). */
+hxm_status hxm_layernorm_rows(const void* x, int64_t ldx, const void* gamma,
+                              const void* beta, void* y, int64_t ldy,
+                              float* mean_out, float* rstd_out, int64_t rows,
+                              int64_t cols, float eps, int32_t dtype,
+                              void* stream);
+
+/* ---- tile search (backend/hmx_search.py) -------------------------------- */
+
+/* Reason codes shared by the two verdict functions below. */
+enum {
+  HXM_REASON_OK = 0,
+  HXM_REASON_FRONTEND_BLOCK_LIMIT = 1,
+  HXM_REASON_MIN_ROWS = 2,
+  HXM_REASON_TILE_ALIGNMENT = 3,
+  HXM_REASON_VTCM_BUDGET = 4,
+  HXM_REASON_LDS_BUDGET = 5,
+  HXM_REASON_UNSUPPORTED_DTYPE = 6,
+  HXM_REASON_NO_KERNEL = 7
+};
+
+/* Reason code -> the reference's vocabulary string ("ok", "min-rows", ...). */
+const char* hxm_reason_string(int32_t reason);
+
+/* hmx_search.tile_ladder (hmx_search.py:246-266): powers of two from 32 to
+ * next_pow2(extent), plus extent itself when it is a power of two, sorted.
+ * Writes up to cap values; returns the full count. */
+int32_t hxm_tile_ladder(int64_t extent, int64_t* out, int32_t cap);
+
+/* hmx_search.tile_verdict (hmx_search.py:269-292), the reference's engine
+ * legality predicate restated exactly (VTCM budget in bytes). */
+int32_t hxm_hmx_tile_verdict(int64_t bm, int64_t bn, int64_t bk,
+                             int64_t vtcm_budget);
+
+/* The same lattice on gfx950: frontend limit -> min-rows -> the 32-wide MFMA
+ * edge -> LDS budget (2 stages x (bm+bn) x bk x elem_bytes <= lds_budget)
+ * -> a compiled kernel exists for (cfg, dtype).  elem_bytes 1 (int8) or 2. */
+int32_t hxm_gpu_tile_verdict(const hxm_gemm_config* cfg, int32_t ab_dtype,
+                             int64_t lds_budget);
+
+/* Every compiled GEMM configuration for ab_dtype (I8, F16 or BF16).
+ * Writes up to cap entries; returns the full count. */
+int32_t hxm_gemm_configs(int32_t ab_dtype, hxm_gemm_config* out, int32_t cap);
+
+/* hmx_search.champion_gate (hmx_search.py:1280-1289): max(3*|cv|, 0.15). */
+double hxm_champion_gate(double cv);
+
+/* hmx_search.quantile_spread_cv (hmx_search.py:1254-1277). */
+double hxm_quantile_spread_cv(double q20, double q50, double q80);
+
+/* hmx_search._quantile (hmx_search.py:1095-1106): linear interpolation. */
+double hxm_quantile(const double* samples, int32_t n, double q);
+
+/* hmx_search.calibration_iters (hmx_search.py:1159-1171). */
+int32_t hxm_calibration_iters(double perf_us, double target_us, int32_t lo,
+                              int32_t hi);
+
+/* The gated walk of hmx_search.judge_champion_round (hmx_search.py:1460-1478).
+ * Rows are given in enumeration order with their q20/q50/q80; `start` is the
+ * incumbent's index (the control arm, else the first measured row); rows
+ * whose q50 is not finite are skipped.  A challenger takes the crown only when
+ * (q50_inc - q50_ch)/q50_inc > max(3*max(cv_ch, cv_inc), 15%) (strict: a tie
+ * keeps the incumbent).  outcome[i] (may be NULL): -1 not compared, 0 kept,
+ * 1 takeover; delta_out/gate_out (may be NULL) receive the fractions.
+ * Returns the champion's index, -1 when start is not a measured row. */
+int32_t hxm_champion_walk(const double* q20, const double* q50,
+                          const double* q80, int32_t n, int32_t start,
+                          int32_t* outcome, double* delta_out,
+                          double* gate_out);
+
+/* hmx_search.canary_verdict's status (hmx_search.py:1292-1367):
+ * 0 "ok", 1 "missing" (present == 0), 2 "unmeasured" (q50 not finite),
+ * 3 "drift" (|q50/ref - 1| > champion_gate(cv)), 4 "reference-established"
+ * (no finite positive reference).  delta_out/gate_out may be NULL. */
+int32_t hxm_canary_status(int32_t present, double q20, double q50, double q80,
+                          double reference_q50, double* delta_out,
+                          double* gate_out);
+
+/* Measured tile search for one GEMM shape on the caller's operands (the
+ * reference's autotune sweep + hexagon_bench + judge_champion_round,
+ * hmx_search.py:1109-1156,1370-1571).  op: HXM_I8 (int8 -> i32, B in
+ * layout NK) or HXM_F16 / HXM_BF16 (-> f16, B in layout NK).  Every legal
+ * compiled config is launched `reps` times after one discarded warm call;
+ * its output is checked bit-exact against the control config's (a config
+ * that differs scores inf); the champion is the deterministic gated walk
+ * from the control config with gate max(3*CV, 15%), preceded by the
+ * 32x32x32 canary.  The winner is cached for (op, M, N, K) and used by
+ * later calls with cfg == NULL.  report (JSON, may be NULL) receives the
+ * per-config quantiles and the verdict.  C is overwritten. */
+hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
+                         int64_t ldb, void* C, int64_t ldc, int64_t M,
+                         int64_t N, int64_t K, int32_t reps,
+                         hxm_gemm_config* best, char* report,
+                         int64_t report_cap, void* stream);
+
+/* Forget every cached tuning winner. */
+void hxm_tune_cache_clear(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HXM_H */

@@ -1,0 +1,106 @@
+"""The C ABI boundary on the CPU: libhxm.so loads, exports every symbol that
+include/hxm.h declares, and refuses bad arguments on the host before any
+launch -- with the manifest-style reason vocabulary -- without a GPU."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import hxm
+from hxm import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hxm.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hxm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_symbols() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", hxm.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (hxm_\w+)", out))
+    missing = [s for s in declared_symbols() if s not in exported]
+    assert not missing, missing
+    for s in declared_symbols():
+        assert getattr(hxm.lib, s) is not None
+
+
+def test_status_strings_and_version():
+    assert hxm.status_string(0) == "ok"
+    assert hxm.status_string(3) == "unsupported-shape"
+    assert hxm.version().startswith("hxm ")
+
+
+def _gpu_present():
+    import torch
+    return torch.cuda.is_available()
+
+
+def test_refusals_happen_before_launch():
+    L = hxm.lib
+    # int8 GEMM with K not a multiple of 16 bytes -> tile-alignment
+    st = L.hxm_gemm_i8(16, 24, 16, 24, hxm.B_NK, 16, 8, 8, 8, 24, 0, None, None)
+    assert st == _lib.HXM_UNSUPPORTED_SHAPE
+    assert hxm.last_error().startswith("tile-alignment")
+    # negative extent -> invalid argument
+    st = L.hxm_gemm_i8(16, 32, 16, 32, hxm.B_NK, 16, 8, -1, 8, 32, 0, None, None)
+    assert st == _lib.HXM_INVALID_ARG
+    # fp32 operands are not an MFMA matmul dtype -> unsupported-dtype
+    st = L.hxm_matmul(16, 32, 16, 32, hxm.B_KN, 16, 32, 4, 4, 32, hxm.F32, hxm.F32, 0, None,
+                      None)
+    assert st == _lib.HXM_UNSUPPORTED_DTYPE
+    assert hxm.last_error().startswith("unsupported-dtype")
+    # leading dimension smaller than the row
+    st = L.hxm_softmax_rows(16, 4, 16, 8, 2, 8, hxm.F16, None)
+    assert st == _lib.HXM_INVALID_ARG
+    # int8 softmax is refused
+    st = L.hxm_softmax_rows(16, 8, 16, 8, 2, 8, hxm.I8, None)
+    assert st == _lib.HXM_UNSUPPORTED_DTYPE
+    # gemv: K not a multiple of 16
+    st = L.hxm_gemv_w8a16(16, 24, 16, 24, 16, 16, 8, 1, 8, 24, None)
+    assert st == _lib.HXM_UNSUPPORTED_SHAPE
+    # an unknown B layout
+    st = L.hxm_gemm_i8(16, 32, 16, 32, 7, 16, 8, 8, 8, 32, 0, None, None)
+    assert st == _lib.HXM_INVALID_ARG
+
+
+@pytest.mark.skipif("_gpu_present()")
+def test_valid_call_without_gpu_reports_no_device():
+    st = hxm.lib.hxm_softmax_rows(16, 8, 16, 8, 2, 8, hxm.F16, None)
+    assert st == _lib.HXM_NO_DEVICE
+    assert hxm.last_error().startswith("no-device")
+
+
+def test_query_contraction_plans():
+    plan = ctypes.c_int32()
+    L = hxm.lib
+    assert L.hxm_query_contraction(256, 256, 256, hxm.F16, hxm.F16, hxm.F16,
+                                   ctypes.byref(plan)) == 0 and plan.value == 0
+    assert L.hxm_query_contraction(4096, 11000, 4096, hxm.I8, hxm.I8, hxm.I32,
+                                   ctypes.byref(plan)) == 0 and plan.value == 1
+    # int8 K not 16-byte aligned
+    assert L.hxm_query_contraction(64, 64, 40, hxm.I8, hxm.I8, hxm.I32,
+                                   ctypes.byref(plan)) == _lib.HXM_UNSUPPORTED_SHAPE
+    assert plan.value == -1
+    assert L.hxm_query_contraction(64, 64, 64, hxm.F32, hxm.F32, hxm.F32,
+                                   ctypes.byref(plan)) == _lib.HXM_UNSUPPORTED_DTYPE
+
+
+def test_product_has_no_oracle_dependency():
+    """The product path never routes through the CPU oracle."""
+    pkg = os.path.join(ROOT, "hexagon-mlir_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")) or f == "Makefile":
+                text = open(os.path.join(dirpath, f), errors="ignore").read()
+                assert "oracle" not in text.lower().replace("oracle/oracle", ""), f

@@ -1,0 +1,169 @@
+"""GPU parity of the MFMA GEMMs against the CPU oracle.
+
+int8 -> int32 and the dequant epilogue are bit-exact; f16/bf16 matmuls are
+within rtol 1e-2 / atol 1e-3 (fp32 accumulate), the tolerance the target
+states, plus a small-integer case that must be bit-exact.  At the full
+4096^3 size the oracle runs on a row sample, and every element is covered
+by exact int64 row- and column-checksums (sum_m C = (1^T A) B and
+sum_n C = A (B 1), which a dropped tile, a transposed block or a wrong
+offset all break)."""
+import numpy as np
+import pytest
+import torch
+
+import hxm
+import hxm.ops as ops
+import hxm.search as S
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def rand_i8(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
+
+
+SHAPES = [(1, 1, 16), (67, 45, 96), (33, 130, 272), (128, 128, 256), (256, 256, 1024),
+          (300, 260, 384), (1000, 520, 272), (5, 4096, 128)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_gemm_i8_bit_exact(dev, M, N, K, layout):
+    print(f"gemm_i8 M={M} N={N} K={K} layout={layout}", flush=True)
+    A = rand_i8((M, K), 1)
+    B = rand_i8((K, N), 2)
+    Bd = B.to(dev) if layout == "kn" else B.t().contiguous().to(dev)
+    C = ops.gemm_i8(A.to(dev), Bd, b_layout=layout).cpu().numpy()
+    assert np.array_equal(C, orc.gemm_i8(A.numpy(), B.numpy()))
+
+
+def test_gemm_i8_golden(dev, golden):
+    g = golden("gemm_i8")
+    A = torch.from_numpy(g["A"]).to(dev)
+    B = torch.from_numpy(g["B"]).to(dev)
+    assert np.array_equal(ops.gemm_i8(A, B).cpu().numpy(), g["C"])
+    d = ops.gemm_i8_dequant(A, B, torch.from_numpy(g["row_scale"]).to(dev),
+                            torch.from_numpy(g["col_scale"]).to(dev))
+    assert np.array_equal(bits(d), g["dequant_f16_bits"])
+
+
+@pytest.mark.parametrize("cfg", S.gemm_configs(hxm.I8), ids=repr)
+def test_gemm_i8_every_config(dev, cfg):
+    print(f"gemm_i8 config {cfg}", flush=True)
+    M, N, K = 300, 260, 640
+    A = rand_i8((M, K), 3)
+    B = rand_i8((N, K), 4)  # resident [N, K] image
+    C = ops.gemm_i8(A.to(dev), B.to(dev), b_layout="nk", config=cfg).cpu().numpy()
+    assert np.array_equal(C, orc.gemm_i8(A.numpy(), B.numpy(), b_nk=True))
+
+
+def test_gemm_i8_accumulate_and_strides(dev):
+    M, N, K = 96, 80, 256
+    Afull = rand_i8((M, 320), 5)
+    A = Afull[:, :K]
+    Ad = Afull.to(dev)[:, :K]              # lda = 320 on the device
+    assert Ad.stride(0) == 320
+    B = rand_i8((N, K), 6)
+    C0 = torch.randint(-2 ** 31, 2 ** 31 - 1, (M, 100), dtype=torch.int32)
+    Cd = C0.to(dev)
+    ops.gemm_i8(Ad, B.to(dev), out=Cd[:, :N], b_layout="nk", accumulate=True)
+    exp = orc.gemm_i8(A.numpy(), B.numpy(), b_nk=True, C=C0[:, :N].numpy(), accumulate=True)
+    got = Cd.cpu().numpy()
+    assert np.array_equal(got[:, :N], exp)
+    assert np.array_equal(got[:, N:], C0[:, N:].numpy()), "wrote outside the output view"
+
+
+def test_gemm_i8_4096_cube(dev):
+    """4096^3, int32 exact and the dequant epilogue."""
+    n = 4096
+    A = rand_i8((n, n), 11)
+    B = rand_i8((n, n), 12)       # as [N, K]
+    g = torch.Generator().manual_seed(13)
+    rs = (torch.rand(n, generator=g) * 0.019 + 0.001).float()
+    cs = (torch.rand(n, generator=g) * 0.019 + 0.001).float()
+    Ad, Bd = A.to(dev), B.to(dev)
+    C = ops.gemm_i8(Ad, Bd, b_layout="nk").cpu().numpy()
+    a64, b64 = A.numpy().astype(np.int64), B.numpy().astype(np.int64)
+    c64 = C.astype(np.int64)
+    assert np.array_equal(c64.sum(axis=0), a64.sum(axis=0) @ b64.T)
+    assert np.array_equal(c64.sum(axis=1), a64 @ b64.sum(axis=0))
+    rows = np.random.default_rng(14).choice(n, 48, replace=False)
+    ref = orc.gemm_i8(A.numpy()[rows], B.numpy(), b_nk=True)
+    assert np.array_equal(C[rows], ref)
+    D = ops.gemm_i8_dequant(Ad, Bd, rs.to(dev), cs.to(dev), b_layout="nk")
+    assert np.array_equal(bits(D), orc.dequant_f16(C, rs.numpy(), cs.numpy()))
+
+
+def test_prepack_is_the_transpose(dev):
+    for dt, K, N in ((torch.int8, 300, 77), (torch.float16, 64, 1000)):
+        B = torch.randn(K, N).to(dt) if dt != torch.int8 else rand_i8((K, N), 7)
+        P = ops.prepack_weight(B.to(dev)).cpu()
+        assert torch.equal(P, B.t().contiguous())
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (64, 128, 64), (1024, 512, 64),
+                                   (256, 64, 2048), (128, 128, 128), (77, 150, 200)])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_matmul_within_tolerance(dev, M, N, K, dt):
+    """BASELINE config 1 (256^3) and the reference's S1/S2/S3 shapes
+    (ROADMAP.md:98-100), U[-1,1] inputs."""
+    print(f"matmul {dt} M={M} N={N} K={K}", flush=True)
+    g = torch.Generator().manual_seed(M + N + K)
+    a = (torch.rand(M, K, generator=g) * 2 - 1).to(dt)
+    b = (torch.rand(K, N, generator=g) * 2 - 1).to(dt)
+    name = "f16" if dt == torch.float16 else "bf16"
+    c = ops.matmul(a.to(dev), b.to(dev)).cpu()
+    ref = orc.to_f32(orc.matmul(bits(a), bits(b), ab_dtype=name, c_dtype=name), name)
+    np.testing.assert_allclose(c.float().numpy(), ref, rtol=1e-2, atol=1e-3)
+    c32 = ops.matmul(a.to(dev), b.t().contiguous().to(dev), b_layout="nk",
+                     out_dtype=torch.float32).cpu().numpy()
+    ref32 = orc.matmul(bits(a), bits(b), ab_dtype=name, c_dtype="f32")
+    np.testing.assert_allclose(c32, ref32, rtol=1e-4, atol=1e-4)
+
+
+def test_matmul_small_integers_bit_exact(dev, golden):
+    g = golden("matmul_f16")
+    a = torch.from_numpy(g["Ai_bits"].view(np.float16)).to(dev)
+    b = torch.from_numpy(g["Bi_bits"].view(np.float16)).to(dev)
+    assert np.array_equal(bits(ops.matmul(a, b)), g["Ci_bits"])
+    ar = torch.from_numpy(g["A_bits"].view(np.float16)).to(dev)
+    br = torch.from_numpy(g["B_bits"].view(np.float16)).to(dev)
+    np.testing.assert_allclose(ops.matmul(ar, br).float().cpu().numpy(), g["C_f64"],
+                               rtol=1e-2, atol=1e-3)
+
+
+def test_matmul_identity_and_accumulate(dev):
+    n = 128
+    B = torch.randn(n, 96).half()
+    I = torch.eye(n).half()
+    assert torch.equal(ops.matmul(I.to(dev), B.to(dev)).cpu(), B)
+    a = torch.randn(64, 128).half()
+    b = torch.randn(128, 96).half()
+    C0 = torch.randn(64, 96)
+    Cd = C0.to(dev)
+    ops.matmul(a.to(dev), b.to(dev), out=Cd, accumulate=True)
+    ref = orc.matmul(bits(a), bits(b), c_dtype="f32", C=C0.numpy(), accumulate=True)
+    np.testing.assert_allclose(Cd.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)
+
+
+def test_zero_k_and_empty(dev):
+    A = torch.empty(8, 0, dtype=torch.float16, device=dev)
+    B = torch.empty(0, 16, dtype=torch.float16, device=dev)
+    C = ops.matmul(A, B)
+    assert torch.equal(C.cpu(), torch.zeros(8, 16, dtype=torch.float16))
+    E = ops.gemm_i8(torch.empty(0, 32, dtype=torch.int8, device=dev),
+                    torch.empty(32, 8, dtype=torch.int8, device=dev))
+    assert E.shape == (0, 8)
+
+
+def test_refuses_misaligned_k(dev):
+    A = torch.zeros(8, 24, dtype=torch.int8, device=dev)
+    B = torch.zeros(24, 8, dtype=torch.int8, device=dev)
+    with pytest.raises(hxm.HxmError, match="tile-alignment"):
+        ops.gemm_i8(A, B)

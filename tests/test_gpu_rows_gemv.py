@@ -1,0 +1,149 @@
+"""GPU parity of the row reductions and the W8A16 GEMV against the CPU
+oracle (rtol 1e-2 / atol 1e-3 for fp16 outputs; the reference's own test
+tolerances, test_softmax.py:27-28 and test_rms_norm.py:24, are looser)."""
+import numpy as np
+import pytest
+import torch
+
+import hxm.ops as ops
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TDT = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+
+
+def host_bits(t, name):
+    t = t.cpu()
+    if name == "f32":
+        return t.numpy()
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+def tol(name):
+    return dict(rtol=1e-2, atol=1e-3) if name != "f32" else dict(rtol=1e-5, atol=1e-6)
+
+
+ROW_SHAPES = [(128, 128), (127, 513), (8192, 4096), (27, 8192), (5, 1), (3, 20000), (64, 1000)]
+
+
+@pytest.mark.parametrize("rows,cols", ROW_SHAPES)
+@pytest.mark.parametrize("name", ["f16", "bf16", "f32"])
+def test_softmax(dev, rows, cols, name):
+    print(f"softmax {name} {rows}x{cols}", flush=True)
+    g = torch.Generator().manual_seed(rows * 7 + cols)
+    x = (torch.randn(rows, cols, generator=g) * 2).to(TDT[name])
+    y = ops.softmax(x.to(dev))
+    ref = orc.to_f32(orc.softmax_rows(host_bits(x, name), name), name)
+    got = y.float().cpu().numpy()
+    np.testing.assert_allclose(got, ref, **tol(name))
+    assert np.allclose(got.sum(axis=1), 1.0, atol=2e-2)
+
+
+@pytest.mark.parametrize("rows,cols", ROW_SHAPES)
+@pytest.mark.parametrize("name", ["f16", "bf16", "f32"])
+def test_rmsnorm(dev, rows, cols, name):
+    print(f"rmsnorm {name} {rows}x{cols}", flush=True)
+    g = torch.Generator().manual_seed(rows * 11 + cols)
+    x = (torch.randn(rows, cols, generator=g) * 2).to(TDT[name])
+    w = (1 + 0.1 * torch.randn(cols, generator=g)).to(TDT[name])
+    y = ops.rms_norm(x.to(dev), (cols,), weight=w.to(dev), eps=1e-6)
+    ref = orc.to_f32(orc.rmsnorm_rows(host_bits(x, name), host_bits(w, name), 1e-6, name), name)
+    np.testing.assert_allclose(y.float().cpu().numpy(), ref, **tol(name))
+
+
+@pytest.mark.parametrize("rows,cols", [(27, 8192), (8192, 4096), (33, 300), (2, 17000)])
+@pytest.mark.parametrize("name", ["f32", "f16"])
+def test_layernorm(dev, rows, cols, name):
+    print(f"layernorm {name} {rows}x{cols}", flush=True)
+    g = torch.Generator().manual_seed(rows + cols)
+    x = torch.rand(rows, cols, generator=g).to(TDT[name])
+    w = torch.rand(cols, generator=g).to(TDT[name])
+    b = torch.rand(cols, generator=g).to(TDT[name])
+    y, mean, rstd = ops.layer_norm(x.to(dev), (cols,), w.to(dev), b.to(dev), eps=1e-5,
+                                   return_stats=True)
+    ry, rm, rr = orc.layernorm_rows(host_bits(x, name), host_bits(w, name), host_bits(b, name),
+                                    1e-5, name)
+    np.testing.assert_allclose(y.float().cpu().numpy(), orc.to_f32(ry, name), **tol(name))
+    np.testing.assert_allclose(mean.cpu().numpy(), rm, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(rstd.cpu().numpy(), rr, rtol=1e-4)
+
+
+def test_rows_golden(dev, golden):
+    g = golden("rows")
+    xs = torch.from_numpy(g["softmax_x_bits"].view(np.float16)).to(dev)
+    np.testing.assert_allclose(ops.softmax(xs).float().cpu().numpy(), g["softmax_y"],
+                               rtol=1e-2, atol=1e-3)
+    xr = torch.from_numpy(g["rms_x_bits"].view(np.float16)).to(dev)
+    gr = torch.from_numpy(g["rms_gamma_bits"].view(np.float16)).to(dev)
+    np.testing.assert_allclose(ops.rms_norm(xr, (513,), gr, eps=1e-6).float().cpu().numpy(),
+                               g["rms_y"], rtol=1e-2, atol=1e-2)
+    xl = torch.from_numpy(g["ln_x"]).to(dev)
+    y = ops.layer_norm(xl, (8192,), torch.from_numpy(g["ln_w"]).to(dev),
+                       torch.from_numpy(g["ln_b"]).to(dev), eps=1e-5)
+    np.testing.assert_allclose(y.cpu().numpy(), g["ln_y"], rtol=1e-5, atol=1e-5)
+
+
+def test_rows_strided_inplace_and_edge_values(dev):
+    x = (torch.randn(16, 700) * 3).half()
+    xd = torch.zeros(16, 704, dtype=torch.float16, device=dev)
+    xd[:, :700] = x.to(dev)
+    view = xd[:, :700]                      # ld 704: aligned rows
+    ops.softmax(view, out=view)             # in place
+    ref = orc.f16_bits_to_f32(orc.softmax_rows(host_bits(x, "f16")))
+    np.testing.assert_allclose(view.float().cpu().numpy(), ref, rtol=1e-2, atol=1e-3)
+    odd = torch.randn(9, 101).half()        # ld 101: unaligned rows
+    od = odd.to(dev)
+    np.testing.assert_allclose(ops.softmax(od).float().cpu().numpy(),
+                               orc.f16_bits_to_f32(orc.softmax_rows(host_bits(odd, "f16"))),
+                               rtol=1e-2, atol=1e-3)
+    # a -inf entry gets probability 0; a constant row is uniform
+    e = torch.zeros(2, 64, dtype=torch.float16)
+    e[0, 5] = float("-inf")
+    y = ops.softmax(e.to(dev)).cpu()
+    assert y[0, 5] == 0 and torch.allclose(y[1].float(), torch.full((64,), 1 / 64), atol=1e-4)
+    # zero row through RMSNorm stays 0 (eps inside the root)
+    z = ops.rms_norm(torch.zeros(1, 256, dtype=torch.float16, device=dev), (256,), eps=1e-6)
+    assert (z.cpu() == 0).all()
+    assert ops.softmax(torch.empty(0, 32, dtype=torch.float16, device=dev)).shape == (0, 32)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_gemv_baseline_shape(dev, M):
+    """N=11008, K=4096, M in {1,4,16}."""
+    print(f"gemv M={M}", flush=True)
+    N, K = 11008, 4096
+    g = torch.Generator().manual_seed(M)
+    x = torch.randn(M, K, generator=g).half()
+    W = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sc = (torch.rand(N, generator=g) * 0.019 + 0.001).half()
+    y = ops.gemv_w8a16(x.to(dev), W.to(dev), sc.to(dev)).cpu()
+    ref = orc.f16_bits_to_f32(orc.gemv_w8a16(host_bits(x, "f16"), W.numpy(),
+                                             host_bits(sc, "f16")))
+    np.testing.assert_allclose(y.float().numpy(), ref, rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("M,N,K", [(3, 100, 272), (33, 64, 512), (1, 17, 16), (16, 48, 256)])
+def test_gemv_ragged(dev, M, N, K):
+    g = torch.Generator().manual_seed(M * N + K)
+    x = torch.randn(M, K, generator=g).half()
+    W = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sc = (torch.rand(N, generator=g) * 0.019 + 0.001).half()
+    y = ops.gemv_w8a16(x.to(dev), W.to(dev), sc.to(dev)).cpu()
+    ref = orc.f16_bits_to_f32(orc.gemv_w8a16(host_bits(x, "f16"), W.numpy(),
+                                             host_bits(sc, "f16")))
+    np.testing.assert_allclose(y.float().numpy(), ref, rtol=1e-2, atol=1e-3)
+
+
+def test_gemv_golden_and_exact_small_ints(dev, golden):
+    gd = golden("gemv_w8a16")
+    y = ops.gemv_w8a16(torch.from_numpy(gd["x_bits"].view(np.float16)).to(dev),
+                       torch.from_numpy(gd["W"]).to(dev),
+                       torch.from_numpy(gd["scale_bits"].view(np.float16)).to(dev))
+    np.testing.assert_allclose(y.float().cpu().numpy(), gd["y_f64"], rtol=1e-2, atol=1e-3)
+    # every int8 value -128..127 through the exact f16 conversion: x = e_k
+    K = 256
+    W = torch.arange(-128, 128, dtype=torch.int16).to(torch.int8).repeat(2, 1)  # [2, 256]
+    x = torch.eye(K)[:16].half()                                                # picks k=0..15
+    y = ops.gemv_w8a16(x.to(dev), W.to(dev), torch.ones(2).half().to(dev)).cpu()
+    assert torch.equal(y.float(), W[:, :16].t().float())

@@ -1,0 +1,44 @@
+"""The measured tile search on the GPU: every candidate is launched, checked
+bit-exact against the control config, timed; the winner is cached and used by
+later calls (hmx_search.py's autotune sweep + hexagon_bench +
+judge_champion_round)."""
+import numpy as np
+import pytest
+import torch
+
+import hxm.ops as ops
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype,M,N,K", [(torch.int8, 512, 512, 512),
+                                         (torch.float16, 256, 256, 256)])
+def test_tune_gemm_picks_a_verified_winner(dev, dtype, M, N, K):
+    g = torch.Generator().manual_seed(M)
+    if dtype == torch.int8:
+        A = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+        B = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+        out = torch.empty(M, N, dtype=torch.int32, device=dev)
+    else:
+        A = (torch.rand(M, K, generator=g) * 2 - 1).half()
+        B = (torch.rand(N, K, generator=g) * 2 - 1).half()
+        out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    Ad, Bd = A.to(dev), B.to(dev)
+    best, rep = ops.tune_gemm(Ad, Bd, out, reps=5)
+    print(rep, flush=True)
+    assert rep["round_verdict"] in ("valid", "invalid-canary")
+    assert rep["champion"] is not None
+    measured = [c for c in rep["configs"] if c["q50"] is not None]
+    assert measured and all(c["verified"] for c in measured)
+    win = rep["configs"][rep["champion"]]
+    assert win["tiles"][:2] == [best.bm, best.bn]
+    # later calls with no config use the cached winner and stay correct
+    if dtype == torch.int8:
+        C = ops.gemm_i8(Ad, Bd, b_layout="nk").cpu().numpy()
+        assert np.array_equal(C, orc.gemm_i8(A.numpy(), B.numpy(), b_nk=True))
+    else:
+        C = ops.matmul(Ad, Bd, b_layout="nk").float().cpu().numpy()
+        bits = lambda t: t.view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+        ref = orc.f16_bits_to_f32(orc.matmul(bits(A), bits(B), b_nk=True))
+        np.testing.assert_allclose(C, ref, rtol=1e-2, atol=1e-3)

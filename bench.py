@@ -5,23 +5,24 @@ Headline: int8 GEMM M=N=K=4096, A,B ~ U{-127..127},
 exact int32 accumulation, per-row x per-col fp32 scales dequantised to fp16
 (hxm_gemm_i8_dequant).  B is the resident [N,K] image made once before the
 timed region (the reference's weight-resident path).  One step = one GEMM
-launch on inputs already resident in HBM.  value = 2*M*N*K / time, in
-tera-ops/s (TFLOP/s slot of the schema, int8 ops counted like flops).
+launch on inputs already resident in HBM.  value = 2*M*N*K / time in
+tera-ops/s (int8 ops are counted like flops in the roofline's TFLOP/s slot).
 
-Also reported under "extra" (not the headline): W8A16 GEMV M in {1,4,16},
-softmax / RMSNorm rows on f16 [8192 x 4096] (all HBM-bound, timed while
-rotating buffer sets larger than the 256 MB Infinity Cache), the fp16 256^3
-matmul (launch-bound) and the int32-output int8 GEMM.
+Also reported under "extra" (not the headline): the int32-output int8 GEMM,
+the fp16 256^3 matmul (launch-bound), W8A16 GEMV M in {1,4,16} and softmax /
+RMSNorm rows on f16 [8192 x 4096] (HBM-bound: timed while rotating buffer
+sets larger than the 256 MB Infinity Cache).
 
 cpu_baseline: the C restatement in oracle/ (OpenMP over the host cores)
 timed on a bounded row sample of the same GEMM.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       python bench.py --only {int8,int8_i32,f16,gemv,rows,copy}  (one workload,
+       for rocprofv3 runs; prints that workload's record)
 """
 from __future__ import annotations
 
 import argparse
-import ctypes
 import json
 import os
 import statistics
@@ -41,22 +42,171 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def event_time_ms(torch, fn, steps, warmup, rotate=1):
-    """Average per-launch time over `steps` launches, HIP events on torch's
-    current stream (the stream every launch here is issued on)."""
-    for i in range(warmup):
-        fn(i % rotate)
+class Ctx:
+    def __init__(self, args):
+        import torch
+
+        import hxm
+        import hxm.ops as ops
+        self.args, self.torch, self.hxm, self.ops = args, torch, hxm, ops
+        self.L = hxm.lib
+        self.dev = torch.device("cuda:0")
+        self.stream = torch.cuda.current_stream().cuda_stream
+
+    def time_ms(self, fn, steps, warmup, rotate=1):
+        """Average per-launch time over `steps` launches: HIP events recorded
+        on torch's current stream, the stream every launch here is issued on."""
+        torch = self.torch
+        for i in range(warmup):
+            fn(i % rotate)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for i in range(steps):
+            fn(i % rotate)
+        e1.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / steps
+        return e0.elapsed_time(e1) / steps, wall
+
+
+def int8_operands(c):
+    torch, dev = c.torch, c.dev
+    n = 4096
+    g = torch.Generator().manual_seed(1)
+    A = torch.randint(-127, 128, (n, n), generator=g, dtype=torch.int8).to(dev)
+    g.manual_seed(2)
+    B_kn = torch.randint(-127, 128, (n, n), generator=g, dtype=torch.int8).to(dev)
+    g.manual_seed(3)
+    rs = (torch.rand(n, generator=g) * 0.019 + 0.001).to(dev)
+    g.manual_seed(4)
+    cs = (torch.rand(n, generator=g) * 0.019 + 0.001).to(dev)
+    Bp = c.ops.prepack_weight(B_kn)             # resident [N, K] image, once
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    return A, Bp, rs, cs
+
+
+def run_int8(c, A, Bp, rs, cs, out_i32=False):
+    torch, hxm, L = c.torch, c.hxm, c.L
+    M = N = K = 4096
+    C = torch.empty(M, N, dtype=torch.int32 if out_i32 else torch.float16, device=c.dev)
+    a, b, r, s, o, st = (A.data_ptr(), Bp.data_ptr(), rs.data_ptr(), cs.data_ptr(),
+                         C.data_ptr(), c.stream)
+    if out_i32:
+        def step(_):
+            hxm.check(L.hxm_gemm_i8(a, K, b, K, hxm.B_NK, o, N, M, N, K, 0, None, st),
+                      "hxm_gemm_i8")
+    else:
+        def step(_):
+            hxm.check(L.hxm_gemm_i8_dequant(a, K, b, K, hxm.B_NK, r, s, o, N, M, N, K, None,
+                                            st), "hxm_gemm_i8_dequant")
+    ms, wall = c.time_ms(step, c.args.steps, c.args.warmup)
+    ops_per = 2.0 * M * N * K
+    return {"us": ms * 1e3, "wall_us": wall * 1e3, "TOPS": ops_per / (ms * 1e-3) / 1e12,
+            "ops_per_launch": ops_per}
+
+
+def run_f16(c):
+    torch, hxm, L = c.torch, c.hxm, c.L
+    a16 = (torch.rand(256, 256, device=c.dev) * 2 - 1).half()
+    b16 = c.ops.prepack_weight((torch.rand(256, 256, device=c.dev) * 2 - 1).half())
+    c16 = torch.empty(256, 256, dtype=torch.float16, device=c.dev)
+    pa, pb, pc, st = a16.data_ptr(), b16.data_ptr(), c16.data_ptr(), c.stream
+
+    def step(_):
+        hxm.check(L.hxm_matmul(pa, 256, pb, 256, hxm.B_NK, pc, 256, 256, 256, 256, hxm.F16,
+                               hxm.F16, 0, None, st), "hxm_matmul")
+    ms, _ = c.time_ms(step, c.args.steps, c.args.warmup)
+    return {"f16_matmul_256": {"us": ms * 1e3, "TFLOPS": 2 * 256 ** 3 / (ms * 1e-3) / 1e12,
+                               "note": "launch-bound; roofline fraction not meaningful"}}
+
+
+def run_gemv(c):
+    torch, hxm, L = c.torch, c.hxm, c.L
+    N, K, R = 11008, 4096, 12            # 12 weight copies = 540 MB rotated
+    Ws = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=c.dev) for _ in range(R)]
+    scs = [(torch.rand(N, device=c.dev) * 0.019 + 0.001).half() for _ in range(R)]
+    wp = [w.data_ptr() for w in Ws]
+    sp = [s.data_ptr() for s in scs]
+    out = {}
+    for M in (1, 4, 16):
+        xs = torch.randn(M, K, device=c.dev).half()
+        ys = torch.empty(M, N, dtype=torch.float16, device=c.dev)
+        px, py, st = xs.data_ptr(), ys.data_ptr(), c.stream
+
+        def step(i, M=M, px=px, py=py):
+            hxm.check(L.hxm_gemv_w8a16(px, K, wp[i], K, sp[i], py, N, M, N, K, st),
+                      "hxm_gemv_w8a16")
+        ms, _ = c.time_ms(step, 240, 24, rotate=R)
+        nbytes = N * K + N * 2 + M * K * 2 + M * N * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"w8a16_gemv_M{M}"] = {"us": ms * 1e3, "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
+                                   "bytes": nbytes}
+    return out
+
+
+def run_rows(c):
+    torch, hxm, L = c.torch, c.hxm, c.L
+    rows, cols, R = 8192, 4096, 4        # 4 sets x 128 MiB rotated
+    xs = [(torch.randn(rows, cols, device=c.dev) * 2).half() for _ in range(R)]
+    ys = [torch.empty_like(xs[0]) for _ in range(R)]
+    gam = (1 + 0.1 * torch.randn(cols, device=c.dev)).half()
+    xp = [t.data_ptr() for t in xs]
+    yp = [t.data_ptr() for t in ys]
+    gp, st = gam.data_ptr(), c.stream
+
+    def softmax(i):
+        hxm.check(L.hxm_softmax_rows(xp[i], cols, yp[i], cols, rows, cols, hxm.F16, st),
+                  "hxm_softmax_rows")
+
+    def rms(i):
+        hxm.check(L.hxm_rmsnorm_rows(xp[i], cols, gp, yp[i], cols, rows, cols, 1e-6, hxm.F16,
+                                     st), "hxm_rmsnorm_rows")
+    out = {}
+    for name, fn, nbytes in (("softmax_f16_8192x4096", softmax, 2 * rows * cols * 2),
+                             ("rmsnorm_f16_8192x4096", rms, 2 * rows * cols * 2 + cols * 2)):
+        ms, _ = c.time_ms(fn, 200, 20, rotate=R)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us": ms * 1e3, "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
+                     "bytes": nbytes}
+    return out
+
+
+def run_copy(c):
+    """A plain 256 MiB device copy (torch's elementwise copy kernel): the
+    known-size reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE."""
+    torch = c.torch
+    src = torch.empty(1 << 28, dtype=torch.uint8, device=c.dev).fill_(1)
+    dst = torch.empty_like(src)
+    ms, _ = c.time_ms(lambda i: dst.copy_(src), c.args.steps, c.args.warmup)
+    return {"copy_256MiB": {"us": ms * 1e3, "bytes_read": 1 << 28, "bytes_written": 1 << 28,
+                            "GB/s": 2 * (1 << 28) / (ms * 1e-3) / 1e9}}
+
+
+def cpu_baseline(A, Bp, seconds):
+    from oracle import oracle as orc
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    threads = max(1, min(threads, os.cpu_count() or 1))
+    Ah, Bh = A.cpu().numpy(), Bp.cpu().numpy()
+    M, K = Ah.shape
+    N = Bh.shape[0]
     t0 = time.perf_counter()
-    e0.record()
-    for i in range(steps):
-        fn(i % rotate)
-    e1.record()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) * 1e3 / steps
-    return e0.elapsed_time(e1) / steps, wall
+    orc.gemm_i8(Ah[:8], Bh, b_nk=True, threads=threads)
+    probe = max(time.perf_counter() - t0, 1e-6)
+    rows = int(min(M, max(8, 8 * seconds / probe / 3)))
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        orc.gemm_i8(Ah[:rows], Bh, b_nk=True, threads=threads)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": 2.0 * rows * N * K / t / 1e12, "unit": "TOPS", "cores": threads,
+            "kind": "port",
+            "sample": f"int8 GEMM rows 0..{rows - 1} of A[{M},{K}] x resident B[{N},{K}] -> "
+                      f"int32 (C restatement oracle/oracle.c, gcc -O3 OpenMP, {threads} "
+                      f"threads), median of 3 runs of {t:.3f} s"}
 
 
 def main() -> int:
@@ -65,157 +215,42 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="approximate CPU time budget of the cpu_baseline sample")
+                    help="approximate CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only", choices=["int8", "int8_i32", "f16", "gemv", "rows", "copy"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: the hot path here is a single-GPU kernel set "
-              "and no multi-GPU path is built (see DESIGN.md, 'How the path would shard').",
+        print("bench.py measures one GPU: this build is the single-GPU kernel set of the hot "
+              "path and has no multi-GPU path (DESIGN.md describes how it would shard).",
               file=sys.stderr)
         return 2
+    c = Ctx(args)
 
-    import numpy as np
-    import torch
+    if args.only:
+        if args.only in ("int8", "int8_i32"):
+            rec = {args.only: run_int8(c, *int8_operands(c), out_i32=args.only == "int8_i32")}
+        else:
+            rec = {"f16": run_f16, "gemv": run_gemv, "rows": run_rows, "copy": run_copy}[
+                args.only](c)
+        print(json.dumps(rec), flush=True)
+        return 0
 
-    import hxm
-    import hxm.ops as ops
-
-    dev = torch.device("cuda:0")
-    stream = torch.cuda.current_stream().cuda_stream
-    L = hxm.lib
-
-    # ---------------- headline: int8 GEMM 4096^3 + dequant -----------------
-    M = N = K = 4096
-    g = torch.Generator().manual_seed(1)
-    A = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
-    g.manual_seed(2)
-    B_kn = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8).to(dev)
-    g.manual_seed(3)
-    rs = (torch.rand(M, generator=g) * 0.019 + 0.001).to(dev)
-    g.manual_seed(4)
-    cs = (torch.rand(N, generator=g) * 0.019 + 0.001).to(dev)
-    Bp = ops.prepack_weight(B_kn)               # resident [N, K] image, once
-    C16 = torch.empty(M, N, dtype=torch.float16, device=dev)
-    C32 = torch.empty(M, N, dtype=torch.int32, device=dev)
-    torch.cuda.synchronize()
-
-    a_p, b_p, rs_p, cs_p, c_p = (A.data_ptr(), Bp.data_ptr(), rs.data_ptr(), cs.data_ptr(),
-                                 C16.data_ptr())
-
-    def step_dequant(_):
-        st = L.hxm_gemm_i8_dequant(a_p, K, b_p, K, hxm.B_NK, rs_p, cs_p, c_p, N, M, N, K,
-                                   None, stream)
-        if st:
-            hxm.check(st, "hxm_gemm_i8_dequant")
-
-    ms, wall_ms = event_time_ms(torch, step_dequant, args.steps, args.warmup)
-    ops_per = 2.0 * M * N * K
-    tops = ops_per / (ms * 1e-3) / 1e12
-    log(f"int8 gemm+dequant 4096^3: {ms * 1e3:.1f} us/launch (wall {wall_ms * 1e3:.1f}), "
-        f"{tops:.0f} TOPS")
-
+    A, Bp, rs, cs = int8_operands(c)
+    head = run_int8(c, A, Bp, rs, cs)
+    log("int8 gemm+dequant 4096^3:", json.dumps(head))
     extra = {}
     if not args.no_extra:
-        c32_p = C32.data_ptr()
-
-        def step_i32(_):
-            hxm.check(L.hxm_gemm_i8(a_p, K, b_p, K, hxm.B_NK, c32_p, N, M, N, K, 0, None,
-                                    stream), "hxm_gemm_i8")
-        ms32, _ = event_time_ms(torch, step_i32, args.steps, args.warmup)
-        extra["int8_gemm_i32_out_4096"] = {"us": ms32 * 1e3,
-                                           "TOPS": ops_per / (ms32 * 1e-3) / 1e12}
-        del C32
-
-        # fp16 matmul 256^3 (launch-bound).
-        a16 = (torch.rand(256, 256, device=dev) * 2 - 1).half()
-        b16 = ops.prepack_weight((torch.rand(256, 256, device=dev) * 2 - 1).half())
-        c16 = torch.empty(256, 256, dtype=torch.float16, device=dev)
-        pa, pb, pc = a16.data_ptr(), b16.data_ptr(), c16.data_ptr()
-
-        def step_mm(_):
-            hxm.check(L.hxm_matmul(pa, 256, pb, 256, hxm.B_NK, pc, 256, 256, 256, 256,
-                                   hxm.F16, hxm.F16, 0, None, stream), "hxm_matmul")
-        msm, _ = event_time_ms(torch, step_mm, args.steps, args.warmup)
-        extra["f16_matmul_256"] = {"us": msm * 1e3,
-                                   "TFLOPS": 2 * 256 ** 3 / (msm * 1e-3) / 1e12,
-                                   "note": "launch-bound; roofline fraction not meaningful"}
-
-        # W8A16 GEMV, N=11008, K=4096: rotate 12 weight copies (540 MB).
-        Ng, Kg, R = 11008, 4096, 12
-        Ws = [torch.randint(-127, 128, (Ng, Kg), dtype=torch.int8, device=dev)
-              for _ in range(R)]
-        scs = [(torch.rand(Ng, device=dev) * 0.019 + 0.001).half() for _ in range(R)]
-        for Mg in (1, 4, 16):
-            xs = torch.randn(Mg, Kg, device=dev).half()
-            ys = torch.empty(Mg, Ng, dtype=torch.float16, device=dev)
-            wp = [w.data_ptr() for w in Ws]
-            sp = [s.data_ptr() for s in scs]
-            px, py = xs.data_ptr(), ys.data_ptr()
-
-            def step_gemv(i, Mg=Mg, wp=wp, sp=sp, px=px, py=py):
-                hxm.check(L.hxm_gemv_w8a16(px, Kg, wp[i], Kg, sp[i], py, Ng, Mg, Ng, Kg,
-                                           stream), "hxm_gemv_w8a16")
-            msg, _ = event_time_ms(torch, step_gemv, 240, 24, rotate=R)
-            nbytes = Ng * Kg + Ng * 2 + Mg * Kg * 2 + Mg * Ng * 2
-            gbs = nbytes / (msg * 1e-3) / 1e9
-            extra[f"w8a16_gemv_M{Mg}"] = {"us": msg * 1e3, "GB/s": gbs,
-                                          "hbm_frac": gbs / PEAK_HBM_GBS, "bytes": nbytes}
-        del Ws, scs
-
-        # Row ops on f16 [8192, 4096], 4 buffer sets (536 MB).
-        rows, cols, R2 = 8192, 4096, 4
-        xs = [(torch.randn(rows, cols, device=dev) * 2).half() for _ in range(R2)]
-        ys = [torch.empty_like(xs[0]) for _ in range(R2)]
-        gam = (1 + 0.1 * torch.randn(cols, device=dev)).half()
-        xp = [t.data_ptr() for t in xs]
-        yp = [t.data_ptr() for t in ys]
-        gp = gam.data_ptr()
-
-        def step_softmax(i):
-            hxm.check(L.hxm_softmax_rows(xp[i], cols, yp[i], cols, rows, cols, hxm.F16,
-                                         stream), "hxm_softmax_rows")
-
-        def step_rms(i):
-            hxm.check(L.hxm_rmsnorm_rows(xp[i], cols, gp, yp[i], cols, rows, cols, 1e-6,
-                                         hxm.F16, stream), "hxm_rmsnorm_rows")
-        for name, fn, nbytes in (("softmax_f16_8192x4096", step_softmax, 2 * rows * cols * 2),
-                                 ("rmsnorm_f16_8192x4096", step_rms,
-                                  2 * rows * cols * 2 + cols * 2)):
-            msr, _ = event_time_ms(torch, fn, 200, 20, rotate=R2)
-            gbs = nbytes / (msr * 1e-3) / 1e9
-            extra[name] = {"us": msr * 1e3, "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
-                           "bytes": nbytes}
-        del xs, ys
+        extra["int8_gemm_i32_out_4096"] = run_int8(c, A, Bp, rs, cs, out_i32=True)
+        for fn in (run_f16, run_gemv, run_rows):
+            extra.update(fn(c))
         for k, v in extra.items():
             log(k, json.dumps(v))
-
-    # ---------------- CPU baseline (oracle, bounded sample) -----------------
-    cpu = None
-    if not args.no_cpu_baseline:
-        from oracle import oracle as orc
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
-        threads = max(1, min(threads, os.cpu_count() or 1))
-        Ah = A.cpu().numpy()
-        Bh = Bp.cpu().numpy()
-        rows = 8
-        t0 = time.perf_counter()
-        orc.gemm_i8(Ah[:rows], Bh, b_nk=True, threads=threads)
-        t_probe = time.perf_counter() - t0
-        rows = int(min(M, max(rows, rows * args.cpu_seconds / max(t_probe, 1e-6))))
-        times = []
-        for _ in range(1 if rows * t_probe / 8 > 3 else 3):
-            t0 = time.perf_counter()
-            orc.gemm_i8(Ah[:rows], Bh, b_nk=True, threads=threads)
-            times.append(time.perf_counter() - t0)
-        t = statistics.median(times)
-        cpu = {"value": 2.0 * rows * N * K / t / 1e12, "unit": "TOPS", "cores": threads,
-               "kind": "port",
-               "sample": f"int8 GEMM rows 0..{rows - 1} of A[4096,4096] x resident "
-                         f"B[4096,4096] -> int32 (C restatement oracle/oracle.c, "
-                         f"gcc -O3 OpenMP), median of {len(times)} run(s), {t:.2f} s each"}
+    cpu = None if args.no_cpu_baseline else cpu_baseline(A, Bp, args.cpu_seconds)
+    if cpu:
         log("cpu baseline", json.dumps(cpu))
 
+    tops = head["TOPS"]
     out = {
         "metric": "int8 GEMM 4096^3 TOPS (int32 accumulate, fp16 dequant) + % MFMA peak",
         "value": tops,
@@ -223,7 +258,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms,
+        "ms_per_step": head["us"] / 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -231,11 +266,11 @@ def main() -> int:
         "data": "synthetic (seeded U{-127..127} int8, U[0.001,0.02] fp32 scales)",
         "config": {"workload": "int8 GEMM M=N=K=4096, int32 accumulate, per-row x per-col "
                                "fp32 scales dequant to fp16; B resident [N,K] image",
-                   "M": M, "N": N, "K": K, "parallelism": "single-gpu"},
+                   "M": 4096, "N": 4096, "K": 4096, "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS,
                      "unit": "TFLOP/s", "frac": tops / PEAK_INT8_TOPS, "traffic": None,
                      "kernel": "gemm_kernel<int8_t,...,kEpiDequant>",
-                     "work_per_launch": ops_per, "avg_launch_us": ms * 1e3},
+                     "work_per_launch": head["ops_per_launch"], "avg_launch_us": head["us"]},
         "cpu_baseline": cpu,
         "extra": extra,
     }

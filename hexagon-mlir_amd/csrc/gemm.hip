@@ -215,8 +215,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
                                                    static_cast<uint32_t>(r))
                             : r;
         } else if constexpr (EPI == kEpiDequant) {
-          // fp32, left to right, two roundings; a product cannot contract.
-          const float d = (static_cast<float>(acc[i][j][v]) * g.row_scale[m]) * cs;
+          // fp32, left to right, each product rounded to fp32 and then once
+          // to f16.  The empty asm pins d as an fp32 register value: without
+          // it the backend folds the last multiply and the f16 conversion
+          // into v_fma_mixlo_f16 (a single rounding), which differs from the
+          // defined spelling in the last f16 bit for some inputs.
+          float d = (static_cast<float>(acc[i][j][v]) * g.row_scale[m]) * cs;
+          asm volatile("" : "+v"(d));
           static_cast<_Float16*>(g.C)[off] = static_cast<_Float16>(d);
         } else {
           float r = acc[i][j][v];

@@ -92,6 +92,13 @@ SIGNATURES = {
 
 
 def _load():
+    # One HIP runtime per process: torch ships its own libamdhip64.so.7.  If
+    # torch is importable it is loaded first, so that libhxm's dependency on
+    # that soname binds to the runtime torch's tensors and streams live in.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     if not os.path.exists(LIB_PATH):
         raise ImportError(
             f"libhxm.so not found at {LIB_PATH}: build it first "

@@ -100,6 +100,24 @@ def test_gemm_i8_4096_cube(dev):
     assert np.array_equal(bits(D), orc.dequant_f16(C, rs.numpy(), cs.numpy()))
 
 
+def test_gemm_i8_dequant_double_rounding(dev):
+    """512 x 512 x 4096: at this size some outputs sit where a fused
+    multiply-convert (one rounding) and the defined fp32-then-f16 spelling
+    (two roundings) disagree, so the epilogue's spelling is observable."""
+    A = rand_i8((512, 4096), 21)
+    B = rand_i8((512, 4096), 22)
+    g = torch.Generator().manual_seed(23)
+    rs = (torch.rand(512, generator=g) * 0.019 + 0.001).float()
+    cs = (torch.rand(512, generator=g) * 0.019 + 0.001).float()
+    D = ops.gemm_i8_dequant(A.to(dev), B.to(dev), rs.to(dev), cs.to(dev), b_layout="nk")
+    acc = orc.gemm_i8(A.numpy(), B.numpy(), b_nk=True)
+    exp = orc.dequant_f16(acc, rs.numpy(), cs.numpy())
+    fused = (acc.astype(np.float32) * rs.numpy()[:, None]).astype(np.float64) * \
+        cs.numpy()[None, :].astype(np.float64)
+    assert not np.array_equal(fused.astype(np.float16).view(np.uint16), exp)
+    assert np.array_equal(bits(D), exp)
+
+
 def test_prepack_is_the_transpose(dev):
     for dt, K, N in ((torch.int8, 300, 77), (torch.float16, 64, 1000)):
         B = torch.randn(K, N).to(dt) if dt != torch.int8 else rand_i8((K, N), 7)

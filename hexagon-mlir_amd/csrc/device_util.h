@@ -18,6 +18,9 @@ typedef float v16f32 __attribute__((ext_vector_type(16)));
 typedef _Float16 v8f16 __attribute__((ext_vector_type(8)));
 typedef __bf16 v8bf16 __attribute__((ext_vector_type(8)));
 typedef _Float16 v2f16 __attribute__((ext_vector_type(2)));
+typedef _Float16 v4f16_t __attribute__((ext_vector_type(4)));
+typedef __bf16 v4bf16_t __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u32_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float tof(_Float16 v) { return static_cast<float>(v); }
 __device__ __forceinline__ float tof(__bf16 v) { return static_cast<float>(v); }

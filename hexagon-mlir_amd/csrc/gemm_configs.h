@@ -1,8 +1,11 @@
-// The compiled GEMM configurations: X(BM, BN, WAVES_M, WAVES_N).  K is staged
-// 128 bytes at a time (128 int8 or 64 f16/bf16 elements), split_k is 1.
-// The tile search (search.cpp) measures exactly this list.
+// The compiled GEMM configurations: X(BM, BN, BKB, STAGES, WAVES_M, WAVES_N)
+// with BKB the K bytes per LDS stage (bk = BKB int8 or BKB/2 f16/bf16
+// elements).  split_k is 1.  The tile search (search.hip) measures exactly
+// this list; the LDS footprint is STAGES * (BM + BN) * BKB bytes.
 #pragma once
 
-#define HXM_GEMM_CONFIG_LIST(X)                                              \
-  X(256, 256, 2, 2), X(256, 128, 2, 2), X(128, 256, 2, 2), X(128, 128, 2, 2), \
-      X(64, 64, 2, 2), X(32, 32, 1, 1)
+#define HXM_GEMM_CONFIG_LIST(X)                                                 \
+  X(256, 256, 128, 2, 2, 2), X(256, 256, 64, 4, 2, 2), X(256, 256, 64, 3, 2, 2), \
+      X(256, 128, 128, 3, 2, 2), X(256, 128, 64, 4, 2, 2),                       \
+      X(128, 256, 64, 4, 2, 2), X(128, 128, 128, 2, 2, 2),                       \
+      X(128, 128, 64, 4, 2, 2), X(64, 64, 128, 2, 2, 2), X(32, 32, 128, 2, 1, 1)

@@ -153,11 +153,13 @@ int32_t hxm_gpu_tile_verdict(const hxm_gemm_config* cfg, int32_t ab_dtype,
       bn % (kTileEdge * cfg->waves_n))
     return HXM_REASON_TILE_ALIGNMENT;
   if (lds_budget <= 0) lds_budget = kDefaultLdsBudget;
-  if (2 * (bm + bn) * bk * eb > lds_budget) return HXM_REASON_LDS_BUDGET;
+  const int64_t stages = cfg->stages > 0 ? cfg->stages : 2;
+  if (stages * (bm + bn) * bk * eb > lds_budget) return HXM_REASON_LDS_BUDGET;
   for (int i = 0; i < num_kernels(); ++i) {
     const hxm_gemm_config k = kernel_config(i, ab_dtype);
     if (k.bm == cfg->bm && k.bn == cfg->bn && k.bk == cfg->bk &&
         k.waves_m == cfg->waves_m && k.waves_n == cfg->waves_n &&
+        (cfg->stages == 0 || cfg->stages == k.stages) &&
         (cfg->split_k == 0 || cfg->split_k == 1))
       return HXM_REASON_OK;
   }
@@ -284,8 +286,8 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
     if (hxm_gpu_tile_verdict(&c, op, 0) == HXM_REASON_OK) cands.push_back(c);
   }
   std::sort(cands.begin(), cands.end(), [](const hxm_gemm_config& a, const hxm_gemm_config& b) {
-    return std::make_tuple(a.bm, a.bn, a.bk, a.waves_m, a.waves_n) <
-           std::make_tuple(b.bm, b.bn, b.bk, b.waves_m, b.waves_n);
+    return std::make_tuple(a.bm, a.bn, a.bk, a.waves_m, a.waves_n, a.stages) <
+           std::make_tuple(b.bm, b.bn, b.bk, b.waves_m, b.waves_n, b.stages);
   });
   const hxm_gemm_config control = default_config(M, N, op);
 
@@ -319,7 +321,7 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
   };
 
   // Canary first: it says whether the device can be read at all.
-  hxm_gemm_config canary{32, 32, static_cast<int32_t>(op == HXM_I8 ? 128 : 64), 1, 1, 1};
+  hxm_gemm_config canary{32, 32, static_cast<int32_t>(op == HXM_I8 ? 128 : 64), 1, 1, 2, 1};
   std::vector<double> cs_samples;
   const int64_t cm = std::min<int64_t>(32, M), cn = std::min<int64_t>(32, N),
                 ck = std::min<int64_t>(K, 32);
@@ -342,6 +344,7 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
   int32_t ctl_idx = -1;
   for (size_t i = 0; i < cands.size(); ++i)
     if (cands[i].bm == control.bm && cands[i].bn == control.bn &&
+        cands[i].bk == control.bk && cands[i].stages == control.stages &&
         cands[i].waves_m == control.waves_m && cands[i].waves_n == control.waves_n)
       ctl_idx = static_cast<int32_t>(i);
   bool have_ref = false;
@@ -417,7 +420,7 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
       r += std::string(i ? "," : "") + "{\"tiles\":[" + std::to_string(c.bm) + "," +
            std::to_string(c.bn) + "," + std::to_string(c.bk) + "],\"waves\":[" +
            std::to_string(c.waves_m) + "," + std::to_string(c.waves_n) +
-           "],\"q20\":" + num(q20[i]) + ",\"q50\":" + num(q50[i]) + ",\"q80\":" +
+           "],\"stages\":" + std::to_string(c.stages) + ",\"q20\":" + num(q20[i]) + ",\"q50\":" + num(q50[i]) + ",\"q80\":" +
            num(q80[i]) + ",\"verified\":" + (verified[i] ? "true" : "false") +
            ",\"outcome\":\"" +
            (outcome[i] == 1 ? "takeover" : outcome[i] == 0 ? "kept" : "-") +

@@ -35,13 +35,15 @@ class HxmError(RuntimeError):
 class GemmConfig(ctypes.Structure):
     _fields_ = [("bm", ctypes.c_int32), ("bn", ctypes.c_int32), ("bk", ctypes.c_int32),
                 ("waves_m", ctypes.c_int32), ("waves_n", ctypes.c_int32),
-                ("split_k", ctypes.c_int32)]
+                ("stages", ctypes.c_int32), ("split_k", ctypes.c_int32)]
 
     def as_tuple(self):
-        return (self.bm, self.bn, self.bk, self.waves_m, self.waves_n, self.split_k)
+        return (self.bm, self.bn, self.bk, self.waves_m, self.waves_n, self.stages,
+                self.split_k)
 
     def __repr__(self):
-        return "GemmConfig(bm=%d, bn=%d, bk=%d, waves=%dx%d, split_k=%d)" % self.as_tuple()
+        return ("GemmConfig(bm=%d, bn=%d, bk=%d, waves=%dx%d, stages=%d, split_k=%d)"
+                % self.as_tuple())
 
 
 _p = ctypes.c_void_p

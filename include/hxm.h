@@ -71,9 +71,10 @@ typedef enum hxm_b_layout { HXM_B_KN = 0, HXM_B_NK = 1 } hxm_b_layout;
  * grid and the K-split).  A zeroed struct means "library default for the
  * shape" (the tuned winner when one is cached). */
 typedef struct hxm_gemm_config {
-  int32_t bm, bn, bk;    /* workgroup tile, bk in elements */
+  int32_t bm, bn, bk;       /* workgroup tile; bk = K elements per LDS stage */
   int32_t waves_m, waves_n; /* wave grid inside the workgroup */
-  int32_t split_k;       /* workgroups along K (1 = none) */
+  int32_t stages;           /* LDS stages (2 = double buffer; prefetch depth stages-1) */
+  int32_t split_k;          /* workgroups along K (1 = none) */
 } hxm_gemm_config;
 
 /* ---- status / library ------------------------------------------------- */
@@ -226,7 +227,7 @@ int32_t hxm_hmx_tile_verdict(int64_t bm, int64_t bn, int64_t bk,
                              int64_t vtcm_budget);
 
 /* The same lattice on gfx950: frontend limit -> min-rows -> the 32-wide MFMA
- * edge -> LDS budget (2 stages x (bm+bn) x bk x elem_bytes <= lds_budget)
+ * edge -> LDS budget (stages x (bm+bn) x bk x elem_bytes <= lds_budget)
  * -> a compiled kernel exists for (cfg, dtype).  elem_bytes 1 (int8) or 2. */
 int32_t hxm_gpu_tile_verdict(const hxm_gemm_config* cfg, int32_t ab_dtype,
                              int64_t lds_budget);

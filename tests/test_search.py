@@ -201,11 +201,14 @@ def test_report_is_json_ready():
 def test_gpu_lattice_admits_exactly_the_compiled_configs(dtype):
     cfgs = S.gemm_configs(dtype)
     assert cfgs
+    eb = 1 if dtype == hxm.I8 else 2
     for c in cfgs:
         assert S.gpu_tile_verdict(c, dtype) == S.REASON_OK, c
-        assert c.bk == (128 if dtype == hxm.I8 else 64)
-    assert S.gpu_tile_verdict((2, 32, 128, 1, 1, 1), dtype) == "min-rows"
-    assert S.gpu_tile_verdict((48, 32, 128, 1, 1, 1), dtype) == "frontend-block-limit"
-    assert S.gpu_tile_verdict((512, 512, 256, 2, 2, 1), dtype) == "lds-budget"
-    assert S.gpu_tile_verdict((64, 64, 128, 4, 4, 1), dtype) == "tile-alignment"
-    assert S.gpu_tile_verdict((512, 32, 32, 1, 1, 1), dtype) == "no-kernel"
+        assert c.bk * eb in (64, 128) and 2 <= c.stages <= 4
+        assert c.stages * (c.bm + c.bn) * c.bk * eb <= S.DEFAULT_LDS_BUDGET
+    assert S.gpu_tile_verdict((2, 32, 128, 1, 1, 2, 1), dtype) == "min-rows"
+    assert S.gpu_tile_verdict((48, 32, 128, 1, 1, 2, 1), dtype) == "frontend-block-limit"
+    assert S.gpu_tile_verdict((512, 512, 256, 2, 2, 2, 1), dtype) == "lds-budget"
+    assert S.gpu_tile_verdict((256, 256, 128 // eb, 2, 2, 4, 1), dtype) == "lds-budget"
+    assert S.gpu_tile_verdict((64, 64, 128, 4, 4, 2, 1), dtype) == "tile-alignment"
+    assert S.gpu_tile_verdict((512, 32, 32, 1, 1, 2, 1), dtype) == "no-kernel"

@@ -326,107 +326,144 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     }
   }
 
-  // ---- epilogue: lane l holds row m = l%32 of the block and, for register
-  // group q = v/4, the four consecutive columns 8q + 4*(l/32) + 0..3 ----
+  // ---- epilogue ----
+  // Lane l holds, for block (i, j) and register group q = v/4, row
+  // m = i*32 + l%32 of the wave tile and the four consecutive columns
+  // j*32 + 8q + 4*(l/32) + 0..3.  Every scale the epilogue needs is loaded
+  // into registers before the first store (a store to C may alias a later
+  // scale load, which would otherwise serialise each load behind the
+  // stores).  The tile is then written through LDS one 32-row block at a
+  // time: each lane stages its 4-element runs as 32-bit words (int32, or the
+  // fp32 value before its final rounding) in a padded [32][TN+4] array, and
+  // the wave reads back row-contiguous 16-byte runs so that each global
+  // store instruction writes whole rows.
+  constexpr int kPad = TN + 4;                 // staging row stride (words)
+  constexpr int kStageWords = 32 * kPad;       // one wave's 32-row block
+  constexpr int kWavesPerBuf = (NW + STAGES - 1) / STAGES;
+  static_assert(kWavesPerBuf * kStageWords * 4 <= SB, "epilogue staging must fit a stage");
   const int r32 = lane & 31, hi = lane >> 5;
+  const int mw = m0 + wm * TM, nw = n0 + wn * TN;
+
+  float rsv[FM];
+  v4f32 csv[FN][4];
+  if constexpr (EPI == kEpiDequant) {
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int m = m0 + wm * TM + i * 32 + r32;
-    if (m >= g.M) continue;
-    float rsm = 0.0f;
-    if constexpr (EPI == kEpiDequant) rsm = g.row_scale[m];
+    for (int i = 0; i < FM; ++i) {
+      const int m = mw + i * 32 + r32;
+      rsv[i] = m < g.M ? g.row_scale[m] : 0.0f;
+    }
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * TN + j * 32 + q * 8 + hi * 4;
-        if (n >= g.N) continue;
-        const int64_t off = static_cast<int64_t>(m) * g.ldc + n;
-        const bool full = g.vec_store && n + 4 <= g.N;
-        if constexpr (EPI == kEpiI32) {
-          int32_t* c = static_cast<int32_t*>(g.C) + off;
-          v4i32 r;
+        const int n = nw + j * 32 + q * 8 + hi * 4;
+        if (n + 4 <= g.N && g.vec_store) {
+          csv[j][q] = *reinterpret_cast<const v4f32*>(g.col_scale + n);
+        } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) r[e] = acc[i][j][q * 4 + e];
+          for (int e = 0; e < 4; ++e) csv[j][q][e] = n + e < g.N ? g.col_scale[n + e] : 0.0f;
+        }
+      }
+  }
+
+  wait_and_barrier<0>();  // every wave is done with the stage buffers
+  float* stg = reinterpret_cast<float*>(buf(wave % STAGES)) + (wave / STAGES) * kStageWords;
+
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    // 1. registers -> LDS (row r32, 4 consecutive columns per group)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v4f32 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (EPI == kEpiI32) {
+            // Copy the element out first: clang lowers __builtin_bit_cast of
+            // an ext-vector element expression as a read of element 0.
+            const int32_t a = acc[i][j][q * 4 + e];
+            w[e] = __builtin_bit_cast(float, a);
+          } else if constexpr (EPI == kEpiDequant) {
+            // fp32, left to right, each product rounded to fp32; the f16
+            // rounding happens after the LDS round trip, so the backend
+            // cannot fuse the last multiply into a one-rounding
+            // v_fma_mixlo_f16.
+            w[e] = (static_cast<float>(acc[i][j][q * 4 + e]) * rsv[i]) * csv[j][q][e];
+          } else {
+            w[e] = acc[i][j][q * 4 + e];
+          }
+        }
+        *reinterpret_cast<v4f32*>(stg + r32 * kPad + j * 32 + q * 8 + hi * 4) = w;
+      }
+    // 2. LDS -> global, 4 consecutive elements of one row per lane
+    constexpr int kRuns = 32 * TN / 4;          // 4-element runs in the block
+    constexpr int kRunsPerRow = TN / 4;
+#pragma unroll
+    for (int it = 0; it < kRuns / 64; ++it) {
+      const int run = it * 64 + lane;
+      const int row = run / kRunsPerRow, col = (run % kRunsPerRow) * 4;
+      const v4f32 w = *reinterpret_cast<const v4f32*>(stg + row * kPad + col);
+      const int m = mw + i * 32 + row, n = nw + col;
+      if (m >= g.M || n >= g.N) continue;
+      const int64_t off = static_cast<int64_t>(m) * g.ldc + n;
+      const bool full = g.vec_store && n + 4 <= g.N;
+      if constexpr (EPI == kEpiI32) {
+        int32_t* c = static_cast<int32_t*>(g.C) + off;
+        v4u32_t r = __builtin_bit_cast(v4u32_t, w);
+        if (full) {
+          if (g.accumulate) r += *reinterpret_cast<const v4u32_t*>(c);
+          *reinterpret_cast<v4u32_t*>(c) = r;
+        } else {
+          for (int e = 0; e < 4 && n + e < g.N; ++e)
+            c[e] = static_cast<int32_t>(g.accumulate ? static_cast<uint32_t>(c[e]) + r[e] : r[e]);
+        }
+      } else if constexpr (EPI == kEpiDequant) {
+        _Float16* c = static_cast<_Float16*>(g.C) + off;
+        v4f16_t h;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = static_cast<_Float16>(w[e]);
+        if (full)
+          *reinterpret_cast<v4f16_t*>(c) = h;
+        else
+          for (int e = 0; e < 4 && n + e < g.N; ++e) c[e] = h[e];
+      } else {
+        v4f32 r = w;
+        if (g.out_dtype == HXM_F32) {
+          float* c = static_cast<float*>(g.C) + off;
+          if (full) {
+            if (g.accumulate) r += *reinterpret_cast<const v4f32*>(c);
+            *reinterpret_cast<v4f32*>(c) = r;
+          } else {
+            for (int e = 0; e < 4 && n + e < g.N; ++e) c[e] = g.accumulate ? c[e] + r[e] : r[e];
+          }
+        } else if (g.out_dtype == HXM_F16) {
+          _Float16* c = static_cast<_Float16*>(g.C) + off;
           if (full) {
             if (g.accumulate) {
-              const v4i32 o = *reinterpret_cast<const v4i32*>(c);
-              r = __builtin_bit_cast(v4i32, __builtin_bit_cast(v4u32_t, r) +
-                                                __builtin_bit_cast(v4u32_t, o));
+              const v4f16_t o = *reinterpret_cast<const v4f16_t*>(c);
+              for (int e = 0; e < 4; ++e) r[e] += static_cast<float>(o[e]);
             }
-            *reinterpret_cast<v4i32*>(c) = r;
+            v4f16_t h;
+            for (int e = 0; e < 4; ++e) h[e] = static_cast<_Float16>(r[e]);
+            *reinterpret_cast<v4f16_t*>(c) = h;
           } else {
             for (int e = 0; e < 4 && n + e < g.N; ++e)
-              c[e] = g.accumulate ? static_cast<int32_t>(static_cast<uint32_t>(c[e]) +
-                                                         static_cast<uint32_t>(r[e]))
-                                  : r[e];
+              c[e] = static_cast<_Float16>(g.accumulate ? r[e] + static_cast<float>(c[e]) : r[e]);
           }
-        } else if constexpr (EPI == kEpiDequant) {
-          _Float16* c = static_cast<_Float16*>(g.C) + off;
-          float cs[4];
-          if (full) {
-            const v4f32 c4 = *reinterpret_cast<const v4f32*>(g.col_scale + n);
-            for (int e = 0; e < 4; ++e) cs[e] = c4[e];
-          } else {
-            for (int e = 0; e < 4; ++e) cs[e] = (n + e < g.N) ? g.col_scale[n + e] : 0.0f;
-          }
-          v4f16_t h;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            // fp32, left to right, each product rounded to fp32 and then once
-            // to f16.  The empty asm pins d as an fp32 register value: without
-            // it the backend folds the last multiply and the f16 conversion
-            // into v_fma_mixlo_f16 (a single rounding), which differs from
-            // the defined spelling in the last f16 bit for some inputs.
-            float d = (static_cast<float>(acc[i][j][q * 4 + e]) * rsm) * cs[e];
-            asm volatile("" : "+v"(d));
-            h[e] = static_cast<_Float16>(d);
-          }
-          if (full)
-            *reinterpret_cast<v4f16_t*>(c) = h;
-          else
-            for (int e = 0; e < 4 && n + e < g.N; ++e) c[e] = h[e];
         } else {
-          float r[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) r[e] = acc[i][j][q * 4 + e];
-          if (g.out_dtype == HXM_F32) {
-            float* c = static_cast<float*>(g.C) + off;
-            if (full) {
-              v4f32 o = {r[0], r[1], r[2], r[3]};
-              if (g.accumulate) o += *reinterpret_cast<const v4f32*>(c);
-              *reinterpret_cast<v4f32*>(c) = o;
-            } else {
-              for (int e = 0; e < 4 && n + e < g.N; ++e) c[e] = g.accumulate ? c[e] + r[e] : r[e];
+          __bf16* c = static_cast<__bf16*>(g.C) + off;
+          if (full) {
+            if (g.accumulate) {
+              const v4bf16_t o = *reinterpret_cast<const v4bf16_t*>(c);
+              for (int e = 0; e < 4; ++e) r[e] += static_cast<float>(o[e]);
             }
-          } else if (g.out_dtype == HXM_F16) {
-            _Float16* c = static_cast<_Float16*>(g.C) + off;
-            if (full) {
-              v4f16_t h;
-              if (g.accumulate) {
-                const v4f16_t o = *reinterpret_cast<const v4f16_t*>(c);
-                for (int e = 0; e < 4; ++e) r[e] += static_cast<float>(o[e]);
-              }
-              for (int e = 0; e < 4; ++e) h[e] = static_cast<_Float16>(r[e]);
-              *reinterpret_cast<v4f16_t*>(c) = h;
-            } else {
-              for (int e = 0; e < 4 && n + e < g.N; ++e)
-                c[e] = static_cast<_Float16>(g.accumulate ? r[e] + static_cast<float>(c[e]) : r[e]);
-            }
+            v4bf16_t h;
+            for (int e = 0; e < 4; ++e) h[e] = static_cast<__bf16>(r[e]);
+            *reinterpret_cast<v4bf16_t*>(c) = h;
           } else {
-            __bf16* c = static_cast<__bf16*>(g.C) + off;
-            if (full) {
-              v4bf16_t h;
-              if (g.accumulate) {
-                const v4bf16_t o = *reinterpret_cast<const v4bf16_t*>(c);
-                for (int e = 0; e < 4; ++e) r[e] += static_cast<float>(o[e]);
-              }
-              for (int e = 0; e < 4; ++e) h[e] = static_cast<__bf16>(r[e]);
-              *reinterpret_cast<v4bf16_t*>(c) = h;
-            } else {
-              for (int e = 0; e < 4 && n + e < g.N; ++e)
-                c[e] = static_cast<__bf16>(g.accumulate ? r[e] + static_cast<float>(c[e]) : r[e]);
-            }
+            for (int e = 0; e < 4 && n + e < g.N; ++e)
+              c[e] = static_cast<__bf16>(g.accumulate ? r[e] + static_cast<float>(c[e]) : r[e]);
           }
         }
       }

@@ -125,9 +125,12 @@ def run_f16(c):
 
 def run_gemv(c):
     torch, hxm, L = c.torch, c.hxm, c.L
-    N, K, R = 11008, 4096, 12            # 12 weight copies = 540 MB rotated
-    Ws = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=c.dev) for _ in range(R)]
+    N, K, R = 11008, 4096, 12            # 12 weight images = 540 MB rotated
+    # Resident (pre-packed) images, made once outside the timed region.
+    Ws = [c.ops.prepack_w8a16(torch.randint(-127, 128, (N, K), dtype=torch.int8,
+                                            device=c.dev)) for _ in range(R)]
     scs = [(torch.rand(N, device=c.dev) * 0.019 + 0.001).half() for _ in range(R)]
+    torch.cuda.synchronize()
     wp = [w.data_ptr() for w in Ws]
     sp = [s.data_ptr() for s in scs]
     out = {}
@@ -137,8 +140,8 @@ def run_gemv(c):
         px, py, st = xs.data_ptr(), ys.data_ptr(), c.stream
 
         def step(i, M=M, px=px, py=py):
-            hxm.check(L.hxm_gemv_w8a16(px, K, wp[i], K, sp[i], py, N, M, N, K, st),
-                      "hxm_gemv_w8a16")
+            hxm.check(L.hxm_gemv_w8a16(px, K, wp[i], K, hxm.W_PACKED, sp[i], py, N, M, N, K,
+                                       st), "hxm_gemv_w8a16")
         ms, _ = c.time_ms(step, 240, 24, rotate=R)
         nbytes = N * K + N * 2 + M * K * 2 + M * N * 2
         gbs = nbytes / (ms * 1e-3) / 1e9

@@ -58,47 +58,101 @@ __device__ __forceinline__ v8f16 i8x8_to_f16(uint32_t lo, uint32_t hi) {
   return r;
 }
 
-template <int KW, int UNROLL>
+// Bytes of the packed (resident) weight image for [N, K]: one 1 KiB block
+// per (16-channel group, 64-wide K slab), zero-padded at the edges.
+inline int64_t packed_bytes(int64_t N, int64_t K) {
+  return ((N + 15) / 16) * ((K + 63) / 64) * 1024;
+}
+
+// Packs W [N, K] (ldw) into the image: block (g, s), lane l holds the 16
+// bytes W[16g + l%16][64s + 16*(l/16) ... +16] at byte 16*l of the block, the
+// exact order in which one wave instruction of the GEMV consumes them.
+__global__ __launch_bounds__(256) void pack_w8a16_kernel(const int8_t* __restrict__ W,
+                                                         int64_t ldw, int N, int K,
+                                                         int8_t* __restrict__ out,
+                                                         int64_t nblocks) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // one lane-chunk
+  const int64_t blk = t >> 6;
+  if (blk >= nblocks) return;
+  const int lane = static_cast<int>(t & 63);
+  const int slabs = (K + 63) / 64;
+  const int64_t g = blk / slabs;
+  const int s = static_cast<int>(blk % slabs);
+  const int64_t n = g * 16 + (lane & 15);
+  const int k = s * 64 + (lane >> 4) * 16;
+  v4i32 v = {0, 0, 0, 0};
+  if (n < N && k < K) v = *reinterpret_cast<const v4i32*>(W + n * ldw + k);
+  *reinterpret_cast<v4i32*>(out + blk * 1024 + lane * 16) = v;
+}
+
+// One workgroup = 16 output channels x all of K; its KW waves split each
+// K chunk of KW*SPW slabs, SPW contiguous slabs per wave.  Per chunk, every W
+// load of the wave (SPW x 16 bytes per lane) is issued first; the x rows of
+// the chunk are then staged once in LDS (row stride padded by 16 bytes so
+// the 16 rows a ds_read_b128 touches land on distinct banks) while those
+// loads are in flight.  PACKED reads the resident image (1 KiB contiguous
+// per wave instruction); otherwise W is the plain [N, K] matrix (16 rows x
+// 64 bytes per instruction).
+template <int KW, int SPW, bool PACKED, int MR>
 __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
+  constexpr int kChunkSlabs = KW * SPW;
+  constexpr int kChunkK = kChunkSlabs * 64;
+  constexpr int kRowBytes = kChunkK * 2 + 16;   // padded x row in LDS
+  __shared__ __attribute__((aligned(16))) uint8_t xs[MR * kRowBytes];  // MR >= rows
   __shared__ v4f32 part[KW][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * 16;
   const int m_base = blockIdx.y * 16;
-  const int r16 = lane & 15;   // W row (channel) for A; x row (m) for B
-  const int kq = lane >> 4;    // which 16-byte quarter of the 64-wide slab
+  const int rows = min(MR, g.M - m_base);       // x rows of this M tile (host: <= MR)
+  const int r16 = lane & 15;                    // W row (channel) for A; x row for B
+  const int kq = lane >> 4;                     // 16-byte quarter of the 64-wide slab
   const int n = n0 + r16;
-  const int m = m_base + r16;
   const bool n_ok = n < g.N;
-  const bool m_ok = m < g.M;
-  const int8_t* wrow = g.W + static_cast<int64_t>(n_ok ? n : 0) * g.ldw;
-  const _Float16* xrow = g.x + static_cast<int64_t>(m_ok ? m : 0) * g.ldx;
   const int slabs = (g.K + 63) / 64;
+  const int8_t* wrow = g.W + static_cast<int64_t>(n_ok ? n : 0) * g.ldw;
+  const int8_t* wblk = g.W + static_cast<int64_t>(blockIdx.x) * slabs * 1024 + lane * 16;
 
   v4f32 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int s0 = wave; s0 < slabs; s0 += KW * UNROLL) {
-    v4i32 w[UNROLL];
-    v4i32 xa[UNROLL], xb[UNROLL];
+  for (int c0 = 0; c0 < slabs; c0 += kChunkSlabs) {
+    const int s_first = c0 + wave * SPW;
+    v4i32 w[SPW];
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int s = s0 + u * KW;
-      const int k = s * 64 + kq * 16;
-      const bool k_ok = s < slabs && k < g.K;
-      w[u] = (n_ok && k_ok) ? *reinterpret_cast<const v4i32*>(wrow + k) : v4i32{0, 0, 0, 0};
-      if (m_ok && k_ok) {
-        xa[u] = *reinterpret_cast<const v4i32*>(xrow + k);
-        xb[u] = *reinterpret_cast<const v4i32*>(xrow + k + 8);
+    for (int u = 0; u < SPW; ++u) {
+      const int s = s_first + u;
+      if constexpr (PACKED) {
+        w[u] = s < slabs ? *reinterpret_cast<const v4i32*>(wblk + static_cast<int64_t>(s) * 1024)
+                         : v4i32{0, 0, 0, 0};
       } else {
-        xa[u] = v4i32{0, 0, 0, 0};
-        xb[u] = v4i32{0, 0, 0, 0};
+        const int k = s * 64 + kq * 16;
+        w[u] = (n_ok && k < g.K) ? *reinterpret_cast<const v4i32*>(wrow + k) : v4i32{0, 0, 0, 0};
       }
     }
+    // Stage x[m_base .. m_base+rows, c0*64 .. +kChunkK) in LDS, zero past K.
+    __syncthreads();  // the previous chunk's reads are done
+    const int kc0 = c0 * 64;
+    const int kvalid = min(kChunkK, g.K - kc0);
+    for (int idx = threadIdx.x; idx < rows * (kChunkK / 8); idx += KW * 64) {
+      const int r = idx / (kChunkK / 8), k8 = (idx % (kChunkK / 8)) * 8;
+      v4i32 v = {0, 0, 0, 0};
+      if (k8 < kvalid)
+        v = *reinterpret_cast<const v4i32*>(g.x + static_cast<int64_t>(m_base + r) * g.ldx + kc0 + k8);
+      *reinterpret_cast<v4i32*>(xs + r * kRowBytes + k8 * 2) = v;
+    }
+    __syncthreads();
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
+    for (int u = 0; u < SPW; ++u) {
+      const int kl = (wave * SPW + u) * 64 + kq * 16;   // K offset inside the chunk
+      v4i32 xa = {0, 0, 0, 0}, xb = {0, 0, 0, 0};
+      if (r16 < rows) {
+        const uint8_t* px = xs + r16 * kRowBytes + kl * 2;
+        xa = *reinterpret_cast<const v4i32*>(px);
+        xb = *reinterpret_cast<const v4i32*>(px + 16);
+      }
       const v8f16 wa = i8x8_to_f16(static_cast<uint32_t>(w[u][0]), static_cast<uint32_t>(w[u][1]));
       const v8f16 wb = i8x8_to_f16(static_cast<uint32_t>(w[u][2]), static_cast<uint32_t>(w[u][3]));
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, __builtin_bit_cast(v8f16, xa[u]), acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, __builtin_bit_cast(v8f16, xb[u]), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, __builtin_bit_cast(v8f16, xa), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, __builtin_bit_cast(v8f16, xb), acc, 0, 0, 0);
     }
   }
 
@@ -125,19 +179,53 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
 
 using namespace hxm;
 
-extern "C" hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W,
-                                     int64_t ldw, const void* w_scale, void* y,
-                                     int64_t ldy, int64_t M, int64_t N, int64_t K,
-                                     void* stream) {
+extern "C" {
+
+int64_t hxm_w8a16_packed_bytes(int64_t N, int64_t K) {
+  if (N < 0 || K < 0) return -1;
+  return packed_bytes(N, K);
+}
+
+hxm_status hxm_prepack_w8a16(const int8_t* W, int64_t ldw, int64_t N, int64_t K,
+                             int8_t* out, int64_t out_bytes, void* stream) {
+  if (N < 0 || K < 0 || ldw < K)
+    return fail(HXM_INVALID_ARG, "invalid-argument: prepack_w8a16 extents/ldw");
+  if (out_bytes < packed_bytes(N, K))
+    return fail(HXM_INVALID_ARG, "invalid-argument: prepack_w8a16 needs %lld output bytes",
+                (long long)packed_bytes(N, K));
+  if (N > 0 && K > 0 && (!W || !out))
+    return fail(HXM_INVALID_ARG, "invalid-argument: prepack_w8a16 null pointer");
+  if (K % 16 || ldw % 16 || (K > 0 && (!aligned16(W) || !aligned16(out))))
+    return fail(HXM_UNSUPPORTED_SHAPE,
+                "tile-alignment: prepack_w8a16 needs K and ldw multiples of 16 and 16-byte "
+                "aligned buffers");
+  if (N > INT32_MAX - 16 || K > INT32_MAX - 64)
+    return fail(HXM_UNSUPPORTED_SHAPE, "tile-alignment: prepack_w8a16 extent too large");
+  hxm_status st = require_device(nullptr);
+  if (st != HXM_OK) return st;
+  if (N == 0 || K == 0) return ok();
+  const int64_t nblocks = packed_bytes(N, K) / 1024;
+  const int64_t threads = nblocks * 64;
+  pack_w8a16_kernel<<<static_cast<unsigned>((threads + 255) / 256), 256, 0, as_stream(stream)>>>(
+      W, ldw, static_cast<int>(N), static_cast<int>(K), out, nblocks);
+  return check_launch("prepack_w8a16");
+}
+
+hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W, int64_t ldw,
+                          int32_t w_layout, const void* w_scale, void* y, int64_t ldy,
+                          int64_t M, int64_t N, int64_t K, void* stream) {
   if (M < 0 || N < 0 || K < 0)
     return fail(HXM_INVALID_ARG, "invalid-argument: gemv_w8a16 negative extent");
+  if (w_layout != HXM_W_NK && w_layout != HXM_W_PACKED)
+    return fail(HXM_INVALID_ARG, "invalid-argument: gemv_w8a16 w_layout=%d", w_layout);
   if (M > 0 && N > 0 && (!y || !w_scale || (K > 0 && (!x || !W))))
     return fail(HXM_INVALID_ARG, "invalid-argument: gemv_w8a16 null operand");
-  if (ldx < K || ldw < K || ldy < N)
+  if (ldx < K || ldy < N || (w_layout == HXM_W_NK && ldw < K))
     return fail(HXM_INVALID_ARG, "invalid-argument: gemv_w8a16 leading dimension too small");
-  if (K % 16 || ldx % 8 || ldw % 16 || (K > 0 && (!aligned16(x) || !aligned16(W))))
+  if (K % 16 || ldx % 8 || (w_layout == HXM_W_NK && ldw % 16) ||
+      (K > 0 && (!aligned16(x) || !aligned16(W))))
     return fail(HXM_UNSUPPORTED_SHAPE,
-                "tile-alignment: gemv_w8a16 needs K and ldw multiples of 16, ldx of 8, "
+                "tile-alignment: gemv_w8a16 needs K (and ldw) multiples of 16, ldx of 8, "
                 "16-byte aligned x and W (K=%lld)",
                 (long long)K);
   if (N > INT32_MAX - 16 || K > INT32_MAX - 64 || M > 65535LL * 16)
@@ -149,6 +237,21 @@ extern "C" hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W
              static_cast<const _Float16*>(w_scale), static_cast<_Float16*>(y), ldy,
              static_cast<int>(M), static_cast<int>(N), static_cast<int>(K)};
   const dim3 grid(static_cast<unsigned>((N + 15) / 16), static_cast<unsigned>((M + 15) / 16));
-  gemv_w8a16_kernel<4, 4><<<grid, 256, 0, as_stream(stream)>>>(g);
+  // x rows staged per workgroup: a single small M tile needs less LDS, which
+  // keeps more workgroups resident per CU.
+  hipStream_t s = as_stream(stream);
+  const bool pk = w_layout == HXM_W_PACKED;
+  if (M <= 1) {
+    if (pk) gemv_w8a16_kernel<8, 4, true, 1><<<grid, 512, 0, s>>>(g);
+    else gemv_w8a16_kernel<8, 4, false, 1><<<grid, 512, 0, s>>>(g);
+  } else if (M <= 4) {
+    if (pk) gemv_w8a16_kernel<8, 4, true, 4><<<grid, 512, 0, s>>>(g);
+    else gemv_w8a16_kernel<8, 4, false, 4><<<grid, 512, 0, s>>>(g);
+  } else {
+    if (pk) gemv_w8a16_kernel<8, 4, true, 16><<<grid, 512, 0, s>>>(g);
+    else gemv_w8a16_kernel<8, 4, false, 16><<<grid, 512, 0, s>>>(g);
+  }
   return check_launch("gemv_w8a16");
 }
+
+}  // extern "C"

@@ -21,6 +21,7 @@ HXM_NO_DEVICE = 6
 
 F16, BF16, F32, I8, I32 = 1, 2, 3, 4, 5
 B_KN, B_NK = 0, 1
+W_NK, W_PACKED = 0, 1
 
 
 class HxmError(RuntimeError):
@@ -68,7 +69,9 @@ SIGNATURES = {
     "hxm_gemm_i8_dequant": (_st, [_p, _i64, _p, _i64, _i32, _p, _p, _p, _i64, _i64, _i64,
                                   _i64, _cfgp, _p]),
     "hxm_prepack_weight": (_st, [_p, _i64, _p, _i64, _i64, _i64, _i32, _p]),
-    "hxm_gemv_w8a16": (_st, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p]),
+    "hxm_gemv_w8a16": (_st, [_p, _i64, _p, _i64, _i32, _p, _p, _i64, _i64, _i64, _i64, _p]),
+    "hxm_w8a16_packed_bytes": (_i64, [_i64, _i64]),
+    "hxm_prepack_w8a16": (_st, [_p, _i64, _i64, _i64, _p, _i64, _p]),
     "hxm_softmax_rows": (_st, [_p, _i64, _p, _i64, _i64, _i64, _i32, _p]),
     "hxm_rmsnorm_rows": (_st, [_p, _i64, _p, _p, _i64, _i64, _i64, _f32, _i32, _p]),
     "hxm_layernorm_rows": (_st, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i64, _i64, _f32, _i32,

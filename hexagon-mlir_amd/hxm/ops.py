@@ -14,7 +14,7 @@ from typing import Optional, Sequence
 
 import torch
 
-from ._lib import (B_KN, B_NK, BF16, F16, F32, I8, I32, GemmConfig, check, lib)
+from ._lib import (B_KN, B_NK, BF16, F16, F32, I8, I32, W_NK, W_PACKED, GemmConfig, check, lib)
 
 _DT = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32,
        torch.int8: I8, torch.int32: I32}
@@ -143,20 +143,44 @@ def prepack_weight(B: torch.Tensor, out: Optional[torch.Tensor] = None, *,
     return out
 
 
+def prepack_w8a16(W: torch.Tensor, *, stream=None) -> torch.Tensor:
+    """int8 W [N, K] -> the resident GEMV image (flat int8 tensor)."""
+    _mat(W, "W")
+    N, K = W.shape
+    out = torch.empty(int(lib.hxm_w8a16_packed_bytes(N, K)), dtype=torch.int8, device=W.device)
+    st = lib.hxm_prepack_w8a16(W.data_ptr(), _ld(W), N, K, out.data_ptr(), out.numel(),
+                               _stream(stream))
+    check(st, "hxm_prepack_w8a16")
+    return out
+
+
 def gemv_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor,
-               out: Optional[torch.Tensor] = None, *, stream=None) -> torch.Tensor:
-    """y = f16((x @ W.T in fp32) * scale) for int8 W [N, K], f16 x [M, K]."""
-    _mat(x, "x"), _mat(W, "W")
+               out: Optional[torch.Tensor] = None, *, N: Optional[int] = None,
+               stream=None) -> torch.Tensor:
+    """y = f16((x @ W.T in fp32) * scale) for int8 W [N, K] and f16 x [M, K].
+
+    W may also be the flat image from :func:`prepack_w8a16`; then N is taken
+    from ``scale`` (or passed explicitly)."""
+    _mat(x, "x")
     M, K = x.shape
-    N = W.shape[0]
-    if W.shape[1] != K:
-        raise ValueError("W must be [N, K]")
+    packed = W.dim() == 1
+    if packed:
+        N = scale.numel() if N is None else N
+        if W.numel() < lib.hxm_w8a16_packed_bytes(N, K):
+            raise ValueError("packed image too small for [N, K]")
+        ldw = K
+    else:
+        _mat(W, "W")
+        N = W.shape[0]
+        if W.shape[1] != K:
+            raise ValueError("W must be [N, K]")
+        ldw = _ld(W)
     if out is None:
         out = torch.empty((M, N), dtype=torch.float16, device=x.device)
     _mat(out, "out")
-    st = lib.hxm_gemv_w8a16(x.data_ptr(), _ld(x), W.data_ptr(), _ld(W),
-                            scale.contiguous().data_ptr(), out.data_ptr(), _ld(out), M, N, K,
-                            _stream(stream))
+    st = lib.hxm_gemv_w8a16(x.data_ptr(), _ld(x), W.data_ptr(), ldw,
+                            W_PACKED if packed else W_NK, scale.contiguous().data_ptr(),
+                            out.data_ptr(), _ld(out), M, N, K, _stream(stream))
     check(st, "hxm_gemv_w8a16")
     return out
 

@@ -159,18 +159,39 @@ hxm_status hxm_prepack_weight(const void* B, int64_t ldb, void* out,
                               int64_t ldo, int64_t K, int64_t N, int32_t dtype,
                               void* stream);
 
+/* Layout of the int8 weight of the W8A16 GEMV.
+ *   HXM_W_NK:     W is [N,K] row-major (output-channel major, K contiguous),
+ *                 ldw >= K.
+ *   HXM_W_PACKED: W is the resident image made once by hxm_prepack_w8a16
+ *                 (ldw ignored): 1 KiB blocks per (16 channels, 64 K), in the
+ *                 order one wave instruction consumes them -- the GEMV's
+ *                 counterpart of the reference's weight pre-pack
+ *                 (backend/hmx_weight_prepack.py:171-183). */
+typedef enum hxm_w_layout { HXM_W_NK = 0, HXM_W_PACKED = 1 } hxm_w_layout;
+
 /* W8A16 weight-resident skinny GEMM / GEMV (the
  * reference's int8 matmul on the HVX path, ScheduleMatmulForHVXPass.cpp:44-80):
  *   y[m,n] = rne_f16( (sum_k f32(x[m,k]) * f32(W[n,k])) * f32(w_scale[n]) )
- * x fp16 [M,K] (ldx >= K); W int8 [N,K] (ldw >= K, output-channel major);
- * w_scale fp16 [N]; y fp16 [M,N] (ldy >= N).  fp32 accumulation in any
- * order (tolerance rtol 1e-2 / atol 1e-3 against the fp32 restatement).
- * Any M >= 1: M <= 16 streams W once through the GEMV kernel, larger M
- * runs the W8A16 MFMA GEMM.  K, ldx, ldw multiples of 16. */
+ * x fp16 [M,K] (ldx >= K); W int8 in layout w_layout; w_scale fp16 [N];
+ * y fp16 [M,N] (ldy >= N).  fp32 accumulation in any order (tolerance
+ * rtol 1e-2 / atol 1e-3 against the fp32 restatement).  W is streamed once
+ * per 16 rows of M.  K multiple of 16, ldx multiple of 8, ldw (HXM_W_NK)
+ * multiple of 16, x and W 16-byte aligned. */
 hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W,
-                          int64_t ldw, const void* w_scale, void* y,
-                          int64_t ldy, int64_t M, int64_t N, int64_t K,
+                          int64_t ldw, int32_t w_layout, const void* w_scale,
+                          void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                           void* stream);
+
+/* Bytes of the packed W8A16 image for [N,K] (-1 for negative extents). */
+int64_t hxm_w8a16_packed_bytes(int64_t N, int64_t K);
+
+/* Builds the packed W8A16 image from W [N,K] (ldw) into out (at least
+ * hxm_w8a16_packed_bytes(N,K) bytes, 16-byte aligned, caller-owned).
+ * Run once per weight (the weight-resident contract: WeightResidentPass.cpp
+ * :10-53, HexagonCAPI.h:52-53). */
+hxm_status hxm_prepack_w8a16(const int8_t* W, int64_t ldw, int64_t N,
+                             int64_t K, int8_t* out, int64_t out_bytes,
+                             void* stream);
 
 /* ---- row reductions (test/python/triton/test_softmax.py:41-69,
  *      test_rms_norm.py:34-60, test_layer_norm.py:39-79, as lowered by

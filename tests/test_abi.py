@@ -67,7 +67,7 @@ def test_refusals_happen_before_launch():
     st = L.hxm_softmax_rows(16, 8, 16, 8, 2, 8, hxm.I8, None)
     assert st == _lib.HXM_UNSUPPORTED_DTYPE
     # gemv: K not a multiple of 16
-    st = L.hxm_gemv_w8a16(16, 24, 16, 24, 16, 16, 8, 1, 8, 24, None)
+    st = L.hxm_gemv_w8a16(16, 24, 16, 24, hxm.W_NK, 16, 16, 8, 1, 8, 24, None)
     assert st == _lib.HXM_UNSUPPORTED_SHAPE
     # an unknown B layout
     st = L.hxm_gemm_i8(16, 32, 16, 32, 7, 16, 8, 8, 8, 32, 0, None, None)

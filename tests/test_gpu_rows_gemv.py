@@ -109,30 +109,57 @@ def test_rows_strided_inplace_and_edge_values(dev):
 
 
 @pytest.mark.parametrize("M", [1, 4, 16])
-def test_gemv_baseline_shape(dev, M):
-    """N=11008, K=4096, M in {1,4,16}."""
-    print(f"gemv M={M}", flush=True)
+@pytest.mark.parametrize("packed", [True, False])
+def test_gemv_baseline_shape(dev, M, packed):
+    """N=11008, K=4096, M in {1,4,16}; resident image and
+    plain [N, K] weights."""
+    print(f"gemv M={M} packed={packed}", flush=True)
     N, K = 11008, 4096
     g = torch.Generator().manual_seed(M)
     x = torch.randn(M, K, generator=g).half()
     W = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
     sc = (torch.rand(N, generator=g) * 0.019 + 0.001).half()
-    y = ops.gemv_w8a16(x.to(dev), W.to(dev), sc.to(dev)).cpu()
+    Wd = W.to(dev)
+    Wd = ops.prepack_w8a16(Wd) if packed else Wd
+    y = ops.gemv_w8a16(x.to(dev), Wd, sc.to(dev)).cpu()
     ref = orc.f16_bits_to_f32(orc.gemv_w8a16(host_bits(x, "f16"), W.numpy(),
                                              host_bits(sc, "f16")))
     np.testing.assert_allclose(y.float().numpy(), ref, rtol=1e-2, atol=1e-3)
 
 
-@pytest.mark.parametrize("M,N,K", [(3, 100, 272), (33, 64, 512), (1, 17, 16), (16, 48, 256)])
-def test_gemv_ragged(dev, M, N, K):
+@pytest.mark.parametrize("M,N,K", [(3, 100, 272), (33, 64, 512), (1, 17, 16), (16, 48, 256),
+                                   (5, 40, 2064), (20, 31, 4160)])
+@pytest.mark.parametrize("packed", [True, False])
+def test_gemv_ragged(dev, M, N, K, packed):
     g = torch.Generator().manual_seed(M * N + K)
     x = torch.randn(M, K, generator=g).half()
     W = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
     sc = (torch.rand(N, generator=g) * 0.019 + 0.001).half()
-    y = ops.gemv_w8a16(x.to(dev), W.to(dev), sc.to(dev)).cpu()
+    Wd = W.to(dev)
+    Wd = ops.prepack_w8a16(Wd) if packed else Wd
+    y = ops.gemv_w8a16(x.to(dev), Wd, sc.to(dev)).cpu()
     ref = orc.f16_bits_to_f32(orc.gemv_w8a16(host_bits(x, "f16"), W.numpy(),
                                              host_bits(sc, "f16")))
     np.testing.assert_allclose(y.float().numpy(), ref, rtol=1e-2, atol=1e-3)
+
+
+def test_w8a16_image_layout(dev):
+    """The image is a pure permutation of W with zero padding: block (g, s),
+    lane l holds W[16g + l%16][64s + 16(l//16) ... +16]."""
+    N, K = 37, 208
+    W = torch.randint(-127, 128, (N, K), dtype=torch.int8)
+    img = ops.prepack_w8a16(W.to(dev)).cpu().numpy()
+    ng, ns = (N + 15) // 16, (K + 63) // 64
+    assert img.size == ng * ns * 1024
+    exp = np.zeros((ng, ns, 64, 16), dtype=np.int8)
+    Wn = W.numpy()
+    for gi in range(ng):
+        for si in range(ns):
+            for lane in range(64):
+                n, k = gi * 16 + lane % 16, si * 64 + (lane // 16) * 16
+                if n < N and k < K:
+                    exp[gi, si, lane] = Wn[n, k:k + 16]
+    assert np.array_equal(img.reshape(ng, ns, 64, 16), exp)
 
 
 def test_gemv_golden_and_exact_small_ints(dev, golden):

@@ -188,6 +188,20 @@ def run_copy(c):
                             "GB/s": 2 * (1 << 28) / (ms * 1e-3) / 1e9}}
 
 
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel from its committed rocprofv3
+    summary (FETCH_SIZE and WRITE_SIZE passes, scaled by the copy
+    calibration); None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "int8_gemm_4096_dequant.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(A, Bp, seconds):
     from oracle import oracle as orc
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
@@ -271,7 +285,9 @@ def main() -> int:
                                "fp32 scales dequant to fp16; B resident [N,K] image",
                    "M": 4096, "N": 4096, "K": 4096, "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS,
-                     "unit": "TFLOP/s", "frac": tops / PEAK_INT8_TOPS, "traffic": None,
+                     "unit": "TFLOP/s", "frac": tops / PEAK_INT8_TOPS,
+                     "traffic": measured_traffic(),
+                     "traffic_source": "profiles/int8_gemm_4096_dequant.md",
                      "kernel": "gemm_kernel<int8_t,...,kEpiDequant>",
                      "work_per_launch": head["ops_per_launch"], "avg_launch_us": head["us"]},
         "cpu_baseline": cpu,

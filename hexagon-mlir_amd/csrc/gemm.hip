@@ -545,7 +545,7 @@ const KernelEntry* find_kernel(const hxm_gemm_config& c, int32_t dt) {
 // CU a workgroup, else the 64x64 tile.
 hxm_gemm_config default_config(int64_t M, int64_t N, int32_t dt) {
   static const int order[][4] = {  // bm, bn, bk bytes, stages
-      {256, 256, 64, 4}, {256, 128, 64, 4}, {128, 128, 64, 4}};
+      {256, 256, 128, 2}, {256, 128, 64, 4}, {128, 128, 128, 2}};
   for (auto& o : order) {
     const int64_t tiles = ((M + o[0] - 1) / o[0]) * ((N + o[1] - 1) / o[1]);
     if (tiles >= 256) {

@@ -120,12 +120,17 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
 #pragma unroll
     for (int u = 0; u < SPW; ++u) {
       const int s = s_first + u;
+      // Weights are streamed exactly once: nontemporal loads keep them from
+      // displacing x and other reusable lines in the caches.
       if constexpr (PACKED) {
-        w[u] = s < slabs ? *reinterpret_cast<const v4i32*>(wblk + static_cast<int64_t>(s) * 1024)
+        w[u] = s < slabs ? __builtin_nontemporal_load(reinterpret_cast<const v4i32*>(
+                               wblk + static_cast<int64_t>(s) * 1024))
                          : v4i32{0, 0, 0, 0};
       } else {
         const int k = s * 64 + kq * 16;
-        w[u] = (n_ok && k < g.K) ? *reinterpret_cast<const v4i32*>(wrow + k) : v4i32{0, 0, 0, 0};
+        w[u] = (n_ok && k < g.K)
+                   ? __builtin_nontemporal_load(reinterpret_cast<const v4i32*>(wrow + k))
+                   : v4i32{0, 0, 0, 0};
       }
     }
     // Stage x[m_base .. m_base+rows, c0*64 .. +kChunkK) in LDS, zero past K.
@@ -241,12 +246,14 @@ hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W, int64_t l
   // keeps more workgroups resident per CU.
   hipStream_t s = as_stream(stream);
   const bool pk = w_layout == HXM_W_PACKED;
+  // Small M: a 4096-wide K chunk (x rows fit LDS), so at K <= 4096 each wave
+  // issues all its weight loads at once and makes one memory round trip.
   if (M <= 1) {
-    if (pk) gemv_w8a16_kernel<8, 4, true, 1><<<grid, 512, 0, s>>>(g);
-    else gemv_w8a16_kernel<8, 4, false, 1><<<grid, 512, 0, s>>>(g);
+    if (pk) gemv_w8a16_kernel<8, 8, true, 1><<<grid, 512, 0, s>>>(g);
+    else gemv_w8a16_kernel<8, 8, false, 1><<<grid, 512, 0, s>>>(g);
   } else if (M <= 4) {
-    if (pk) gemv_w8a16_kernel<8, 4, true, 4><<<grid, 512, 0, s>>>(g);
-    else gemv_w8a16_kernel<8, 4, false, 4><<<grid, 512, 0, s>>>(g);
+    if (pk) gemv_w8a16_kernel<8, 8, true, 4><<<grid, 512, 0, s>>>(g);
+    else gemv_w8a16_kernel<8, 8, false, 4><<<grid, 512, 0, s>>>(g);
   } else {
     if (pk) gemv_w8a16_kernel<8, 4, true, 16><<<grid, 512, 0, s>>>(g);
     else gemv_w8a16_kernel<8, 4, false, 16><<<grid, 512, 0, s>>>(g);

@@ -37,6 +37,7 @@
 //     (optionally += C, one rounding), or the int8 dequant
 //     f16(((float)acc * row_scale) * col_scale).
 #include <cstring>
+#include <type_traits>
 #include <mutex>
 #include <vector>
 
@@ -71,6 +72,7 @@ struct GemmArgs {
   int accumulate;
   int out_dtype;  // HXM_I32, HXM_F16, HXM_BF16, HXM_F32
   int vec_store;  // C rows allow 4-element vector stores
+  int vec8_store; // C rows allow 8-element (16-byte f16) vector stores
   const float* row_scale;
   const float* col_scale;
   int group_m;  // tile-rows per group in the XCD walk
@@ -163,34 +165,58 @@ struct StageLoad {
   static constexpr int L = ROWS / RPI / NW;         // instructions per wave per stage
   static_assert(L >= 1 && (ROWS / RPI) % NW == 0, "tile rows must split over waves");
   uint32_t off[L];
-  int chunk_byte[L];
+
+  // LDS row and source chunk (16-byte unit within the row's BKB bytes) that
+  // lane fills in instruction i.
+  __device__ static __forceinline__ int row_of(int i, int wave, int lane) {
+    return (i * NW + wave) * RPI + lane / CH;
+  }
+  __device__ static __forceinline__ int chunk_of(int i, int wave, int lane) {
+    return (lane % CH) ^ swz<BKB>(row_of(i, wave, lane));
+  }
 
   __device__ __forceinline__ void init(int64_t ld_bytes, int rows_left, int wave, int lane) {
 #pragma unroll
     for (int i = 0; i < L; ++i) {
-      const int q = i * NW + wave;
-      const int row = q * RPI + lane / CH;
-      const int chunk = (lane % CH) ^ swz<BKB>(row);
-      chunk_byte[i] = chunk * 16;
-      off[i] = row < rows_left ? static_cast<uint32_t>(row * ld_bytes + chunk * 16) : kOob;
+      const int row = row_of(i, wave, lane);
+      off[i] = row < rows_left ? static_cast<uint32_t>(row * ld_bytes + chunk_of(i, wave, lane) * 16)
+                               : kOob;
     }
   }
 
-  // A whole stage inside K.
-  __device__ __forceinline__ void issue(v4i32 r, uint8_t* lds, int wave, int kb0) const {
-#pragma unroll
-    for (int i = 0; i < L; ++i) dma16(lds + (i * NW + wave) * 1024, r, off[i], kb0);
-  }
-  // The stage that straddles the end of K: chunks at or past K read zero.
-  __device__ __forceinline__ void issue_tail(v4i32 r, uint8_t* lds, int wave, int kb0,
-                                             int K_bytes) const {
-#pragma unroll
-    for (int i = 0; i < L; ++i) {
-      const uint32_t o = kb0 + chunk_byte[i] < K_bytes ? off[i] : kOob;
-      dma16(lds + (i * NW + wave) * 1024, r, o, kb0);
-    }
+  // Instruction i of a stage at K byte kb0; 16-byte chunks at or past
+  // K_bytes read as zero (only the last stage can straddle the end of K).
+  // The chunk is recomputed (a few VALU operations under the MFMAs) rather
+  // than kept in a register per instruction.
+  template <int I>
+  __device__ __forceinline__ void issue_one(v4i32 r, uint8_t* lds, int wave, int lane, int kb0,
+                                            int K_bytes) const {
+    const uint32_t o = kb0 + chunk_of(I, wave, lane) * 16 < K_bytes ? off[I] : kOob;
+    dma16(lds + (I * NW + wave) * 1024, r, o, kb0);
   }
 };
+
+// One LDS-DMA of 4 bytes per lane: rsrc at voffset into LDS at lds + lane*4.
+__device__ __forceinline__ void dma4(float* lds, v4i32 rsrc, uint32_t voffset) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)lds)));
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "buffer_load_dword %1, %2, 0 offen lds"
+      :
+      : "s"(m0), "v"(voffset), "s"(rsrc)
+      : "memory", "m0");
+}
+
+// Calls f(integral_constant<int, I>) for I = B .. E-1, so every index inside
+// f is a compile-time constant (register arrays stay in registers).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 
 template <int BKB>
 __device__ __forceinline__ v4i32 lds_frag(const uint8_t* lds, int row, int chunk) {
@@ -204,20 +230,26 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 blocks per wave
   constexpr int KS = BKB / 32;               // MFMA k-steps per stage
   constexpr int SB = (BM + BN) * BKB;        // bytes per stage
-  constexpr int P = STAGES - 1;              // prefetch distance
+  constexpr int NF = FM * FN;                // MFMA slots per k-step
+  constexpr int NR = FM + FN;                // fragment reads per k-step
+  constexpr int HALF = NF / 2;               // barrier slot of the last k-step
+  constexpr int PB = (KS - 1) * NF + HALF;   // slots of a stage before its barrier
   static_assert(FM >= 1 && FN >= 1, "wave tile must hold a 32x32 block");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
+  static_assert(KS % 2 == 0, "fragment double buffer assumes an even k-step count");
   using acc_t = typename Mfma<T>::acc_t;
   using LA = StageLoad<BM, BKB, NW>;
   using LB = StageLoad<BN, BKB, NW>;
   constexpr int LPW = LA::L + LB::L;  // DMA instructions per wave per stage
-  static_assert(LPW * (P - 1) <= 63, "vmcnt range");
+  // Dequant scales: rows [0, QR*64), columns [QR*64, (QR+QC)*64) floats.
+  constexpr int QR = (BM + 63) / 64, QC = (BN + 63) / 64;
 
   // One __shared__ object per stage (see the header comment).
   __shared__ __attribute__((aligned(1024))) uint8_t s0[SB];
   __shared__ __attribute__((aligned(1024))) uint8_t s1[SB];
   __shared__ __attribute__((aligned(1024))) uint8_t s2[STAGES > 2 ? SB : 1024];
   __shared__ __attribute__((aligned(1024))) uint8_t s3[STAGES > 3 ? SB : 1024];
+  __shared__ __attribute__((aligned(16))) float ssc[EPI == kEpiDequant ? (QR + QC) * 64 : 4];
   auto buf = [&](int u) -> uint8_t* {
     return u == 0 ? s0 : u == 1 ? s1 : u == 2 ? s2 : s3;
   };
@@ -248,6 +280,18 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   la.init(g.lda_bytes, g.M - m0, wave, lane);
   lb.init(g.ldb_bytes, g.N - n0, wave, lane);
 
+  // The tile's dequant scales go to LDS by DMA ahead of the first stage, so
+  // they arrive under the prologue and cost the epilogue one LDS read each.
+  // Scales of rows / columns outside C read as zero.
+  if constexpr (EPI == kEpiDequant) {
+    const v4i32 rr = operand_rsrc(reinterpret_cast<const uint8_t*>(g.row_scale), 4, m0, g.M);
+    const v4i32 rc = operand_rsrc(reinterpret_cast<const uint8_t*>(g.col_scale), 4, n0, g.N);
+    for (int q = wave; q < QR + QC; q += NW) {
+      if (q < QR) dma4(ssc + q * 64, rr, (q * 64 + lane) * 4);
+      else dma4(ssc + q * 64, rc, ((q - QR) * 64 + lane) * 4);
+    }
+  }
+
   acc_t acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -256,117 +300,139 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
 
   const int KT = (g.K_bytes + BKB - 1) / BKB;
   const int K_bytes = g.K_bytes;
-  auto issue = [&](int kt, uint8_t* dst) {
-    const int kb0 = kt * BKB;
-    if (kb0 + BKB <= K_bytes) {
-      la.issue(ra, dst, wave, kb0);
-      lb.issue(rb, dst + BM * BKB, wave, kb0);
-    } else {
-      la.issue_tail(ra, dst, wave, kb0, K_bytes);
-      lb.issue_tail(rb, dst + BM * BKB, wave, kb0, K_bytes);
-    }
+
+  // DMA instruction D (A's first, then B's) of the stage at K byte kb0.
+  auto dma = [&](auto D, uint8_t* dst, int kb0) {
+    constexpr int d = decltype(D)::value;
+    if constexpr (d < LA::L) la.template issue_one<d>(ra, dst, wave, lane, kb0, K_bytes);
+    else lb.template issue_one<d - LA::L>(rb, dst + BM * BKB, wave, lane, kb0, K_bytes);
+  };
+  auto issue_stage = [&](int kt, uint8_t* dst) {
+    static_for<0, LPW>([&](auto D) { dma(D, dst, kt * BKB); });
   };
 
-  auto compute = [&](const uint8_t* stage) {
-    const uint8_t* pa = stage + (wm * TM) * BKB;
-    const uint8_t* pb = stage + (BM + wn * TN) * BKB;
-    v4i32 af[2][FM], bf[2][FN];
-    const int r32 = lane & 31, hi = lane >> 5;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) af[0][i] = lds_frag<BKB>(pa, i * 32 + r32, hi);
-#pragma unroll
-    for (int j = 0; j < FN; ++j) bf[0][j] = lds_frag<BKB>(pb, j * 32 + r32, hi);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int cur = ks & 1;
-      if (ks + 1 < KS) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-          af[cur ^ 1][i] = lds_frag<BKB>(pa, i * 32 + r32, (ks + 1) * 2 + hi);
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          bf[cur ^ 1][j] = lds_frag<BKB>(pb, j * 32 + r32, (ks + 1) * 2 + hi);
-      }
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = Mfma<T>::run(bf[cur][j], af[cur][i], acc[i][j]);
-    }
+  // Fragments of the k-step being multiplied ([ks & 1]) and of the next one.
+  // Read R of a k-step: A block 0, the FN B blocks, then A blocks 1..FM-1 --
+  // the order the MFMA slots (i, j) = (s / FN, s % FN) first need them.
+  v4i32 af[2][FM], bf[2][FN];
+  const int r32 = lane & 31, hi = lane >> 5;
+  auto read = [&](auto R, int dstb, const uint8_t* stage, int ks) {
+    constexpr int r = decltype(R)::value;
+    constexpr bool is_b = r >= 1 && r <= FN;
+    constexpr int idx = r == 0 ? 0 : is_b ? r - 1 : r - FN;
+    if constexpr (is_b)
+      bf[dstb][idx] = lds_frag<BKB>(stage + (BM + wn * TN) * BKB, idx * 32 + r32, ks * 2 + hi);
+    else
+      af[dstb][idx] = lds_frag<BKB>(stage + (wm * TM) * BKB, idx * 32 + r32, ks * 2 + hi);
   };
 
-  // Prologue: stages 0 .. P-1.
-#pragma unroll
-  for (int p = 0; p < P; ++p)
-    if (p < KT) issue(p, buf(p));
+  // Every stage slot issues its DMAs, also past the end of K: a stage at or
+  // past K_bytes reads zeros (see issue_one) into a buffer no later stage
+  // uses, so the number of stages in flight is the same at every wait and
+  // the instruction stream has no branches for the compiler's waitcnt
+  // analysis to merge.
 
-  // Main loop, unrolled by STAGES so every buffer choice is static.
-  for (int kt0 = 0; kt0 < KT; kt0 += STAGES) {
-#pragma unroll
-    for (int u = 0; u < STAGES; ++u) {
-      const int kt = kt0 + u;
-      if (kt < KT) {
-        // Stages issued after kt that may stay in flight.
-        const int ahead = min(kt + P, KT) - kt - 1;
-        // Afterwards stage kt is visible to all waves and the buffer of
-        // stage kt-1 is free for the next DMA.
-        if constexpr (P >= 3) {
-          if (ahead >= 2) wait_and_barrier<(P >= 3 ? 2 * LPW : 0)>();
-          else if (ahead == 1) wait_and_barrier<LPW>();
-          else wait_and_barrier<0>();
-        } else if constexpr (P == 2) {
-          if (ahead >= 1) wait_and_barrier<LPW>();
-          else wait_and_barrier<0>();
-        } else {
-          wait_and_barrier<0>();
-        }
-        if (kt + P < KT) issue(kt + P, buf((u + P) % STAGES));
-        compute(buf(u));
-      }
+  // DMA schedule.  Stage j goes to buffer j % STAGES, which is free from the
+  // barrier of iteration j-STAGES on (every read of stage j-STAGES precedes
+  // that barrier) and must have landed at the barrier of iteration j-1.
+  // Instruction d of stage j issues at position dv(d) of iteration
+  // j-STAGES+1, counted from its first slot; a negative position is a slot
+  // after the barrier of the iteration before.  With two stages the
+  // instructions are packed into the first two thirds of the window so the
+  // last ones land before the wait; with more stages they are spread over
+  // the whole window.
+  constexpr int SLOTS = KS * NF;             // MFMA slots per stage
+  constexpr int POST = SLOTS - PB;           // slots after the barrier
+  constexpr int DW = STAGES == 2 ? (2 * SLOTS) / 3 : SLOTS;
+  static_assert(((LPW - 1) * DW) / LPW - POST < PB, "DMA window ends before the barrier");
+  constexpr int NEG = [] {                   // instructions issued a stage early
+    int n = 0;
+    for (int d = 0; d < LPW; ++d) n += (d * DW) / LPW - POST < 0;
+    return n;
+  }();
+  static_assert((STAGES - 2) * LPW + NEG <= 63, "vmcnt range");
+
+  // One stage.  Its KS*NF MFMA slots run in a fixed order (a scheduling
+  // barrier closes each slot).  Spread over the slots: the DMA instructions
+  // (above), and the fragment reads of k-step ks+1.  At slot HALF of the
+  // last k-step the wave waits for stage kt+1 (stages kt+2 .. kt+STAGES-1 may
+  // stay in flight); the barrier also tells it that every wave is done
+  // reading stage kt, whose buffer the early DMAs of stage kt+STAGES then
+  // refill.  It then reads stage kt+1's first fragments under the remaining
+  // MFMAs.
+  auto stage = [&](auto U, int kt) {
+    constexpr int u = decltype(U)::value;
+    const uint8_t* cur = buf(u);
+    const uint8_t* nxt = buf((u + 1) % STAGES);
+    uint8_t* dbuf = buf((u + STAGES - 1) % STAGES);  // stage kt+STAGES-1
+    uint8_t* ebuf = buf(u);                          // stage kt+STAGES (early part)
+    const int kbd = (kt + STAGES - 1) * BKB;
+    static_for<0, KS>([&](auto KSI) {
+      constexpr int ks = decltype(KSI)::value;
+      constexpr int cb = ks & 1;
+      static_for<0, NF>([&](auto SI) {
+        constexpr int sl = decltype(SI)::value;
+        constexpr int slot = ks * NF + sl;
+        if constexpr (ks == KS - 1 && sl == HALF) wait_and_barrier<(STAGES - 2) * LPW>();
+        static_for<0, LPW>([&](auto D) {
+          constexpr int v = (decltype(D)::value * DW) / LPW - POST;
+          if constexpr (v >= 0 && v == slot) dma(D, dbuf, kbd);
+          if constexpr (v < 0 && SLOTS + v == slot) dma(D, ebuf, kbd + BKB);
+        });
+        static_for<0, NR>([&](auto R) {
+          constexpr int r = decltype(R)::value;
+          if constexpr (ks < KS - 1) {
+            if constexpr ((r * NF) / NR == sl) read(R, cb ^ 1, cur, ks + 1);
+          } else {
+            if constexpr (HALF + (r * (NF - HALF)) / NR == sl) read(R, cb ^ 1, nxt, 0);
+          }
+        });
+        constexpr int i = sl / FN, j = sl % FN;
+        acc[i][j] = Mfma<T>::run(bf[cb][j], af[cb][i], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    });
+  };
+
+  if (KT > 0) {
+    // Prologue: stages 0 .. STAGES-2, the early part of stage STAGES-1, then
+    // the first k-step's fragments.
+    static_for<0, STAGES - 1>([&](auto Pi) {
+      issue_stage(decltype(Pi)::value, buf(decltype(Pi)::value));
+    });
+    static_for<0, LPW>([&](auto D) {
+      if constexpr ((decltype(D)::value * DW) / LPW - POST < 0)
+        dma(D, buf(STAGES - 1), (STAGES - 1) * BKB);
+    });
+    wait_and_barrier<(STAGES - 2) * LPW + NEG>();
+    static_for<0, NR>([&](auto R) { read(R, 0, buf(0), 0); });
+
+    // Main loop, unrolled by STAGES so every buffer choice is static.
+    for (int kt0 = 0; kt0 < KT; kt0 += STAGES) {
+      static_for<0, STAGES>([&](auto U) {
+        const int kt = kt0 + decltype(U)::value;
+        if (kt < KT) stage(U, kt);
+      });
     }
   }
 
   // ---- epilogue ----
   // Lane l holds, for block (i, j) and register group q = v/4, row
   // m = i*32 + l%32 of the wave tile and the four consecutive columns
-  // j*32 + 8q + 4*(l/32) + 0..3.  Every scale the epilogue needs is loaded
-  // into registers before the first store (a store to C may alias a later
-  // scale load, which would otherwise serialise each load behind the
-  // stores).  The tile is then written through LDS one 32-row block at a
-  // time: each lane stages its 4-element runs as 32-bit words (int32, or the
-  // fp32 value before its final rounding) in a padded [32][TN+4] array, and
-  // the wave reads back row-contiguous 16-byte runs so that each global
-  // store instruction writes whole rows.
+  // j*32 + 8q + 4*(l/32) + 0..3.  The tile is written through LDS one 32-row
+  // block at a time: each lane stages its 4-element runs as 32-bit words
+  // (int32, or the fp32 accumulator) in a padded [32][TN+4] array, and the
+  // wave reads back row-contiguous 16-byte runs, applies the output
+  // conversion (the dequant scales come from LDS) and stores whole rows.
+  // Keeping the register-to-LDS copy a plain move keeps the accumulators in
+  // AGPRs through the epilogue.
   constexpr int kPad = TN + 4;                 // staging row stride (words)
   constexpr int kStageWords = 32 * kPad;       // one wave's 32-row block
   constexpr int kWavesPerBuf = (NW + STAGES - 1) / STAGES;
   static_assert(kWavesPerBuf * kStageWords * 4 <= SB, "epilogue staging must fit a stage");
-  const int r32 = lane & 31, hi = lane >> 5;
   const int mw = m0 + wm * TM, nw = n0 + wn * TN;
 
-  float rsv[FM];
-  v4f32 csv[FN][4];
-  if constexpr (EPI == kEpiDequant) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int m = mw + i * 32 + r32;
-      rsv[i] = m < g.M ? g.row_scale[m] : 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = nw + j * 32 + q * 8 + hi * 4;
-        if (n + 4 <= g.N && g.vec_store) {
-          csv[j][q] = *reinterpret_cast<const v4f32*>(g.col_scale + n);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) csv[j][q][e] = n + e < g.N ? g.col_scale[n + e] : 0.0f;
-        }
-      }
-  }
-
-  wait_and_barrier<0>();  // every wave is done with the stage buffers
+  wait_and_barrier<0>();  // stage buffers free; scales landed and visible
   float* stg = reinterpret_cast<float*>(buf(wave % STAGES)) + (wave / STAGES) * kStageWords;
 
 #pragma unroll
@@ -379,24 +445,57 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         v4f32 w;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          if constexpr (EPI == kEpiI32) {
-            // Copy the element out first: clang lowers __builtin_bit_cast of
-            // an ext-vector element expression as a read of element 0.
+          if constexpr (EPI == kEpiFloat) {
+            w[e] = acc[i][j][q * 4 + e];
+          } else {
+            // int32 bits.  Copy the element out first: clang lowers
+            // __builtin_bit_cast of an ext-vector element expression as a
+            // read of element 0.
             const int32_t a = acc[i][j][q * 4 + e];
             w[e] = __builtin_bit_cast(float, a);
-          } else if constexpr (EPI == kEpiDequant) {
-            // fp32, left to right, each product rounded to fp32; the f16
-            // rounding happens after the LDS round trip, so the backend
-            // cannot fuse the last multiply into a one-rounding
-            // v_fma_mixlo_f16.
-            w[e] = (static_cast<float>(acc[i][j][q * 4 + e]) * rsv[i]) * csv[j][q][e];
-          } else {
-            w[e] = acc[i][j][q * 4 + e];
           }
         }
         *reinterpret_cast<v4f32*>(stg + r32 * kPad + j * 32 + q * 8 + hi * 4) = w;
       }
-    // 2. LDS -> global, 4 consecutive elements of one row per lane
+    // 2. LDS -> global.  The dequant output takes 8 consecutive f16 of one
+    // row per lane (16-byte stores); the other outputs 4 elements per lane.
+    if constexpr (EPI == kEpiDequant) {
+      constexpr int kRuns8 = 32 * TN / 8, kRunsPerRow8 = TN / 8;
+      static_assert(kRuns8 % 64 == 0, "8-element runs must fill the wave");
+#pragma unroll
+      for (int it = 0; it < kRuns8 / 64; ++it) {
+        const int run = it * 64 + lane;
+        const int row = run / kRunsPerRow8, col = (run % kRunsPerRow8) * 8;
+        const v4f32 w0 = *reinterpret_cast<const v4f32*>(stg + row * kPad + col);
+        const v4f32 w1 = *reinterpret_cast<const v4f32*>(stg + row * kPad + col + 4);
+        const int m = mw + i * 32 + row, n = nw + col;
+        if (m >= g.M || n >= g.N) continue;
+        // fp32, left to right, each product rounded to fp32, then one
+        // rounding to f16.  The empty asm pins the fp32 product in a
+        // register so the backend cannot fuse the last multiply and the
+        // conversion into a single-rounding v_fma_mixlo_f16.
+        const float rs = ssc[wm * TM + i * 32 + row];
+        const float* csp = ssc + QR * 64 + wn * TN + col;
+        const v4f32 c0 = *reinterpret_cast<const v4f32*>(csp);
+        const v4f32 c1 = *reinterpret_cast<const v4f32*>(csp + 4);
+        v8f16 h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float we = e < 4 ? w0[e] : w1[e - 4];
+          const float ce = e < 4 ? c0[e] : c1[e - 4];
+          float p = (static_cast<float>(__builtin_bit_cast(int32_t, we)) * rs) * ce;
+          asm volatile("" : "+v"(p));
+          h[e] = static_cast<_Float16>(p);
+        }
+        _Float16* c = static_cast<_Float16*>(g.C) + static_cast<int64_t>(m) * g.ldc + n;
+        if (g.vec8_store && n + 8 <= g.N) {
+          __builtin_nontemporal_store(h, reinterpret_cast<v8f16*>(c));  // C is not re-read here
+        } else {
+          for (int e = 0; e < 8 && n + e < g.N; ++e) c[e] = h[e];
+        }
+      }
+      continue;
+    }
     constexpr int kRuns = 32 * TN / 4;          // 4-element runs in the block
     constexpr int kRunsPerRow = TN / 4;
 #pragma unroll
@@ -412,21 +511,16 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         int32_t* c = static_cast<int32_t*>(g.C) + off;
         v4u32_t r = __builtin_bit_cast(v4u32_t, w);
         if (full) {
-          if (g.accumulate) r += *reinterpret_cast<const v4u32_t*>(c);
-          *reinterpret_cast<v4u32_t*>(c) = r;
+          if (g.accumulate) {
+            r += *reinterpret_cast<const v4u32_t*>(c);
+            *reinterpret_cast<v4u32_t*>(c) = r;
+          } else {
+            __builtin_nontemporal_store(r, reinterpret_cast<v4u32_t*>(c));
+          }
         } else {
           for (int e = 0; e < 4 && n + e < g.N; ++e)
             c[e] = static_cast<int32_t>(g.accumulate ? static_cast<uint32_t>(c[e]) + r[e] : r[e]);
         }
-      } else if constexpr (EPI == kEpiDequant) {
-        _Float16* c = static_cast<_Float16*>(g.C) + off;
-        v4f16_t h;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = static_cast<_Float16>(w[e]);
-        if (full)
-          *reinterpret_cast<v4f16_t*>(c) = h;
-        else
-          for (int e = 0; e < 4 && n + e < g.N; ++e) c[e] = h[e];
       } else {
         v4f32 r = w;
         if (g.out_dtype == HXM_F32) {
@@ -544,9 +638,12 @@ const KernelEntry* find_kernel(const hxm_gemm_config& c, int32_t dt) {
 // the first entry of this preference list whose tile count still gives every
 // CU a workgroup, else the 64x64 tile.
 hxm_gemm_config default_config(int64_t M, int64_t N, int32_t dt) {
-  static const int order[][4] = {  // bm, bn, bk bytes, stages
-      {256, 256, 128, 2}, {256, 128, 64, 4}, {128, 128, 128, 2}};
-  for (auto& o : order) {
+  // bm, bn, bk bytes, stages.  The two-stage 256x256 tile is the int8
+  // choice; with f16/bf16 operands that kernel spills registers, so the
+  // four-stage tile leads there.
+  static const int order_i8[][4] = {{256, 256, 128, 2}, {256, 256, 64, 4}, {128, 128, 128, 2}};
+  static const int order_f16[][4] = {{256, 256, 64, 4}, {256, 128, 128, 3}, {128, 128, 128, 2}};
+  for (auto& o : (dt == HXM_I8 ? order_i8 : order_f16)) {
     const int64_t tiles = ((M + o[0] - 1) / o[0]) * ((N + o[1] - 1) / o[1]);
     if (tiles >= 256) {
       hxm_gemm_config c{o[0], o[1], o[2] / elem_bytes(dt), 0, 0, o[3], 1};
@@ -688,6 +785,7 @@ hxm_status run_gemm(int32_t op, int32_t ab_dtype, int epi, const void* A,
   {
     const int64_t ob = dtype_bytes(out_dtype);
     g.vec_store = (reinterpret_cast<uintptr_t>(C) % (4 * ob) == 0) && ((ldc * ob) % (4 * ob) == 0);
+    g.vec8_store = (reinterpret_cast<uintptr_t>(C) % 16 == 0) && ((ldc * ob) % 16 == 0);
   }
   if ((st = launch_gemm(*e, ab_dtype, epi, g, stream)) != HXM_OK) return st;
   return ok();

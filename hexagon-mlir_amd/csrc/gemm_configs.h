@@ -4,8 +4,11 @@
 // this list; the LDS footprint is STAGES * (BM + BN) * BKB bytes.
 #pragma once
 
+// A build may predefine the list (for example to compile one configuration).
+#ifndef HXM_GEMM_CONFIG_LIST
 #define HXM_GEMM_CONFIG_LIST(X)                                                 \
   X(256, 256, 128, 2, 2, 2), X(256, 256, 64, 4, 2, 2),                           \
       X(256, 128, 128, 3, 2, 2), X(256, 128, 64, 4, 2, 2),                       \
       X(128, 256, 64, 4, 2, 2), X(128, 128, 128, 2, 2, 2),                       \
       X(128, 128, 64, 4, 2, 2), X(64, 64, 128, 2, 2, 2), X(32, 32, 128, 2, 1, 1)
+#endif

@@ -103,6 +103,7 @@ def run_int8(c, A, Bp, rs, cs, out_i32=False):
             hxm.check(L.hxm_gemm_i8_dequant(a, K, b, K, hxm.B_NK, r, s, o, N, M, N, K, None,
                                             st), "hxm_gemm_i8_dequant")
     ms, wall = c.time_ms(step, c.args.steps, c.args.warmup)
+    c.last_step = step
     ops_per = 2.0 * M * N * K
     return {"us": ms * 1e3, "wall_us": wall * 1e3, "TOPS": ops_per / (ms * 1e-3) / 1e12,
             "ops_per_launch": ops_per}
@@ -226,6 +227,47 @@ def cpu_baseline(A, Bp, seconds):
                       f"threads), median of 3 runs of {t:.3f} s"}
 
 
+def sclk_under_load(c, fn, seconds=1.0):
+    """Shader clock (MHz) while `fn` runs back to back for about `seconds`:
+    rocm-smi is sampled from a host thread during the loop.  Returns the
+    median sample and the raw samples, or None when rocm-smi gives nothing."""
+    import re
+    import subprocess
+    import threading
+    samples, stop = [], threading.Event()
+
+    def sample():
+        while not stop.is_set():
+            try:
+                out = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True,
+                                     text=True, timeout=5).stdout
+            except (OSError, subprocess.SubprocessError):
+                return
+            m = re.search(r"sclk clock level:\s*\d+:\s*\(?(\d+)\s*Mhz", out, re.I)
+            if m:
+                samples.append(int(m.group(1)))
+            time.sleep(0.05)
+
+    fn(0)
+    c.torch.cuda.synchronize()
+    th = threading.Thread(target=sample, daemon=True)
+    th.start()
+    t0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(200):
+            fn(i)
+            i += 1
+        c.torch.cuda.synchronize()
+    stop.set()
+    th.join(timeout=10)
+    if not samples:
+        return None
+    steady = samples[len(samples) // 2:]  # the first samples still see the ramp from idle
+    return {"median_mhz": statistics.median(steady), "samples_mhz": samples,
+            "source": "rocm-smi --showclocks sampled while the headline GEMM runs back to back"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -256,6 +298,8 @@ def main() -> int:
     A, Bp, rs, cs = int8_operands(c)
     head = run_int8(c, A, Bp, rs, cs)
     log("int8 gemm+dequant 4096^3:", json.dumps(head))
+    clk = sclk_under_load(c, c.last_step)
+    log("sclk under load:", json.dumps(clk))
     extra = {}
     if not args.no_extra:
         extra["int8_gemm_i32_out_4096"] = run_int8(c, A, Bp, rs, cs, out_i32=True)
@@ -289,7 +333,10 @@ def main() -> int:
                      "traffic": measured_traffic(),
                      "traffic_source": "profiles/int8_gemm_4096_dequant.md",
                      "kernel": "gemm_kernel<int8_t,...,kEpiDequant>",
-                     "work_per_launch": head["ops_per_launch"], "avg_launch_us": head["us"]},
+                     "work_per_launch": head["ops_per_launch"], "avg_launch_us": head["us"],
+                     "sclk_under_load": clk,
+                     "frac_at_measured_sclk": (tops / (PEAK_INT8_TOPS * clk["median_mhz"] / 2400.0)
+                                               if clk else None)},
         "cpu_baseline": cpu,
         "extra": extra,
     }

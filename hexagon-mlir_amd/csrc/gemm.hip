@@ -60,8 +60,15 @@ __device__ __forceinline__ int swz(int row) {
 enum Epilogue {
   kEpiI32 = 0,      // int32 out (accumulate flag honoured)
   kEpiDequant = 1,  // int8: f16(((float)acc * rs[m]) * cs[n])
-  kEpiFloat = 2     // f16/bf16: fp32 acc -> out dtype (accumulate honoured)
+  kEpiFloat = 2,    // f16/bf16: fp32 acc -> out dtype (accumulate honoured)
+  kEpiW8 = 3,       // f16 A x int8 B: f16(acc * cs[n])
+  kEpiSwiglu = 4    // f16 A x int8 gate/up image: f16(silu(g * sg) * (u * su))
 };
+
+// The int8-weight epilogues take B as int8 [N, K] converted to f16 in
+// registers (the W8A16 GEMM of the SwiGLU FFN).
+constexpr bool b_is_int8(int epi) { return epi == kEpiW8 || epi == kEpiSwiglu; }
+constexpr int32_t kOpW8 = HXM_OP_W8A16, kOpSwiglu = HXM_OP_W8A16_SWIGLU;  // tuning-cache keys
 
 struct GemmArgs {
   const uint8_t* A;  // [M, K] row-major, lda_bytes
@@ -76,6 +83,7 @@ struct GemmArgs {
   const float* row_scale;
   const float* col_scale;
   int group_m;  // tile-rows per group in the XCD walk
+  int n_out;    // kEpiSwiglu: output columns (gate/up channel count)
 };
 
 template <typename T>
@@ -229,7 +237,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   constexpr int TM = BM / WM, TN = BN / WN;  // wave sub-tile
   constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 blocks per wave
   constexpr int KS = BKB / 32;               // MFMA k-steps per stage
-  constexpr int SB = (BM + BN) * BKB;        // bytes per stage
+  constexpr bool BQ = b_is_int8(EPI);        // B int8, converted to f16 in registers
+  constexpr int BKB_B = BQ ? BKB / 2 : BKB;  // B bytes per LDS row
+  constexpr int SB = BM * BKB + BN * BKB_B;  // bytes per stage
   constexpr int NF = FM * FN;                // MFMA slots per k-step
   constexpr int NR = FM + FN;                // fragment reads per k-step
   constexpr int HALF = NF / 2;               // barrier slot of the last k-step
@@ -239,17 +249,20 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   static_assert(KS % 2 == 0, "fragment double buffer assumes an even k-step count");
   using acc_t = typename Mfma<T>::acc_t;
   using LA = StageLoad<BM, BKB, NW>;
-  using LB = StageLoad<BN, BKB, NW>;
+  using LB = StageLoad<BN, BKB_B, NW>;
   constexpr int LPW = LA::L + LB::L;  // DMA instructions per wave per stage
-  // Dequant scales: rows [0, QR*64), columns [QR*64, (QR+QC)*64) floats.
-  constexpr int QR = (BM + 63) / 64, QC = (BN + 63) / 64;
+  static_assert(!BQ || std::is_same<T, _Float16>::value, "int8 B pairs with f16 A");
+  static_assert(EPI != kEpiSwiglu || TN == 128, "SwiGLU image interleaves 64-channel blocks");
+  // Epilogue scales in LDS: rows [0, QR*64), columns [QR*64, (QR+QC)*64) floats.
+  constexpr int QR = EPI == kEpiDequant ? (BM + 63) / 64 : 0;
+  constexpr int QC = EPI == kEpiDequant || BQ ? (BN + 63) / 64 : 0;
 
   // One __shared__ object per stage (see the header comment).
   __shared__ __attribute__((aligned(1024))) uint8_t s0[SB];
   __shared__ __attribute__((aligned(1024))) uint8_t s1[SB];
   __shared__ __attribute__((aligned(1024))) uint8_t s2[STAGES > 2 ? SB : 1024];
   __shared__ __attribute__((aligned(1024))) uint8_t s3[STAGES > 3 ? SB : 1024];
-  __shared__ __attribute__((aligned(16))) float ssc[EPI == kEpiDequant ? (QR + QC) * 64 : 4];
+  __shared__ __attribute__((aligned(16))) float ssc[QR + QC > 0 ? (QR + QC) * 64 : 4];
   auto buf = [&](int u) -> uint8_t* {
     return u == 0 ? s0 : u == 1 ? s1 : u == 2 ? s2 : s3;
   };
@@ -280,11 +293,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   la.init(g.lda_bytes, g.M - m0, wave, lane);
   lb.init(g.ldb_bytes, g.N - n0, wave, lane);
 
-  // The tile's dequant scales go to LDS by DMA ahead of the first stage, so
+  // The tile's epilogue scales go to LDS by DMA ahead of the first stage, so
   // they arrive under the prologue and cost the epilogue one LDS read each.
   // Scales of rows / columns outside C read as zero.
-  if constexpr (EPI == kEpiDequant) {
-    const v4i32 rr = operand_rsrc(reinterpret_cast<const uint8_t*>(g.row_scale), 4, m0, g.M);
+  if constexpr (QR + QC > 0) {
+    const v4i32 rr = QR ? operand_rsrc(reinterpret_cast<const uint8_t*>(g.row_scale), 4, m0, g.M)
+                        : v4i32{};
     const v4i32 rc = operand_rsrc(reinterpret_cast<const uint8_t*>(g.col_scale), 4, n0, g.N);
     for (int q = wave; q < QR + QC; q += NW) {
       if (q < QR) dma4(ssc + q * 64, rr, (q * 64 + lane) * 4);
@@ -299,13 +313,18 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     for (int j = 0; j < FN; ++j) acc[i][j] = acc_t{};
 
   const int KT = (g.K_bytes + BKB - 1) / BKB;
-  const int K_bytes = g.K_bytes;
+  const int K_bytes = g.K_bytes;                    // of A
+  const int K_bytes_B = BQ ? K_bytes / 2 : K_bytes;  // of B
 
-  // DMA instruction D (A's first, then B's) of the stage at K byte kb0.
+  // DMA instruction D (A's first, then B's) of the stage at A byte kb0.
   auto dma = [&](auto D, uint8_t* dst, int kb0) {
     constexpr int d = decltype(D)::value;
-    if constexpr (d < LA::L) la.template issue_one<d>(ra, dst, wave, lane, kb0, K_bytes);
-    else lb.template issue_one<d - LA::L>(rb, dst + BM * BKB, wave, lane, kb0, K_bytes);
+    if constexpr (d < LA::L) {
+      la.template issue_one<d>(ra, dst, wave, lane, kb0, K_bytes);
+    } else {
+      const int kb0_b = BQ ? kb0 / 2 : kb0;
+      lb.template issue_one<d - LA::L>(rb, dst + BM * BKB, wave, lane, kb0_b, K_bytes_B);
+    }
   };
   auto issue_stage = [&](int kt, uint8_t* dst) {
     static_for<0, LPW>([&](auto D) { dma(D, dst, kt * BKB); });
@@ -314,16 +333,28 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   // Fragments of the k-step being multiplied ([ks & 1]) and of the next one.
   // Read R of a k-step: A block 0, the FN B blocks, then A blocks 1..FM-1 --
   // the order the MFMA slots (i, j) = (s / FN, s % FN) first need them.
+  // With an int8 B the read brings the lane's 8 bytes (K range
+  // [16ks + 8hi, +8) of its row) into braw, and cvt_b turns them into the f16
+  // fragment one MFMA slot before its first use.
   v4i32 af[2][FM], bf[2][FN];
+  uint2 braw[2][BQ ? FN : 1];
   const int r32 = lane & 31, hi = lane >> 5;
   auto read = [&](auto R, int dstb, const uint8_t* stage, int ks) {
     constexpr int r = decltype(R)::value;
     constexpr bool is_b = r >= 1 && r <= FN;
     constexpr int idx = r == 0 ? 0 : is_b ? r - 1 : r - FN;
-    if constexpr (is_b)
+    if constexpr (is_b && BQ) {
+      const int row = idx * 32 + r32;
+      braw[dstb][idx] = *reinterpret_cast<const uint2*>(
+          stage + BM * BKB + (wn * TN + row) * BKB_B + ((ks ^ swz<BKB_B>(row)) << 4) + hi * 8);
+    } else if constexpr (is_b) {
       bf[dstb][idx] = lds_frag<BKB>(stage + (BM + wn * TN) * BKB, idx * 32 + r32, ks * 2 + hi);
-    else
+    } else {
       af[dstb][idx] = lds_frag<BKB>(stage + (wm * TM) * BKB, idx * 32 + r32, ks * 2 + hi);
+    }
+  };
+  auto cvt_b = [&](int b, int j) {
+    if constexpr (BQ) bf[b][j] = __builtin_bit_cast(v4i32, i8x8_to_f16(braw[b][j].x, braw[b][j].y));
   };
 
   // Every stage slot issues its DMAs, also past the end of K: a stage at or
@@ -389,6 +420,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         });
         constexpr int i = sl / FN, j = sl % FN;
         acc[i][j] = Mfma<T>::run(bf[cb][j], af[cb][i], acc[i][j]);
+        // int8 B: convert fragment sl+1 of this k-step under this MFMA, and
+        // fragment 0 of the next k-step under the last one.
+        if constexpr (BQ && sl + 1 < FN) cvt_b(cb, sl + 1);
+        if constexpr (BQ && sl == NF - 1) cvt_b(cb ^ 1, 0);
         __builtin_amdgcn_sched_barrier(0);
       });
     });
@@ -406,6 +441,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     });
     wait_and_barrier<(STAGES - 2) * LPW + NEG>();
     static_for<0, NR>([&](auto R) { read(R, 0, buf(0), 0); });
+    cvt_b(0, 0);
 
     // Main loop, unrolled by STAGES so every buffer choice is static.
     for (int kt0 = 0; kt0 < KT; kt0 += STAGES) {
@@ -445,7 +481,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         v4f32 w;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          if constexpr (EPI == kEpiFloat) {
+          if constexpr (EPI == kEpiFloat || BQ) {
             w[e] = acc[i][j][q * 4 + e];
           } else {
             // int32 bits.  Copy the element out first: clang lowers
@@ -492,6 +528,76 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
           __builtin_nontemporal_store(h, reinterpret_cast<v8f16*>(c));  // C is not re-read here
         } else {
           for (int e = 0; e < 8 && n + e < g.N; ++e) c[e] = h[e];
+        }
+      }
+      continue;
+    }
+    if constexpr (EPI == kEpiW8) {
+      // f16(acc * cs[n]): the fp32 product, then one rounding to f16.
+      constexpr int kRuns8 = 32 * TN / 8, kRunsPerRow8 = TN / 8;
+#pragma unroll
+      for (int it = 0; it < kRuns8 / 64; ++it) {
+        const int run = it * 64 + lane;
+        const int row = run / kRunsPerRow8, col = (run % kRunsPerRow8) * 8;
+        const v4f32 w0 = *reinterpret_cast<const v4f32*>(stg + row * kPad + col);
+        const v4f32 w1 = *reinterpret_cast<const v4f32*>(stg + row * kPad + col + 4);
+        const int m = mw + i * 32 + row, n = nw + col;
+        if (m >= g.M || n >= g.N) continue;
+        const float* csp = ssc + QR * 64 + wn * TN + col;
+        const v4f32 c0 = *reinterpret_cast<const v4f32*>(csp);
+        const v4f32 c1 = *reinterpret_cast<const v4f32*>(csp + 4);
+        v8f16 h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float p = (e < 4 ? w0[e] : w1[e - 4]) * (e < 4 ? c0[e] : c1[e - 4]);
+          asm volatile("" : "+v"(p));
+          h[e] = static_cast<_Float16>(p);
+        }
+        _Float16* c = static_cast<_Float16*>(g.C) + static_cast<int64_t>(m) * g.ldc + n;
+        if (g.vec8_store && n + 8 <= g.N) {
+          __builtin_nontemporal_store(h, reinterpret_cast<v8f16*>(c));
+        } else {
+          for (int e = 0; e < 8 && n + e < g.N; ++e) c[e] = h[e];
+        }
+      }
+      continue;
+    }
+    if constexpr (EPI == kEpiSwiglu) {
+      // The wave's 128 image rows are 64 gate channels then the same 64 up
+      // channels: output column o = (n0 + wn*128)/2 + col takes the gate
+      // value from staged column col and the up value from column 64 + col.
+      // h = f16(silu(g) * u) with g = acc_g * sg, u = acc_u * su in fp32 and
+      // silu(g) = g / (1 + exp(-g)).
+      constexpr int kRunsS = 32 * 64 / 8, kRunsPerRowS = 64 / 8;
+#pragma unroll
+      for (int it = 0; it < kRunsS / 64; ++it) {
+        const int run = it * 64 + lane;
+        const int row = run / kRunsPerRowS, col = (run % kRunsPerRowS) * 8;
+        const float* sp = stg + row * kPad + col;
+        const v4f32 g0 = *reinterpret_cast<const v4f32*>(sp);
+        const v4f32 g1 = *reinterpret_cast<const v4f32*>(sp + 4);
+        const v4f32 u0 = *reinterpret_cast<const v4f32*>(sp + 64);
+        const v4f32 u1 = *reinterpret_cast<const v4f32*>(sp + 68);
+        const int m = mw + i * 32 + row, o = nw / 2 + col;
+        if (m >= g.M || o >= g.n_out) continue;
+        const float* csp = ssc + QR * 64 + wn * TN + col;
+        const v4f32 sg0 = *reinterpret_cast<const v4f32*>(csp);
+        const v4f32 sg1 = *reinterpret_cast<const v4f32*>(csp + 4);
+        const v4f32 su0 = *reinterpret_cast<const v4f32*>(csp + 64);
+        const v4f32 su1 = *reinterpret_cast<const v4f32*>(csp + 68);
+        v8f16 h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float gv = (e < 4 ? g0[e] : g1[e - 4]) * (e < 4 ? sg0[e] : sg1[e - 4]);
+          const float uv = (e < 4 ? u0[e] : u1[e - 4]) * (e < 4 ? su0[e] : su1[e - 4]);
+          const float ex = __builtin_amdgcn_exp2f(-gv * 1.4426950408889634f);
+          h[e] = static_cast<_Float16>(gv * __builtin_amdgcn_rcpf(1.0f + ex) * uv);
+        }
+        _Float16* c = static_cast<_Float16*>(g.C) + static_cast<int64_t>(m) * g.ldc + o;
+        if (g.vec8_store && o + 8 <= g.n_out) {
+          __builtin_nontemporal_store(h, reinterpret_cast<v8f16*>(c));
+        } else {
+          for (int e = 0; e < 8 && o + e < g.n_out; ++e) c[e] = h[e];
         }
       }
       continue;
@@ -611,6 +717,30 @@ struct KernelEntry {
 
 static const KernelEntry kKernels[] = {HXM_GEMM_CONFIG_LIST(HXM_ENTRY)};
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
+
+// W8A16 kernels: cfg.bk in A bytes (bk = BKB/2 f16 elements on the way out).
+struct W8Entry {
+  hxm_gemm_config cfg;
+  int threads;
+  gemm_fn w8, swiglu;  // swiglu is null unless the wave tile is 128 wide
+};
+
+template <int BM, int BN, int BKB, int ST, int WM, int WN>
+constexpr gemm_fn swiglu_fn() {
+  if constexpr (BN / WN == 128)
+    return gemm_kernel<_Float16, BM, BN, BKB, ST, WM, WN, kEpiSwiglu>;
+  else
+    return nullptr;
+}
+
+#define HXM_W8_ENTRY(BM, BN, BKB, ST, WM, WN)                                  \
+  W8Entry{{BM, BN, BKB, WM, WN, ST, 1},                                        \
+          WM * WN * 64,                                                        \
+          gemm_kernel<_Float16, BM, BN, BKB, ST, WM, WN, kEpiW8>,              \
+          swiglu_fn<BM, BN, BKB, ST, WM, WN>()}
+
+static const W8Entry kW8Kernels[] = {HXM_W8_CONFIG_LIST(HXM_W8_ENTRY)};
+constexpr int kNumW8Kernels = sizeof(kW8Kernels) / sizeof(kW8Kernels[0]);
 
 static int elem_bytes(int32_t dt) { return dt == HXM_I8 ? 1 : 2; }
 
@@ -791,6 +921,128 @@ hxm_status run_gemm(int32_t op, int32_t ab_dtype, int epi, const void* A,
   return ok();
 }
 
+// ---- W8A16 GEMM (f16 x int8 [N, K]) ----
+
+int num_w8_kernels() { return kNumW8Kernels; }
+hxm_gemm_config w8_kernel_config(int i) {
+  hxm_gemm_config c = kW8Kernels[i].cfg;
+  c.bk /= 2;  // f16 elements of K per stage
+  return c;
+}
+bool w8_kernel_has_swiglu(int i) { return kW8Kernels[i].swiglu != nullptr; }
+
+static const W8Entry* find_w8_kernel(const hxm_gemm_config& c, bool swiglu) {
+  for (int i = 0; i < kNumW8Kernels; ++i) {
+    const hxm_gemm_config k = w8_kernel_config(i);
+    if (k.bm == c.bm && k.bn == c.bn && (c.bk == 0 || c.bk == k.bk) &&
+        (c.waves_m == 0 || c.waves_m == k.waves_m) &&
+        (c.waves_n == 0 || c.waves_n == k.waves_n) &&
+        (c.stages == 0 || c.stages == k.stages) && (c.split_k == 0 || c.split_k == 1) &&
+        (!swiglu || kW8Kernels[i].swiglu))
+      return &kW8Kernels[i];
+  }
+  return nullptr;
+}
+
+// The first table entry (largest tiles first) that still gives every CU a
+// workgroup, else the entry with the most tiles.
+hxm_gemm_config default_w8_config(int64_t M, int64_t N, bool swiglu) {
+  int best = -1;
+  int64_t best_tiles = -1;
+  for (int i = 0; i < kNumW8Kernels; ++i) {
+    if (swiglu && !kW8Kernels[i].swiglu) continue;
+    const hxm_gemm_config k = w8_kernel_config(i);
+    const int64_t tiles = ((M + k.bm - 1) / k.bm) * ((N + k.bn - 1) / k.bn);
+    if (tiles >= 256) return k;
+    if (tiles > best_tiles) best = i, best_tiles = tiles;
+  }
+  return w8_kernel_config(best);
+}
+
+// The SwiGLU weight image: rows [128c, 128c+64) are gate channels
+// [64c, 64c+64), rows [128c+64, 128c+128) the same up channels; channels
+// >= I are zero rows with zero scale.  One workgroup per image row.
+__global__ __launch_bounds__(256) void swiglu_pack_kernel(
+    const int8_t* __restrict__ wg, const int8_t* __restrict__ wu, int64_t ldw,
+    const float* __restrict__ sg, const float* __restrict__ su, int64_t I, int64_t K,
+    int8_t* __restrict__ out, float* __restrict__ out_scale) {
+  const int64_t r = blockIdx.x;
+  const int64_t ch = (r / 128) * 64 + (r % 64);
+  const bool up = (r % 128) >= 64;
+  const int8_t* src = up ? wu : wg;
+  int8_t* dst = out + r * K;
+  for (int64_t k = threadIdx.x; k < K; k += blockDim.x)
+    dst[k] = ch < I ? src[ch * ldw + k] : int8_t(0);
+  if (threadIdx.x == 0)
+    out_scale[r] = ch < I ? (up ? su : sg)[ch] : 0.0f;
+}
+
+hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const int8_t* W,
+                       int64_t ldw, const float* scale, void* C, int64_t ldc, int64_t M,
+                       int64_t N, int64_t K, int64_t n_out, const hxm_gemm_config* cfg,
+                       hipStream_t stream) {
+  const bool sw = epi == kEpiSwiglu;
+  hxm_gemm_config c;
+  if (cfg && cfg->bm) {
+    c = *cfg;
+  } else if (!lookup_tuned(op, M, sw ? n_out : N, K, &c)) {
+    c = default_w8_config(M, N, sw);
+  }
+  const W8Entry* e = find_w8_kernel(c, sw);
+  if (!e)
+    return fail(HXM_UNSUPPORTED_SHAPE,
+                "no-kernel: no compiled W8A16 GEMM%s for bm=%d bn=%d bk=%d waves=%dx%d",
+                sw ? " (SwiGLU: wave tile must be 128 wide)" : "", c.bm, c.bn, c.bk,
+                c.waves_m, c.waves_n);
+  hxm_status st = require_device(nullptr);
+  if (st != HXM_OK) return st;
+  if (M == 0 || N == 0) return ok();
+  GemmArgs g;
+  g.A = static_cast<const uint8_t*>(x);
+  g.B = reinterpret_cast<const uint8_t*>(W);
+  g.C = C;
+  g.lda_bytes = ldx * 2;
+  g.ldb_bytes = ldw;
+  g.ldc = ldc;
+  g.M = static_cast<int>(M);
+  g.N = static_cast<int>(N);
+  g.K_bytes = static_cast<int>(K * 2);
+  g.accumulate = 0;
+  g.out_dtype = HXM_F16;
+  g.row_scale = nullptr;
+  g.col_scale = scale;
+  g.group_m = 4;
+  g.n_out = static_cast<int>(n_out);
+  g.vec_store = (reinterpret_cast<uintptr_t>(C) % 8 == 0) && ((ldc * 2) % 8 == 0);
+  g.vec8_store = (reinterpret_cast<uintptr_t>(C) % 16 == 0) && ((ldc * 2) % 16 == 0);
+  const int64_t tiles = ((M + e->cfg.bm - 1) / e->cfg.bm) * ((N + e->cfg.bn - 1) / e->cfg.bn);
+  hipLaunchKernelGGL(sw ? e->swiglu : e->w8, dim3(static_cast<unsigned>(tiles)),
+                     dim3(e->threads), 0, stream, g);
+  if ((st = check_launch("w8a16 gemm kernel")) != HXM_OK) return st;
+  return ok();
+}
+
+// Checks shared by the W8A16 entry points.  x [M, K] f16 and W [N, K] int8
+// stream 16-byte K chunks: K a multiple of 16, 16-byte aligned rows.
+static hxm_status validate_w8(const char* op, const void* x, int64_t ldx, const void* W,
+                              int64_t ldw, const void* scale, const void* C, int64_t ldc,
+                              int64_t M, int64_t N, int64_t K, int64_t out_cols) {
+  if (M < 0 || N < 0 || K < 0)
+    return fail(HXM_INVALID_ARG, "invalid-argument: %s negative extent", op);
+  if (M > 0 && out_cols > 0 && (!C || !scale || (K > 0 && (!x || !W))))
+    return fail(HXM_INVALID_ARG, "invalid-argument: %s null operand", op);
+  if (ldx < K || ldw < K || ldc < out_cols)
+    return fail(HXM_INVALID_ARG, "invalid-argument: %s leading dimension too small", op);
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 4)
+    return fail(HXM_UNSUPPORTED_SHAPE, "tile-alignment: %s extent beyond 2^29", op);
+  if (K % 16 || (K > 0 && ((ldx * 2) % 16 || ldw % 16 || !aligned16(x) || !aligned16(W))))
+    return fail(HXM_UNSUPPORTED_SHAPE,
+                "tile-alignment: %s needs K, ldw in multiples of 16 and lda in multiples "
+                "of 8, with 16-byte aligned x and W (K=%lld)",
+                op, (long long)K);
+  return HXM_OK;
+}
+
 }  // namespace hxm
 
 using namespace hxm;
@@ -900,6 +1152,48 @@ hxm_status hxm_prepack_weight(const void* B, int64_t ldb, void* out,
     transpose_kernel<uint16_t><<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(B), ldb,
                                                     static_cast<uint16_t*>(out), ldo, K, N);
   return check_launch("prepack");
+}
+
+hxm_status hxm_gemm_w8a16(const void* x, int64_t ldx, const int8_t* W, int64_t ldw,
+                          const float* w_scale, void* y, int64_t ldy, int64_t M, int64_t N,
+                          int64_t K, const hxm_gemm_config* cfg, void* stream) {
+  hxm_status st = validate_w8("gemm_w8a16", x, ldx, W, ldw, w_scale, y, ldy, M, N, K, N);
+  if (st != HXM_OK) return st;
+  return run_gemm_w8(kEpiW8, kOpW8, x, ldx, W, ldw, w_scale, y, ldy, M, N, K, N, cfg,
+                     as_stream(stream));
+}
+
+int64_t hxm_swiglu_packed_rows(int64_t I) { return I < 0 ? -1 : 128 * ((I + 63) / 64); }
+
+hxm_status hxm_swiglu_pack(const int8_t* Wg, const int8_t* Wu, int64_t ldw,
+                           const float* gate_scale, const float* up_scale, int64_t I,
+                           int64_t K, int8_t* Wgu, float* sgu, void* stream) {
+  if (I < 0 || K < 0 || ldw < K)
+    return fail(HXM_INVALID_ARG, "invalid-argument: swiglu_pack extents/leading dim");
+  if (I > 0 && (!Wgu || !sgu || !gate_scale || !up_scale || (K > 0 && (!Wg || !Wu))))
+    return fail(HXM_INVALID_ARG, "invalid-argument: swiglu_pack null pointer");
+  if (I > INT32_MAX / 4)
+    return fail(HXM_UNSUPPORTED_SHAPE, "tile-alignment: swiglu_pack I=%lld too large",
+                (long long)I);
+  hxm_status st = require_device(nullptr);
+  if (st != HXM_OK) return st;
+  if (I == 0) return ok();
+  const int64_t rows = hxm_swiglu_packed_rows(I);
+  swiglu_pack_kernel<<<static_cast<unsigned>(rows), 256, 0, as_stream(stream)>>>(
+      Wg, Wu, ldw, gate_scale, up_scale, I, K, Wgu, sgu);
+  return check_launch("swiglu pack");
+}
+
+hxm_status hxm_gemm_w8a16_swiglu(const void* x, int64_t ldx, const int8_t* Wgu,
+                                 const float* sgu, void* h, int64_t ldh, int64_t M,
+                                 int64_t I, int64_t K, const hxm_gemm_config* cfg,
+                                 void* stream) {
+  if (I < 0) return fail(HXM_INVALID_ARG, "invalid-argument: gemm_w8a16_swiglu I < 0");
+  const int64_t N = hxm_swiglu_packed_rows(I);
+  hxm_status st = validate_w8("gemm_w8a16_swiglu", x, ldx, Wgu, K, sgu, h, ldh, M, N, K, I);
+  if (st != HXM_OK) return st;
+  return run_gemm_w8(kEpiSwiglu, kOpSwiglu, x, ldx, Wgu, K, sgu, h, ldh, M, N, K, I, cfg,
+                     as_stream(stream));
 }
 
 }  // extern "C"

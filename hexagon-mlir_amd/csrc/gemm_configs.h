@@ -12,3 +12,13 @@
       X(128, 256, 64, 4, 2, 2), X(128, 128, 128, 2, 2, 2),                       \
       X(128, 128, 64, 4, 2, 2), X(64, 64, 128, 2, 2, 2), X(32, 32, 128, 2, 1, 1)
 #endif
+
+// W8A16 GEMM (f16 activations x int8 [N, K] weights, BKB = A bytes per
+// stage; B rows hold BKB/2 int8).  The SwiGLU variant exists for the entries
+// whose wave tile is 128 columns wide (BN / WAVES_N == 128).
+#ifndef HXM_W8_CONFIG_LIST
+#define HXM_W8_CONFIG_LIST(X)                                                   \
+  X(256, 256, 128, 3, 2, 2), X(256, 256, 128, 2, 2, 2),                          \
+      X(128, 256, 128, 4, 2, 2), X(256, 128, 128, 3, 2, 2),                      \
+      X(128, 128, 128, 3, 2, 2)
+#endif

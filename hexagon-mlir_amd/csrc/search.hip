@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <mutex>
 #include <string>
@@ -33,6 +34,15 @@ hxm_status run_gemm(int32_t op, int32_t ab_dtype, int epi, const void* A,
                     const float* cs, const hxm_gemm_config* cfg,
                     hipStream_t stream);
 hxm_gemm_config default_config(int64_t M, int64_t N, int32_t dt);
+int num_w8_kernels();
+hxm_gemm_config w8_kernel_config(int i);
+bool w8_kernel_has_swiglu(int i);
+hxm_gemm_config default_w8_config(int64_t M, int64_t N, bool swiglu);
+hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const int8_t* W,
+                       int64_t ldw, const float* scale, void* C, int64_t ldc, int64_t M,
+                       int64_t N, int64_t K, int64_t n_out, const hxm_gemm_config* cfg,
+                       hipStream_t stream);
+constexpr int kEpiW8Code = 3, kEpiSwigluCode = 4;  // gemm.hip's Epilogue values
 
 // Constants of hmx_search.py :172-205 (tile edge, min rows, front-end block
 // limit) and :1184-1185 (the gate's two factors).
@@ -91,6 +101,183 @@ __global__ void copy_rows_kernel(const uint32_t* a, int64_t lda_words,
     b[i] = a[r * lda_words + c];
   }
 }
+
+
+namespace {
+// One measured search: every candidate timed on the caller's stream,
+// verified against the control's output, then the champion walk.
+struct TuneSpec {
+  int32_t op;                         // cache key op code
+  int64_t M, N, K;                    // cache key shape (N = output columns)
+  std::vector<hxm_gemm_config> cands; // enumeration order
+  hxm_gemm_config control, canary;
+  int64_t cm, cn, ck;                 // the canary problem
+  std::function<hxm_status(const hxm_gemm_config&, int64_t, int64_t, int64_t)> run;
+  void* C;
+  int64_t ldc, out_eb, out_cols;
+  hipStream_t stream;
+};
+
+void sort_configs(std::vector<hxm_gemm_config>* v) {
+  std::sort(v->begin(), v->end(), [](const hxm_gemm_config& a, const hxm_gemm_config& b) {
+    return std::make_tuple(a.bm, a.bn, a.bk, a.waves_m, a.waves_n, a.stages) <
+           std::make_tuple(b.bm, b.bn, b.bk, b.waves_m, b.waves_n, b.stages);
+  });
+}
+
+hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, char* report,
+                     int64_t report_cap) {
+  hipStream_t s = sp.stream;
+  hxm_status st = HXM_OK;
+  const int32_t op = sp.op;
+  const int64_t M = sp.M, N = sp.N, K = sp.K;
+  const std::vector<hxm_gemm_config>& cands = sp.cands;
+  const hxm_gemm_config control = sp.control;
+  void* const C = sp.C;
+  const int64_t ldc = sp.ldc, out_eb = sp.out_eb;
+  const int64_t row_words = (sp.out_cols * out_eb) / 4;
+  const bool word_rows = (sp.out_cols * out_eb) % 4 == 0 && (ldc * out_eb) % 4 == 0;
+
+  void* ws = nullptr;
+  const size_t ref_bytes = word_rows ? static_cast<size_t>(M * row_words * 4) : 0;
+  if ((st = stream_workspace(s, ref_bytes + 256, &ws)) != HXM_OK) return st;
+  uint32_t* ref = static_cast<uint32_t*>(ws);
+  unsigned* bad = reinterpret_cast<unsigned*>(static_cast<char*>(ws) + ref_bytes);
+
+  hipEvent_t e0, e1;
+  HXM_HIP_TRY(hipEventCreate(&e0));
+  HXM_HIP_TRY(hipEventCreate(&e1));
+
+  auto measure = [&](const hxm_gemm_config& c, int64_t m, int64_t n, int64_t k,
+                     std::vector<double>* samples) -> hxm_status {
+    hxm_status r = sp.run(c, m, n, k);  // discarded warm call
+    if (r != HXM_OK) return r;
+    for (int i = 0; i < reps; ++i) {
+      HXM_HIP_TRY(hipEventRecord(e0, s));
+      r = sp.run(c, m, n, k);
+      if (r != HXM_OK) return r;
+      HXM_HIP_TRY(hipEventRecord(e1, s));
+      HXM_HIP_TRY(hipEventSynchronize(e1));
+      float ms = 0.0f;
+      HXM_HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+      samples->push_back(1000.0 * ms);
+    }
+    return HXM_OK;
+  };
+
+  // Canary first: it says whether the device can be read at all.
+  std::vector<double> cs_samples;
+  const bool canary_ok = measure(sp.canary, sp.cm, sp.cn, sp.ck, &cs_samples) == HXM_OK;
+  const double c20 = canary_ok ? hxm_quantile(cs_samples.data(), reps, 0.2) : INFINITY;
+  const double c50 = canary_ok ? hxm_quantile(cs_samples.data(), reps, 0.5) : INFINITY;
+  const double c80 = canary_ok ? hxm_quantile(cs_samples.data(), reps, 0.8) : INFINITY;
+  double cref = NAN;
+  {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    auto it = g_canary_ref.find(op);
+    if (it != g_canary_ref.end()) cref = it->second;
+  }
+  double cdelta = NAN, cgate = NAN;
+  const int32_t cstatus = hxm_canary_status(1, c20, c50, c80, cref, &cdelta, &cgate);
+  const bool round_valid = cstatus == 0 || cstatus == 4;
+
+  // Control output is the verify reference.
+  int32_t ctl_idx = -1;
+  for (size_t i = 0; i < cands.size(); ++i)
+    if (cands[i].bm == control.bm && cands[i].bn == control.bn &&
+        cands[i].bk == control.bk && cands[i].stages == control.stages &&
+        cands[i].waves_m == control.waves_m && cands[i].waves_n == control.waves_n)
+      ctl_idx = static_cast<int32_t>(i);
+  bool have_ref = false;
+  if (ctl_idx >= 0 && word_rows &&
+      sp.run(cands[ctl_idx], M, N, K) == HXM_OK) {
+    copy_rows_kernel<<<1024, 256, 0, s>>>(static_cast<const uint32_t*>(C),
+                                          (ldc * out_eb) / 4, ref, M, row_words);
+    have_ref = hipGetLastError() == hipSuccess;
+  }
+
+  const int n = static_cast<int>(cands.size());
+  std::vector<double> q20(n, INFINITY), q50(n, INFINITY), q80(n, INFINITY);
+  std::vector<int> verified(n, 0);
+  for (int i = 0; i < n; ++i) {
+    std::vector<double> samples;
+    if (measure(cands[i], M, N, K, &samples) != HXM_OK) continue;  // scores inf
+    if (have_ref) {
+      HXM_HIP_TRY(hipMemsetAsync(bad, 0, sizeof(unsigned), s));
+      count_mismatch_kernel<<<1024, 256, 0, s>>>(static_cast<const uint32_t*>(C),
+                                                 (ldc * out_eb) / 4, ref, M, row_words, bad);
+      unsigned h = 1;
+      HXM_HIP_TRY(hipMemcpyAsync(&h, bad, sizeof(unsigned), hipMemcpyDeviceToHost, s));
+      HXM_HIP_TRY(hipStreamSynchronize(s));
+      if (h != 0) continue;  // a wrong config is wrong, not slow
+      verified[i] = 1;
+    }
+    q20[i] = hxm_quantile(samples.data(), reps, 0.2);
+    q50[i] = hxm_quantile(samples.data(), reps, 0.5);
+    q80[i] = hxm_quantile(samples.data(), reps, 0.8);
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+
+  int32_t start = (ctl_idx >= 0 && is_fin(q50[ctl_idx])) ? ctl_idx : -1;
+  if (start < 0)
+    for (int i = 0; i < n && start < 0; ++i)
+      if (is_fin(q50[i])) start = i;
+  std::vector<int32_t> outcome(n);
+  std::vector<double> delta(n), gate(n);
+  const int32_t champ = hxm_champion_walk(q20.data(), q50.data(), q80.data(), n, start,
+                                          outcome.data(), delta.data(), gate.data());
+  hxm_gemm_config win = champ >= 0 ? cands[champ] : control;
+  {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    if (champ >= 0) g_tuned[TuneKey(op, M, N, K)] = win;
+    if (canary_ok && round_valid) g_canary_ref[op] = c50;
+  }
+  if (best) *best = win;
+
+  if (report && report_cap > 0) {
+    static const char* kCanary[] = {"ok", "missing", "unmeasured", "drift",
+                                    "reference-established"};
+    auto num = [](double v) {
+      char b[64];
+      if (!is_fin(v)) return std::string("null");
+      snprintf(b, sizeof(b), "%.4f", v);
+      return std::string(b);
+    };
+    std::string r = "{\"kind\":\"hxm-search-champion\",\"op\":" + std::to_string(op) +
+                    ",\"shape_mnk\":[" + std::to_string(M) + "," + std::to_string(N) + "," +
+                    std::to_string(K) + "],\"reps\":" + std::to_string(reps) +
+                    ",\"unit\":\"us\",\"round_verdict\":\"" +
+                    (round_valid ? "valid" : "invalid-canary") +
+                    "\",\"canary\":{\"status\":\"" + kCanary[cstatus] +
+                    "\",\"q50\":" + num(c50) + ",\"reference_q50\":" + num(cref) +
+                    ",\"delta_pct\":" + num(100.0 * cdelta) + "},\"control\":" +
+                    (ctl_idx >= 0 ? std::to_string(ctl_idx) : "null") +
+                    ",\"champion\":" + (champ >= 0 ? std::to_string(champ) : "null") +
+                    ",\"configs\":[";
+    for (int i = 0; i < n; ++i) {
+      const hxm_gemm_config& c = cands[i];
+      r += std::string(i ? "," : "") + "{\"tiles\":[" + std::to_string(c.bm) + "," +
+           std::to_string(c.bn) + "," + std::to_string(c.bk) + "],\"waves\":[" +
+           std::to_string(c.waves_m) + "," + std::to_string(c.waves_n) +
+           "],\"stages\":" + std::to_string(c.stages) + ",\"q20\":" + num(q20[i]) + ",\"q50\":" + num(q50[i]) + ",\"q80\":" +
+           num(q80[i]) + ",\"verified\":" + (verified[i] ? "true" : "false") +
+           ",\"outcome\":\"" +
+           (outcome[i] == 1 ? "takeover" : outcome[i] == 0 ? "kept" : "-") +
+           "\",\"delta_pct\":" + num(100.0 * delta[i]) + ",\"gate_pct\":" +
+           num(100.0 * gate[i]) + "}";
+    }
+    r += "]}";
+    const size_t nb = std::min<size_t>(r.size(), static_cast<size_t>(report_cap - 1));
+    memcpy(report, r.data(), nb);
+    report[nb] = 0;
+  }
+  if (champ < 0)
+    return fail(HXM_UNSUPPORTED_SHAPE, "no-kernel: no config measured for this shape");
+  return ok();
+}
+
+}  // namespace
 
 }  // namespace hxm
 
@@ -274,167 +461,80 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
   hipStream_t s = as_stream(stream);
   const int32_t out_dt = (op == HXM_I8) ? HXM_I32 : op;
   const int epi = (op == HXM_I8) ? 0 : 2;
-  const int64_t out_eb = dtype_bytes(out_dt);
-  const int64_t row_words = (N * out_eb) / 4;
-  const bool word_rows = (N * out_eb) % 4 == 0 && (ldc * out_eb) % 4 == 0;
 
   // Candidates in enumeration order (tiles, then label), with the control
   // (the untuned default) and the canary (32x32 tile on a 32^3 problem).
-  std::vector<hxm_gemm_config> cands;
+  TuneSpec sp;
+  sp.op = op;
+  sp.M = M, sp.N = N, sp.K = K;
   for (int i = 0; i < num_kernels(); ++i) {
     hxm_gemm_config c = kernel_config(i, op);
-    if (hxm_gpu_tile_verdict(&c, op, 0) == HXM_REASON_OK) cands.push_back(c);
+    if (hxm_gpu_tile_verdict(&c, op, 0) == HXM_REASON_OK) sp.cands.push_back(c);
   }
-  std::sort(cands.begin(), cands.end(), [](const hxm_gemm_config& a, const hxm_gemm_config& b) {
-    return std::make_tuple(a.bm, a.bn, a.bk, a.waves_m, a.waves_n, a.stages) <
-           std::make_tuple(b.bm, b.bn, b.bk, b.waves_m, b.waves_n, b.stages);
-  });
-  const hxm_gemm_config control = default_config(M, N, op);
-
-  void* ws = nullptr;
-  const size_t ref_bytes = word_rows ? static_cast<size_t>(M * row_words * 4) : 0;
-  if ((st = stream_workspace(s, ref_bytes + 256, &ws)) != HXM_OK) return st;
-  uint32_t* ref = static_cast<uint32_t*>(ws);
-  unsigned* bad = reinterpret_cast<unsigned*>(static_cast<char*>(ws) + ref_bytes);
-
-  hipEvent_t e0, e1;
-  HXM_HIP_TRY(hipEventCreate(&e0));
-  HXM_HIP_TRY(hipEventCreate(&e1));
-
-  auto measure = [&](const hxm_gemm_config& c, int64_t m, int64_t n, int64_t k,
-                     std::vector<double>* samples) -> hxm_status {
-    hxm_status r = run_gemm(op, op, epi, A, lda, B, ldb, HXM_B_NK, C, ldc, m, n, k,
-                            out_dt, 0, nullptr, nullptr, &c, s);  // discarded warm call
-    if (r != HXM_OK) return r;
-    for (int i = 0; i < reps; ++i) {
-      HXM_HIP_TRY(hipEventRecord(e0, s));
-      r = run_gemm(op, op, epi, A, lda, B, ldb, HXM_B_NK, C, ldc, m, n, k, out_dt, 0,
-                   nullptr, nullptr, &c, s);
-      if (r != HXM_OK) return r;
-      HXM_HIP_TRY(hipEventRecord(e1, s));
-      HXM_HIP_TRY(hipEventSynchronize(e1));
-      float ms = 0.0f;
-      HXM_HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
-      samples->push_back(1000.0 * ms);
-    }
-    return HXM_OK;
+  sort_configs(&sp.cands);
+  sp.control = default_config(M, N, op);
+  sp.canary = hxm_gemm_config{32, 32, static_cast<int32_t>(op == HXM_I8 ? 128 : 64), 1, 1, 2, 1};
+  sp.cm = std::min<int64_t>(32, M), sp.cn = std::min<int64_t>(32, N);
+  const int64_t ck = std::min<int64_t>(K, 32);
+  sp.ck = ((ck * eb + 15) / 16) * 16 / eb;
+  sp.run = [=](const hxm_gemm_config& c, int64_t m, int64_t n, int64_t k) {
+    return run_gemm(op, op, epi, A, lda, B, ldb, HXM_B_NK, C, ldc, m, n, k, out_dt, 0,
+                    nullptr, nullptr, &c, s);
   };
+  sp.C = C, sp.ldc = ldc, sp.out_eb = dtype_bytes(out_dt), sp.out_cols = N;
+  sp.stream = s;
+  return tune_core(sp, reps, best, report, report_cap);
+}
 
-  // Canary first: it says whether the device can be read at all.
-  hxm_gemm_config canary{32, 32, static_cast<int32_t>(op == HXM_I8 ? 128 : 64), 1, 1, 2, 1};
-  std::vector<double> cs_samples;
-  const int64_t cm = std::min<int64_t>(32, M), cn = std::min<int64_t>(32, N),
-                ck = std::min<int64_t>(K, 32);
-  const int64_t ck16 = ((ck * eb + 15) / 16) * 16 / eb;
-  const bool canary_ok = measure(canary, cm, cn, ck16, &cs_samples) == HXM_OK;
-  const double c20 = canary_ok ? hxm_quantile(cs_samples.data(), reps, 0.2) : INFINITY;
-  const double c50 = canary_ok ? hxm_quantile(cs_samples.data(), reps, 0.5) : INFINITY;
-  const double c80 = canary_ok ? hxm_quantile(cs_samples.data(), reps, 0.8) : INFINITY;
-  double cref = NAN;
-  {
-    std::lock_guard<std::mutex> lk(g_tune_mu);
-    auto it = g_canary_ref.find(op);
-    if (it != g_canary_ref.end()) cref = it->second;
+int32_t hxm_w8a16_configs(int32_t swiglu, hxm_gemm_config* out, int32_t cap) {
+  int32_t n = 0;
+  for (int i = 0; i < num_w8_kernels(); ++i) {
+    if (swiglu && !w8_kernel_has_swiglu(i)) continue;
+    if (n < cap && out) out[n] = w8_kernel_config(i);
+    ++n;
   }
-  double cdelta = NAN, cgate = NAN;
-  const int32_t cstatus = hxm_canary_status(1, c20, c50, c80, cref, &cdelta, &cgate);
-  const bool round_valid = cstatus == 0 || cstatus == 4;
+  return n;
+}
 
-  // Control output is the verify reference.
-  int32_t ctl_idx = -1;
-  for (size_t i = 0; i < cands.size(); ++i)
-    if (cands[i].bm == control.bm && cands[i].bn == control.bn &&
-        cands[i].bk == control.bk && cands[i].stages == control.stages &&
-        cands[i].waves_m == control.waves_m && cands[i].waves_n == control.waves_n)
-      ctl_idx = static_cast<int32_t>(i);
-  bool have_ref = false;
-  if (ctl_idx >= 0 && word_rows &&
-      run_gemm(op, op, epi, A, lda, B, ldb, HXM_B_NK, C, ldc, M, N, K, out_dt, 0,
-               nullptr, nullptr, &cands[ctl_idx], s) == HXM_OK) {
-    copy_rows_kernel<<<1024, 256, 0, s>>>(static_cast<const uint32_t*>(C),
-                                          (ldc * out_eb) / 4, ref, M, row_words);
-    have_ref = hipGetLastError() == hipSuccess;
-  }
+hxm_status hxm_tune_w8a16(int32_t op, const void* x, int64_t ldx, const int8_t* W,
+                          int64_t ldw, const float* scale, void* C, int64_t ldc, int64_t M,
+                          int64_t N, int64_t K, int32_t reps, hxm_gemm_config* best,
+                          char* report, int64_t report_cap, void* stream) {
+  if (op != HXM_OP_W8A16 && op != HXM_OP_W8A16_SWIGLU)
+    return fail(HXM_INVALID_ARG, "invalid-argument: tune_w8a16 op %d", op);
+  const bool sw = op == HXM_OP_W8A16_SWIGLU;
+  if (M <= 0 || N <= 0 || K <= 0 || reps <= 0 || reps > 10000)
+    return fail(HXM_INVALID_ARG, "invalid-argument: tune extents/reps");
+  const int64_t rows = sw ? hxm_swiglu_packed_rows(N) : N;
+  if (!x || !W || !scale || !C || ldx < K || ldw < K || ldc < N)
+    return fail(HXM_INVALID_ARG, "invalid-argument: tune operands");
+  if (K % 16 || (ldx * 2) % 16 || ldw % 16 || !aligned16(x) || !aligned16(W) ||
+      (sw && ldw != K))
+    return fail(HXM_UNSUPPORTED_SHAPE,
+                "tile-alignment: tune_w8a16 needs K, ldw in multiples of 16, lda in "
+                "multiples of 8, aligned x and W (the SwiGLU image has ldw == K)");
+  hxm_status st = require_device(nullptr);
+  if (st != HXM_OK) return st;
+  hipStream_t s = as_stream(stream);
+  const int epi = sw ? kEpiSwigluCode : kEpiW8Code;
 
-  const int n = static_cast<int>(cands.size());
-  std::vector<double> q20(n, INFINITY), q50(n, INFINITY), q80(n, INFINITY);
-  std::vector<int> verified(n, 0);
-  for (int i = 0; i < n; ++i) {
-    std::vector<double> samples;
-    if (measure(cands[i], M, N, K, &samples) != HXM_OK) continue;  // scores inf
-    if (have_ref) {
-      HXM_HIP_TRY(hipMemsetAsync(bad, 0, sizeof(unsigned), s));
-      count_mismatch_kernel<<<1024, 256, 0, s>>>(static_cast<const uint32_t*>(C),
-                                                 (ldc * out_eb) / 4, ref, M, row_words, bad);
-      unsigned h = 1;
-      HXM_HIP_TRY(hipMemcpyAsync(&h, bad, sizeof(unsigned), hipMemcpyDeviceToHost, s));
-      HXM_HIP_TRY(hipStreamSynchronize(s));
-      if (h != 0) continue;  // a wrong config is wrong, not slow
-      verified[i] = 1;
-    }
-    q20[i] = hxm_quantile(samples.data(), reps, 0.2);
-    q50[i] = hxm_quantile(samples.data(), reps, 0.5);
-    q80[i] = hxm_quantile(samples.data(), reps, 0.8);
-  }
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-
-  int32_t start = (ctl_idx >= 0 && is_fin(q50[ctl_idx])) ? ctl_idx : -1;
-  if (start < 0)
-    for (int i = 0; i < n && start < 0; ++i)
-      if (is_fin(q50[i])) start = i;
-  std::vector<int32_t> outcome(n);
-  std::vector<double> delta(n), gate(n);
-  const int32_t champ = hxm_champion_walk(q20.data(), q50.data(), q80.data(), n, start,
-                                          outcome.data(), delta.data(), gate.data());
-  hxm_gemm_config win = champ >= 0 ? cands[champ] : control;
-  {
-    std::lock_guard<std::mutex> lk(g_tune_mu);
-    if (champ >= 0) g_tuned[TuneKey(op, M, N, K)] = win;
-    if (canary_ok && round_valid) g_canary_ref[op] = c50;
-  }
-  if (best) *best = win;
-
-  if (report && report_cap > 0) {
-    static const char* kCanary[] = {"ok", "missing", "unmeasured", "drift",
-                                    "reference-established"};
-    auto num = [](double v) {
-      char b[64];
-      if (!is_fin(v)) return std::string("null");
-      snprintf(b, sizeof(b), "%.4f", v);
-      return std::string(b);
-    };
-    std::string r = "{\"kind\":\"hxm-search-champion\",\"op\":" + std::to_string(op) +
-                    ",\"shape_mnk\":[" + std::to_string(M) + "," + std::to_string(N) + "," +
-                    std::to_string(K) + "],\"reps\":" + std::to_string(reps) +
-                    ",\"unit\":\"us\",\"round_verdict\":\"" +
-                    (round_valid ? "valid" : "invalid-canary") +
-                    "\",\"canary\":{\"status\":\"" + kCanary[cstatus] +
-                    "\",\"q50\":" + num(c50) + ",\"reference_q50\":" + num(cref) +
-                    ",\"delta_pct\":" + num(100.0 * cdelta) + "},\"control\":" +
-                    (ctl_idx >= 0 ? std::to_string(ctl_idx) : "null") +
-                    ",\"champion\":" + (champ >= 0 ? std::to_string(champ) : "null") +
-                    ",\"configs\":[";
-    for (int i = 0; i < n; ++i) {
-      const hxm_gemm_config& c = cands[i];
-      r += std::string(i ? "," : "") + "{\"tiles\":[" + std::to_string(c.bm) + "," +
-           std::to_string(c.bn) + "," + std::to_string(c.bk) + "],\"waves\":[" +
-           std::to_string(c.waves_m) + "," + std::to_string(c.waves_n) +
-           "],\"stages\":" + std::to_string(c.stages) + ",\"q20\":" + num(q20[i]) + ",\"q50\":" + num(q50[i]) + ",\"q80\":" +
-           num(q80[i]) + ",\"verified\":" + (verified[i] ? "true" : "false") +
-           ",\"outcome\":\"" +
-           (outcome[i] == 1 ? "takeover" : outcome[i] == 0 ? "kept" : "-") +
-           "\",\"delta_pct\":" + num(100.0 * delta[i]) + ",\"gate_pct\":" +
-           num(100.0 * gate[i]) + "}";
-    }
-    r += "]}";
-    const size_t nb = std::min<size_t>(r.size(), static_cast<size_t>(report_cap - 1));
-    memcpy(report, r.data(), nb);
-    report[nb] = 0;
-  }
-  if (champ < 0)
-    return fail(HXM_UNSUPPORTED_SHAPE, "no-kernel: no config measured for this shape");
-  return ok();
+  TuneSpec sp;
+  sp.op = op;
+  sp.M = M, sp.N = N, sp.K = K;
+  for (int i = 0; i < num_w8_kernels(); ++i)
+    if (!sw || w8_kernel_has_swiglu(i)) sp.cands.push_back(w8_kernel_config(i));
+  sort_configs(&sp.cands);
+  sp.control = default_w8_config(M, rows, sw);
+  sp.canary = sp.cands.front();  // the smallest compiled tile on a 32-row slice
+  sp.cm = std::min<int64_t>(32, M), sp.cn = std::min<int64_t>(sw ? 64 : 32, N);
+  sp.ck = std::min<int64_t>(K, 32);
+  sp.run = [=](const hxm_gemm_config& c, int64_t m, int64_t n, int64_t k) {
+    const int64_t nr = sw ? hxm_swiglu_packed_rows(n) : n;
+    return run_gemm_w8(epi, op, x, ldx, W, ldw, scale, C, ldc, m, nr, k, n, &c, s);
+  };
+  sp.C = C, sp.ldc = ldc, sp.out_eb = 2, sp.out_cols = N;
+  sp.stream = s;
+  return tune_core(sp, reps, best, report, report_cap);
 }
 
 }  // extern "C"

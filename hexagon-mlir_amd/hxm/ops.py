@@ -14,7 +14,8 @@ from typing import Optional, Sequence
 
 import torch
 
-from ._lib import (B_KN, B_NK, BF16, F16, F32, I8, I32, W_NK, W_PACKED, GemmConfig, check, lib)
+from ._lib import (B_KN, B_NK, BF16, F16, F32, I8, I32, OP_W8A16, OP_W8A16_SWIGLU, W_NK,
+                   W_PACKED, GemmConfig, check, lib)
 
 _DT = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32,
        torch.int8: I8, torch.int32: I32}
@@ -183,6 +184,116 @@ def gemv_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor,
                             out.data_ptr(), _ld(out), M, N, K, _stream(stream))
     check(st, "hxm_gemv_w8a16")
     return out
+
+
+def _f32_vec(t: torch.Tensor, n: int, name: str) -> torch.Tensor:
+    if not t.is_cuda or t.dtype != torch.float32 or t.numel() != n:
+        raise ValueError(f"{name} must be a GPU float32 tensor of {n} elements")
+    return t.contiguous()
+
+
+def gemm_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor,
+               out: Optional[torch.Tensor] = None, *, config=None, stream=None) -> torch.Tensor:
+    """y = f16((x @ W.T in fp32) * scale) for f16 x [M, K], int8 W [N, K] and
+    fp32 per-channel scale [N] (the large-M W8A16 GEMM of the FFN)."""
+    _mat(x, "x"), _mat(W, "W")
+    M, K = x.shape
+    N = W.shape[0]
+    if W.shape[1] != K:
+        raise ValueError("W must be [N, K]")
+    scale = _f32_vec(scale, N, "scale")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    _mat(out, "out")
+    cfg = _cfg(config)
+    st = lib.hxm_gemm_w8a16(x.data_ptr(), _ld(x), W.data_ptr(), _ld(W), scale.data_ptr(),
+                            out.data_ptr(), _ld(out), M, N, K, _ptr_or_none(cfg),
+                            _stream(stream))
+    check(st, "hxm_gemm_w8a16")
+    return out
+
+
+def swiglu_pack(Wg: torch.Tensor, Wu: torch.Tensor, gate_scale: torch.Tensor,
+                up_scale: torch.Tensor, *, stream=None):
+    """The fused gate/up image (int8 [128*ceil(I/64), K]) and its fp32 scales
+    from gate/up weights int8 [I, K] and fp32 scales [I]; made once per
+    weight pair."""
+    _mat(Wg, "Wg"), _mat(Wu, "Wu")
+    I, K = Wg.shape
+    if tuple(Wu.shape) != (I, K) or _ld(Wu) != _ld(Wg):
+        raise ValueError("Wg and Wu must both be [I, K] with the same row stride")
+    sg = _f32_vec(gate_scale, I, "gate_scale")
+    su = _f32_vec(up_scale, I, "up_scale")
+    rows = lib.hxm_swiglu_packed_rows(I)
+    Wgu = torch.empty((rows, K), dtype=torch.int8, device=Wg.device)
+    sgu = torch.empty(rows, dtype=torch.float32, device=Wg.device)
+    st = lib.hxm_swiglu_pack(Wg.data_ptr(), Wu.data_ptr(), _ld(Wg), sg.data_ptr(),
+                             su.data_ptr(), I, K, Wgu.data_ptr(), sgu.data_ptr(),
+                             _stream(stream))
+    check(st, "hxm_swiglu_pack")
+    return Wgu, sgu
+
+
+def gemm_w8a16_swiglu(x: torch.Tensor, Wgu: torch.Tensor, sgu: torch.Tensor, I: int,
+                      out: Optional[torch.Tensor] = None, *, config=None,
+                      stream=None) -> torch.Tensor:
+    """h = f16(silu(x @ Wg.T * sg) * (x @ Wu.T * su)) from the
+    :func:`swiglu_pack` image; h is [M, I]."""
+    _mat(x, "x"), _mat(Wgu, "Wgu")
+    M, K = x.shape
+    rows = lib.hxm_swiglu_packed_rows(I)
+    if tuple(Wgu.shape) != (rows, K) or _ld(Wgu) != K:
+        raise ValueError(f"Wgu must be the contiguous [{rows}, {K}] swiglu_pack image")
+    sgu = _f32_vec(sgu, rows, "sgu")
+    if out is None:
+        out = torch.empty((M, I), dtype=torch.float16, device=x.device)
+    _mat(out, "out")
+    cfg = _cfg(config)
+    st = lib.hxm_gemm_w8a16_swiglu(x.data_ptr(), _ld(x), Wgu.data_ptr(), sgu.data_ptr(),
+                                   out.data_ptr(), _ld(out), M, I, K, _ptr_or_none(cfg),
+                                   _stream(stream))
+    check(st, "hxm_gemm_w8a16_swiglu")
+    return out
+
+
+def swiglu_ffn(x: torch.Tensor, gamma: torch.Tensor, Wgu: torch.Tensor, sgu: torch.Tensor,
+               Wd: torch.Tensor, sd: torch.Tensor, I: int, *, eps: float = 1e-6,
+               configs=(None, None), stream=None) -> torch.Tensor:
+    """The Llama-style SwiGLU FFN block: RMSNorm -> fused gate/up GEMM with
+    SiLU * mul -> down GEMM.  x f16 [T, H]; gamma f16 [H]; Wgu/sgu from
+    :func:`swiglu_pack`; Wd int8 [H, I] with fp32 scales sd [H]."""
+    xn = rms_norm(x, (x.shape[-1],), gamma, eps=eps, stream=stream)
+    h = gemm_w8a16_swiglu(xn, Wgu, sgu, I, config=configs[0], stream=stream)
+    return gemm_w8a16(h, Wd, sd, config=configs[1], stream=stream)
+
+
+def w8a16_configs(swiglu: bool = False):
+    """The compiled W8A16 GEMM configurations (bk in f16 elements)."""
+    n = lib.hxm_w8a16_configs(int(swiglu), None, 0)
+    arr = (GemmConfig * n)()
+    lib.hxm_w8a16_configs(int(swiglu), arr, n)
+    return list(arr)
+
+
+def tune_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor, out: torch.Tensor, *,
+               swiglu: bool = False, reps: int = 5, stream=None):
+    """Measured tile search for :func:`gemm_w8a16` (W [N, K], scale [N]) or,
+    with swiglu=True, :func:`gemm_w8a16_swiglu` (W = Wgu, scale = sgu, out
+    [M, I]).  The winner is cached for later calls; returns (GemmConfig,
+    report dict)."""
+    import ctypes
+    import json
+    _mat(x, "x"), _mat(W, "W"), _mat(out, "out")
+    M, K = x.shape
+    N = out.shape[1]
+    best = GemmConfig()
+    buf = ctypes.create_string_buffer(1 << 16)
+    st = lib.hxm_tune_w8a16(OP_W8A16_SWIGLU if swiglu else OP_W8A16, x.data_ptr(), _ld(x),
+                            W.data_ptr(), _ld(W), scale.contiguous().data_ptr(),
+                            out.data_ptr(), _ld(out), M, N, K, reps, ctypes.byref(best), buf,
+                            len(buf), _stream(stream))
+    check(st, "hxm_tune_w8a16")
+    return best, json.loads(buf.value.decode())
 
 
 def _rows(x: torch.Tensor):

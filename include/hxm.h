@@ -193,6 +193,72 @@ hxm_status hxm_prepack_w8a16(const int8_t* W, int64_t ldw, int64_t N,
                              int64_t K, int8_t* out, int64_t out_bytes,
                              void* stream);
 
+/* ---- SwiGLU FFN block (RMSNorm -> int8-weight gate/up
+ *      GEMMs -> SiLU*mul -> down GEMM).  The reference composes it from the
+ *      linalg ops its pipeline lowers: linalg.matmul (MatmulToHmxPass.cpp
+ *      :101-121 admission; int8 operands take the HVX path,
+ *      ScheduleMatmulForHVXPass.cpp:44-80) and elementwise linalg.generic
+ *      ops.  The int8 weights stay int8 in HBM and are converted to fp16 in
+ *      registers (exactly) in front of the fp16 MFMA. ---- */
+
+/* Tuning-cache op codes of the W8A16 GEMMs (hxm_tune_w8a16). */
+enum { HXM_OP_W8A16 = 16, HXM_OP_W8A16_SWIGLU = 17 };
+
+/* Large-M W8A16 GEMM (the gate/up/down projections of the FFN; the GEMV
+ * above covers M <= 16 best):
+ *   y[m,n] = rne_f16( (sum_k f32(x[m,k]) * f32(W[n,k])) * f32(w_scale[n]) )
+ * x fp16 [M,K] (ldx >= K); W int8 [N,K] (ldw >= K); w_scale fp32 [N];
+ * y fp16 [M,N] (ldy >= N).  fp32 accumulation in MFMA order (tolerance
+ * rtol 1e-2 / atol 1e-3).  K multiple of 16, ldx multiple of 8, ldw
+ * multiple of 16, x and W 16-byte aligned.  cfg: NULL = tuned winner or the
+ * default tile; else one of hxm_w8a16_configs. */
+hxm_status hxm_gemm_w8a16(const void* x, int64_t ldx, const int8_t* W,
+                          int64_t ldw, const float* w_scale, void* y,
+                          int64_t ldy, int64_t M, int64_t N, int64_t K,
+                          const hxm_gemm_config* cfg, void* stream);
+
+/* Rows of the fused gate/up image for I intermediate channels:
+ * 128 * ceil(I / 64) (-1 for I < 0). */
+int64_t hxm_swiglu_packed_rows(int64_t I);
+
+/* Builds the gate/up image once per weight pair (the weight-resident
+ * contract, WeightResidentPass.cpp:10-53): Wgu int8 [hxm_swiglu_packed_rows(I),
+ * K] (row stride K) whose rows [128c, 128c+64) are gate channels
+ * [64c, 64c+64) and rows [128c+64, 128c+128) the same up channels, channels
+ * >= I zero; sgu fp32 [rows] the matching scales (zero for padding).
+ * Wg, Wu int8 [I,K] (ldw >= K); gate_scale, up_scale fp32 [I]. */
+hxm_status hxm_swiglu_pack(const int8_t* Wg, const int8_t* Wu, int64_t ldw,
+                           const float* gate_scale, const float* up_scale,
+                           int64_t I, int64_t K, int8_t* Wgu, float* sgu,
+                           void* stream);
+
+/* Fused gate/up projection + SiLU * mul:
+ *   g = f32(sum_k x[m,k] * Wg[i,k]) * sg[i],  u = (same with Wu) * su[i]
+ *   h[m,i] = rne_f16( g / (1 + exp(-g)) * u )
+ * x fp16 [M,K] (ldx >= K); Wgu/sgu from hxm_swiglu_pack; h fp16 [M,I]
+ * (ldh >= I).  exp and the reciprocal use the hardware approximations
+ * (tolerance rtol 1e-2 / atol 1e-3).  Same K/alignment rules as
+ * hxm_gemm_w8a16; cfg must have a 128-column wave tile (bn / waves_n). */
+hxm_status hxm_gemm_w8a16_swiglu(const void* x, int64_t ldx, const int8_t* Wgu,
+                                 const float* sgu, void* h, int64_t ldh,
+                                 int64_t M, int64_t I, int64_t K,
+                                 const hxm_gemm_config* cfg, void* stream);
+
+/* The compiled W8A16 GEMM configurations (bk in fp16 elements of K); with
+ * swiglu != 0 only those that have the fused SwiGLU kernel.  Returns the
+ * count; writes up to cap entries. */
+int32_t hxm_w8a16_configs(int32_t swiglu, hxm_gemm_config* out, int32_t cap);
+
+/* hxm_tune_gemm for the W8A16 GEMMs (same protocol, report and cache):
+ * op HXM_OP_W8A16 measures hxm_gemm_w8a16 (scale = w_scale, N output
+ * channels); HXM_OP_W8A16_SWIGLU measures hxm_gemm_w8a16_swiglu (W = Wgu
+ * with ldw == K, scale = sgu, N = I).  C is the [M,N] fp16 output. */
+hxm_status hxm_tune_w8a16(int32_t op, const void* x, int64_t ldx,
+                          const int8_t* W, int64_t ldw, const float* scale,
+                          void* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                          int32_t reps, hxm_gemm_config* best, char* report,
+                          int64_t report_cap, void* stream);
+
 /* ---- row reductions (test/python/triton/test_softmax.py:41-69,
  *      test_rms_norm.py:34-60, test_layer_norm.py:39-79, as lowered by
  *      VectorRowReducePass.cpp:10-31 / SplitReduceGenericPass.cpp:62-93) -- */

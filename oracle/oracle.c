@@ -16,6 +16,12 @@
  *   hxo_matmul_f16     hmx.matmul (HmxOps.td:47) / test_matmul.py:73-88:
  *                      wide accumulate (fp32 here), one rounding to C.
  *   hxo_gemv_w8a16     int8-weight matmul, fp32 accumulate, per-channel scale.
+ *   hxo_gemm_w8a16     the same with fp32 scales (the FFN projections of the
+ *                      BASELINE SwiGLU block; int8 operands of linalg.matmul
+ *                      take the HVX path, ScheduleMatmulForHVXPass.cpp:44-80).
+ *   hxo_swiglu_gateup  gate/up projections + SiLU * mul of that block:
+ *                      h = f16(silu(g) * u), g = acc_g * sg, u = acc_u * su,
+ *                      silu(g) = g / (1 + exp(-g)) evaluated in fp64.
  *   hxo_softmax_rows   test/python/triton/test_softmax.py:41-69 (fp32 sum).
  *   hxo_rmsnorm_rows   test/python/triton/test_rms_norm.py:34-60.
  *   hxo_layernorm_rows test/python/triton/test_layer_norm.py:39-79.
@@ -239,6 +245,49 @@ void hxo_softmax_rows(const void* x, int64_t ldx, void* y, int64_t ldy,
 }
 
 /* y = x * (1/sqrt(mean(x^2) + eps)) * gamma; statistics in fp64. */
+/* y[m,n] = f16((sum_k f32(x[m,k]) * f32(W[n,k])) * scale[n]), the sum in
+ * fp32 in increasing k. */
+void hxo_gemm_w8a16(const uint16_t* x, int64_t ldx, const int8_t* W, int64_t ldw,
+                    const float* scale, uint16_t* y, int64_t ldy, int64_t M, int64_t N,
+                    int64_t K, int threads) {
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+#endif
+  for (int64_t n = 0; n < N; ++n) {
+    for (int64_t m = 0; m < M; ++m) {
+      float s = 0.0f;
+      for (int64_t k = 0; k < K; ++k)
+        s += hxo_f16_to_f32(x[m * ldx + k]) * (float)W[n * ldw + k];
+      y[m * ldy + n] = hxo_f32_to_f16(s * scale[n]);
+    }
+  }
+}
+
+/* h[m,i] = f16(silu(g) * u) with g = f32(sum_k x*Wg[i,k]) * sg[i] and
+ * u = f32(sum_k x*Wu[i,k]) * su[i] (fp32 sums in increasing k, fp32
+ * products); silu and the product in fp64. */
+void hxo_swiglu_gateup(const uint16_t* x, int64_t ldx, const int8_t* Wg, const int8_t* Wu,
+                       int64_t ldw, const float* sg, const float* su, uint16_t* h,
+                       int64_t ldh, int64_t M, int64_t I, int64_t K, int threads) {
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+#endif
+  for (int64_t i = 0; i < I; ++i) {
+    for (int64_t m = 0; m < M; ++m) {
+      float ag = 0.0f, au = 0.0f;
+      for (int64_t k = 0; k < K; ++k) {
+        const float xv = hxo_f16_to_f32(x[m * ldx + k]);
+        ag += xv * (float)Wg[i * ldw + k];
+        au += xv * (float)Wu[i * ldw + k];
+      }
+      const double g = (double)(ag * sg[i]), u = (double)(au * su[i]);
+      h[m * ldh + i] = hxo_f32_to_f16((float)(g / (1.0 + exp(-g)) * u));
+    }
+  }
+}
+
 void hxo_rmsnorm_rows(const void* x, int64_t ldx, const void* gamma, void* y,
                       int64_t ldy, int64_t rows, int64_t cols, float eps,
                       int dtype) {

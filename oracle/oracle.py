@@ -30,6 +30,10 @@ matmul (f16/bf16)      torch.matmul (the reference test's own oracle,
                        test_matmul.py:86-88) in float64; small-integer KAT
                        that makes every sum exact (bit-exact expectation)
 gemv_w8a16             numpy float64 matmul of the dequantised weights
+gemm_w8a16             numpy float64 matmul of the dequantised weights;
+                       small-integer KAT (every fp32 sum exact -> bit-exact)
+swiglu_gateup          numpy float64 silu(g)*u on numpy's float64 gate/up
+                       products; g = 0 -> 0, g >> 0 -> g*u, g << 0 -> 0
 softmax_rows           torch.softmax in float64 (test_softmax.py:91);
                        invariants: rows sum to 1, shift invariance, constant
                        row -> 1/cols, argmax preserved
@@ -76,6 +80,9 @@ _SIGS = {
     "hxo_matmul": (None, [_p, _i64, _p, _i64, _i32, _i32, _p, _i64, _i32, _i32,
                           _i64, _i64, _i64, _i32]),
     "hxo_gemv_w8a16": (None, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32]),
+    "hxo_gemm_w8a16": (None, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32]),
+    "hxo_swiglu_gateup": (None, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64,
+                                 _i32]),
     "hxo_softmax_rows": (None, [_p, _i64, _p, _i64, _i64, _i64, _i32]),
     "hxo_rmsnorm_rows": (None, [_p, _i64, _p, _p, _i64, _i64, _i64, _f32, _i32]),
     "hxo_layernorm_rows": (None, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i64, _i64, _f32, _i32]),
@@ -213,6 +220,44 @@ def gemv_w8a16(x_bits: np.ndarray, W: np.ndarray, scale_bits: np.ndarray,
     y = np.empty((M, N), dtype=np.uint16)
     lib().hxo_gemv_w8a16(_ptr(x), K, _ptr(W), K, _ptr(sc), _ptr(y), N, M, N, K, threads)
     return y
+
+
+def gemm_w8a16(x_bits: np.ndarray, W: np.ndarray, scale: np.ndarray,
+               threads: int = 0) -> np.ndarray:
+    """y = f16((x . W^T) * scale): x f16 bits [M,K], W int8 [N,K], scale fp32 [N]."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    W = np.ascontiguousarray(W, dtype=np.int8)
+    sc = np.ascontiguousarray(scale, dtype=np.float32)
+    M, K = x.shape
+    N = W.shape[0]
+    y = np.zeros((M, N), dtype=np.uint16)
+    lib().hxo_gemm_w8a16(_ptr(x), K, _ptr(W), K, _ptr(sc), _ptr(y), N, M, N, K, threads)
+    return y
+
+
+def swiglu_gateup(x_bits: np.ndarray, Wg: np.ndarray, Wu: np.ndarray, sg: np.ndarray,
+                  su: np.ndarray, threads: int = 0) -> np.ndarray:
+    """h = f16(silu(g) * u) with g = (x . Wg^T) * sg, u = (x . Wu^T) * su."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    Wg = np.ascontiguousarray(Wg, dtype=np.int8)
+    Wu = np.ascontiguousarray(Wu, dtype=np.int8)
+    sg = np.ascontiguousarray(sg, dtype=np.float32)
+    su = np.ascontiguousarray(su, dtype=np.float32)
+    M, K = x.shape
+    I = Wg.shape[0]
+    h = np.zeros((M, I), dtype=np.uint16)
+    lib().hxo_swiglu_gateup(_ptr(x), K, _ptr(Wg), _ptr(Wu), K, _ptr(sg), _ptr(su), _ptr(h), I,
+                            M, I, K, threads)
+    return h
+
+
+def swiglu_ffn(x_bits: np.ndarray, gamma_bits: np.ndarray, Wg, Wu, sg, su, Wd, sd,
+               eps: float = 1e-6, threads: int = 0) -> np.ndarray:
+    """The BASELINE SwiGLU FFN block with fp16 tensors between the stages:
+    xn = rmsnorm(x) (f16), h = swiglu_gateup(xn) (f16), y = gemm_w8a16(h, Wd)."""
+    xn = rmsnorm_rows(x_bits, gamma_bits, eps, "f16")
+    h = swiglu_gateup(xn, Wg, Wu, sg, su, threads)
+    return gemm_w8a16(h, Wd, sd, threads)
 
 
 def _rows_io(x, dtype):

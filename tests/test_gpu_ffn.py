@@ -1,0 +1,207 @@
+"""GPU parity of the SwiGLU FFN block against the CPU
+oracle: the large-M W8A16 GEMM, the gate/up image, the fused gate/up GEMM
+with SiLU * mul, and the whole block RMSNorm -> gate/up -> down.
+
+fp16 outputs are held to rtol 1e-2 / atol 1e-3 (fp32 accumulation in MFMA
+order vs the oracle's increasing-k fp32 sums); a small-integer case makes
+every sum exact, so the W8A16 GEMM must match bit for bit.  At the BASELINE
+size (tokens 2048, hidden 4096, intermediate 11008) the oracle runs on a row
+sample of the same inputs."""
+import numpy as np
+import pytest
+import torch
+
+import hxm.ops as ops
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(rtol=1e-2, atol=1e-3)
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def f32(b):
+    return orc.f16_bits_to_f32(b)
+
+
+def operands(M, N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).half()
+    W = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    s = (torch.rand(N, generator=g) * 0.019 + 0.001).half().float()  # fp16-valued fp32
+    return x, W, s
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 512), (300, 260, 1024), (33, 96, 64),
+                                   (1, 40, 16), (512, 4096, 1024)])
+def test_gemm_w8a16(dev, M, N, K):
+    print(f"gemm_w8a16 M={M} N={N} K={K}", flush=True)
+    x, W, s = operands(M, N, K, M + N + K)
+    y = ops.gemm_w8a16(x.to(dev), W.to(dev), s.to(dev))
+    ref = orc.gemm_w8a16(bits(x), W.numpy(), s.numpy())
+    np.testing.assert_allclose(y.float().cpu().numpy(), f32(ref), **TOL)
+
+
+@pytest.mark.parametrize("cfg", ops.w8a16_configs(), ids=repr)
+def test_gemm_w8a16_every_config(dev, cfg):
+    print(f"gemm_w8a16 config {cfg}", flush=True)
+    M, N, K = 300, 520, 640
+    x, W, s = operands(M, N, K, 7)
+    y = ops.gemm_w8a16(x.to(dev), W.to(dev), s.to(dev), config=cfg)
+    ref = orc.gemm_w8a16(bits(x), W.numpy(), s.numpy())
+    np.testing.assert_allclose(y.float().cpu().numpy(), f32(ref), **TOL)
+
+
+def test_gemm_w8a16_small_integers_bit_exact(dev):
+    """|x| <= 4, |W| <= 8, K = 256: every product and partial sum is an
+    integer below 2^24, so every summation order gives the same fp32 sum and
+    the f16 result must equal the oracle's bit for bit."""
+    g = torch.Generator().manual_seed(3)
+    M, N, K = 128, 256, 256
+    x = torch.randint(-4, 5, (M, K), generator=g).half()
+    W = torch.randint(-8, 9, (N, K), generator=g, dtype=torch.int8)
+    s = torch.full((N,), 0.125)
+    y = ops.gemm_w8a16(x.to(dev), W.to(dev), s.to(dev))
+    assert np.array_equal(bits(y), orc.gemm_w8a16(bits(x), W.numpy(), s.numpy()))
+
+
+def test_gemm_w8a16_strided_and_refusals(dev):
+    x, W, s = operands(64, 128, 256, 11)
+    xb = torch.zeros(64, 264, dtype=torch.float16, device=dev)
+    xb[:, :256] = x.to(dev)
+    Wb = torch.zeros(128, 272, dtype=torch.int8, device=dev)
+    Wb[:, :256] = W.to(dev)
+    yb = torch.full((64, 136), 7.0, dtype=torch.float16, device=dev)
+    ops.gemm_w8a16(xb[:, :256], Wb[:, :256], s.to(dev), out=yb[:, :128])
+    ref = orc.gemm_w8a16(bits(x), W.numpy(), s.numpy())
+    np.testing.assert_allclose(yb[:, :128].float().cpu().numpy(), f32(ref), **TOL)
+    assert (yb[:, 128:] == 7).all()                      # outside the view untouched
+    with pytest.raises(Exception, match="tile-alignment"):
+        ops.gemm_w8a16(x[:, :24].contiguous().to(dev), W[:, :24].contiguous().to(dev),
+                       s.to(dev))
+
+
+def test_swiglu_pack_layout(dev):
+    """Image rows [128c, 128c+64) = gate channels [64c, 64c+64), the next 64
+    rows the same up channels; channels >= I zero rows with zero scale."""
+    I, K = 100, 48
+    g = torch.Generator().manual_seed(5)
+    Wg = torch.randint(-127, 128, (I, K), generator=g, dtype=torch.int8)
+    Wu = torch.randint(-127, 128, (I, K), generator=g, dtype=torch.int8)
+    sg, su = torch.rand(I, generator=g), torch.rand(I, generator=g)
+    Wgu, sgu = ops.swiglu_pack(Wg.to(dev), Wu.to(dev), sg.to(dev), su.to(dev))
+    rows = 128 * ((I + 63) // 64)
+    assert tuple(Wgu.shape) == (rows, K) and sgu.numel() == rows
+    expW = np.zeros((rows, K), np.int8)
+    exps = np.zeros(rows, np.float32)
+    for r in range(rows):
+        ch = (r // 128) * 64 + r % 64
+        if ch < I:
+            src, ss = (Wu, su) if r % 128 >= 64 else (Wg, sg)
+            expW[r], exps[r] = src[ch].numpy(), ss[ch].item()
+    assert np.array_equal(Wgu.cpu().numpy(), expW)
+    assert np.array_equal(sgu.cpu().numpy(), exps)
+
+
+def swiglu_operands(M, I, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).half()
+    Wg = torch.randint(-127, 128, (I, K), generator=g, dtype=torch.int8)
+    Wu = torch.randint(-127, 128, (I, K), generator=g, dtype=torch.int8)
+    # scales ~ 1/sqrt(K * 127^2 / 3) keep g and u near unit size
+    sc = 1.0 / np.sqrt(K * 127.0 ** 2 / 3.0)
+    sg = ((torch.rand(I, generator=g) + 0.5) * sc).half().float()
+    su = ((torch.rand(I, generator=g) + 0.5) * sc).half().float()
+    return x, Wg, Wu, sg, su
+
+
+@pytest.mark.parametrize("M,I,K", [(256, 128, 512), (300, 100, 1024), (17, 64, 64),
+                                   (512, 704, 1024)])
+def test_gemm_w8a16_swiglu(dev, M, I, K):
+    print(f"swiglu M={M} I={I} K={K}", flush=True)
+    x, Wg, Wu, sg, su = swiglu_operands(M, I, K, M + I)
+    Wgu, sgu = ops.swiglu_pack(Wg.to(dev), Wu.to(dev), sg.to(dev), su.to(dev))
+    h = ops.gemm_w8a16_swiglu(x.to(dev), Wgu, sgu, I)
+    ref = orc.swiglu_gateup(bits(x), Wg.numpy(), Wu.numpy(), sg.numpy(), su.numpy())
+    np.testing.assert_allclose(h.float().cpu().numpy(), f32(ref), **TOL)
+
+
+@pytest.mark.parametrize("cfg", ops.w8a16_configs(swiglu=True), ids=repr)
+def test_gemm_w8a16_swiglu_every_config(dev, cfg):
+    print(f"swiglu config {cfg}", flush=True)
+    M, I, K = 300, 200, 512
+    x, Wg, Wu, sg, su = swiglu_operands(M, I, K, 9)
+    Wgu, sgu = ops.swiglu_pack(Wg.to(dev), Wu.to(dev), sg.to(dev), su.to(dev))
+    h = ops.gemm_w8a16_swiglu(x.to(dev), Wgu, sgu, I, config=cfg)
+    ref = orc.swiglu_gateup(bits(x), Wg.numpy(), Wu.numpy(), sg.numpy(), su.numpy())
+    np.testing.assert_allclose(h.float().cpu().numpy(), f32(ref), **TOL)
+
+
+def ffn_operands(T, H, I, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, H, generator=g).half()
+    gamma = (1 + 0.1 * torch.randn(H, generator=g)).half()
+    sc_h = 1.0 / np.sqrt(H * 127.0 ** 2 / 3.0)
+    sc_i = 1.0 / np.sqrt(I * 127.0 ** 2 / 3.0)
+    Wg = torch.randint(-127, 128, (I, H), generator=g, dtype=torch.int8)
+    Wu = torch.randint(-127, 128, (I, H), generator=g, dtype=torch.int8)
+    Wd = torch.randint(-127, 128, (H, I), generator=g, dtype=torch.int8)
+    sg = ((torch.rand(I, generator=g) + 0.5) * sc_h).half().float()
+    su = ((torch.rand(I, generator=g) + 0.5) * sc_h).half().float()
+    sd = ((torch.rand(H, generator=g) + 0.5) * sc_i).half().float()
+    return x, gamma, Wg, Wu, Wd, sg, su, sd
+
+
+def run_ffn(dev, x, gamma, Wg, Wu, Wd, sg, su, sd):
+    I = Wg.shape[0]
+    Wgu, sgu = ops.swiglu_pack(Wg.to(dev), Wu.to(dev), sg.to(dev), su.to(dev))
+    return ops.swiglu_ffn(x.to(dev), gamma.to(dev), Wgu, sgu, Wd.to(dev), sd.to(dev), I)
+
+
+def test_swiglu_ffn_block(dev):
+    T, H, I = 256, 512, 704
+    ops_ = ffn_operands(T, H, I, 21)
+    y = run_ffn(dev, *ops_)
+    x, gamma, Wg, Wu, Wd, sg, su, sd = ops_
+    ref = orc.swiglu_ffn(bits(x), bits(gamma), Wg.numpy(), Wu.numpy(), sg.numpy(),
+                         su.numpy(), Wd.numpy(), sd.numpy())
+    np.testing.assert_allclose(y.float().cpu().numpy(), f32(ref), rtol=1e-2, atol=2e-3)
+
+
+def test_swiglu_ffn_baseline_size_row_sample(dev):
+    """tokens 2048, hidden 4096, intermediate 11008: the whole block on the GPU,
+    the oracle on 16 sampled token rows (rows are independent in every stage)."""
+    T, H, I = 2048, 4096, 11008
+    x, gamma, Wg, Wu, Wd, sg, su, sd = ffn_operands(T, H, I, 31)
+    y = run_ffn(dev, x, gamma, Wg, Wu, Wd, sg, su, sd).float().cpu().numpy()
+    assert np.isfinite(y).all()
+    rows = np.array([0, 1, 255, 256, 511, 777, 1023, 1024, 1290, 1535, 1536, 1800, 2000,
+                     2045, 2046, 2047])
+    ref = orc.swiglu_ffn(bits(x)[rows], bits(gamma), Wg.numpy(), Wu.numpy(), sg.numpy(),
+                         su.numpy(), Wd.numpy(), sd.numpy())
+    np.testing.assert_allclose(y[rows], f32(ref), rtol=1e-2, atol=2e-3)
+
+
+def test_tune_w8a16_caches_a_verified_winner(dev):
+    import hxm
+    hxm.lib.hxm_tune_cache_clear()
+    M, N, K = 512, 1024, 512
+    x, W, s = operands(M, N, K, 41)
+    xd, Wd, sd = x.to(dev), W.to(dev), s.to(dev)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    best, rep = ops.tune_w8a16(xd, Wd, sd, out, reps=3)
+    assert rep["kind"] == "hxm-search-champion" and rep["champion"] is not None
+    assert any(c["verified"] for c in rep["configs"])
+    y = ops.gemm_w8a16(xd, Wd, sd)                       # now runs the cached winner
+    np.testing.assert_allclose(y.float().cpu().numpy(),
+                               f32(orc.gemm_w8a16(bits(x), W.numpy(), s.numpy())), **TOL)
+    I = 256
+    xs, Wg, Wu, sg, su = swiglu_operands(M, I, K, 43)
+    Wgu, sgu = ops.swiglu_pack(Wg.to(dev), Wu.to(dev), sg.to(dev), su.to(dev))
+    h = torch.empty(M, I, dtype=torch.float16, device=dev)
+    best, rep = ops.tune_w8a16(xs.to(dev), Wgu, sgu, h, swiglu=True, reps=3)
+    assert rep["champion"] is not None and best.bn // best.waves_n == 128
+    hxm.lib.hxm_tune_cache_clear()

@@ -176,6 +176,70 @@ def test_gemv_scale_is_per_output_channel():
     assert np.array_equal(y, np.array([[32.0, 64.0, 16.0]], dtype=np.float32))
 
 
+def test_gemm_w8a16_vs_numpy_f64_and_small_integer_kat():
+    rng = np.random.default_rng(4)
+    x = h(rng.standard_normal((9, 80)))
+    W = rng.integers(-127, 128, (13, 80)).astype(np.int8)
+    sc = rng.uniform(0.001, 0.02, 13).astype(np.float32)
+    y = orc.f16_bits_to_f32(orc.gemm_w8a16(x, W, sc))
+    ref = (orc.f16_bits_to_f32(x).astype(np.float64) @ W.T.astype(np.float64)) * sc
+    np.testing.assert_allclose(y, ref, rtol=2 ** -10, atol=1e-6)   # within ~1 f16 ulp
+    # small integers: exact sums -> bit-exact against the float64 product
+    xs = h(rng.integers(-4, 5, (6, 256)))
+    Ws = rng.integers(-8, 9, (7, 256)).astype(np.int8)
+    s8 = np.full(7, 0.125, np.float32)
+    exact = (orc.f16_bits_to_f32(xs).astype(np.float64) @ Ws.T.astype(np.float64)) * 0.125
+    assert np.array_equal(orc.f16_bits_to_f32(orc.gemm_w8a16(xs, Ws, s8)), exact)
+    # the scale belongs to the output channel (a transposed scale fails this)
+    y3 = orc.f16_bits_to_f32(orc.gemm_w8a16(h(np.ones((1, 32))), np.ones((3, 32), np.int8),
+                                            np.array([1.0, 2.0, 0.5], np.float32)))
+    assert np.array_equal(y3, np.array([[32.0, 64.0, 16.0]], np.float32))
+
+
+def test_swiglu_gateup_vs_numpy_f64_and_limits():
+    rng = np.random.default_rng(5)
+    K = 64
+    x = h(rng.standard_normal((5, K)))
+    Wg = rng.integers(-127, 128, (11, K)).astype(np.int8)
+    Wu = rng.integers(-127, 128, (11, K)).astype(np.int8)
+    sg = rng.uniform(0.001, 0.003, 11).astype(np.float32)
+    su = rng.uniform(0.001, 0.003, 11).astype(np.float32)
+    hh = orc.f16_bits_to_f32(orc.swiglu_gateup(x, Wg, Wu, sg, su))
+    xf = orc.f16_bits_to_f32(x).astype(np.float64)
+    g = (xf @ Wg.T.astype(np.float64)) * sg
+    u = (xf @ Wu.T.astype(np.float64)) * su
+    ref = g / (1.0 + np.exp(-g)) * u
+    np.testing.assert_allclose(hh, ref, rtol=2 ** -9, atol=1e-6)
+    # limits: g = 0 -> 0; g >> 0 -> g * u; g << 0 -> 0 (gate and up swapped fail these)
+    one = h(np.ones((1, 16)))
+    Wz = np.zeros((3, 16), np.int8)
+    Wp = np.full((3, 16), 100, np.int8)
+    Wun = np.ones((3, 16), np.int8)
+    s1 = np.ones(3, np.float32)
+    assert np.all(orc.f16_bits_to_f32(orc.swiglu_gateup(one, Wz, Wun, s1, s1)) == 0)
+    big = orc.f16_bits_to_f32(orc.swiglu_gateup(one, Wp, Wun, s1, s1))
+    assert np.array_equal(big, np.full((1, 3), 1600.0 * 16.0, np.float32))
+    neg = orc.f16_bits_to_f32(orc.swiglu_gateup(one, -Wp, Wun, s1, s1))
+    assert np.all(np.abs(neg) < 1e-30)
+
+
+def test_swiglu_ffn_composes_the_stages():
+    rng = np.random.default_rng(6)
+    T, H, I = 4, 32, 48
+    x = h(rng.standard_normal((T, H)))
+    gamma = h(1 + 0.1 * rng.standard_normal(H))
+    Wg = rng.integers(-127, 128, (I, H)).astype(np.int8)
+    Wu = rng.integers(-127, 128, (I, H)).astype(np.int8)
+    Wd = rng.integers(-127, 128, (H, I)).astype(np.int8)
+    sg = np.full(I, 0.003, np.float32)
+    su = np.full(I, 0.002, np.float32)
+    sd = np.full(H, 0.004, np.float32)
+    y = orc.swiglu_ffn(x, gamma, Wg, Wu, sg, su, Wd, sd)
+    xn = orc.rmsnorm_rows(x, gamma, 1e-6, "f16")
+    hh = orc.swiglu_gateup(xn, Wg, Wu, sg, su)
+    assert np.array_equal(y, orc.gemm_w8a16(hh, Wd, sd))
+
+
 # ---- row reductions ----------------------------------------------------------------
 
 def test_softmax_golden_and_invariants(golden):

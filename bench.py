@@ -11,13 +11,15 @@ tera-ops/s (int8 ops are counted like flops in the roofline's TFLOP/s slot).
 Also reported under "extra" (not the headline): the int32-output int8 GEMM,
 the fp16 256^3 matmul (launch-bound), W8A16 GEMV M in {1,4,16} and softmax /
 RMSNorm rows on f16 [8192 x 4096] (HBM-bound: timed while rotating buffer
-sets larger than the 256 MB Infinity Cache).
+sets larger than the 256 MB Infinity Cache), the SwiGLU FFN block (tokens
+2048, hidden 4096, intermediate 11008; tiles autotuned per GEMM) and a plain
+256 MiB device copy (the practical HBM copy rate next to the nominal peak).
 
 cpu_baseline: the C restatement in oracle/ (OpenMP over the host cores)
 timed on a bounded row sample of the same GEMM.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-       python bench.py --only {int8,int8_i32,f16,gemv,rows,copy}  (one workload,
+       python bench.py --only {int8,int8_i32,f16,gemv,rows,ffn,copy}  (one workload,
        for rocprofv3 runs; prints that workload's record)
 """
 from __future__ import annotations
@@ -178,6 +180,67 @@ def run_rows(c):
     return out
 
 
+def run_ffn(c):
+    """the SwiGLU FFN block, tokens 2048, hidden 4096,
+    intermediate 11008.  RMSNorm (eps 1e-6) -> fused gate/up W8A16 GEMM with
+    SiLU * mul -> down W8A16 GEMM; fp16 activations N(0,1), int8 weights
+    U{-127..127} with per-channel scales.  Each GEMM's tile is autotuned on
+    these operands first (outside the timed region); a step is the whole
+    block."""
+    import math
+    torch, hxm, L, ops = c.torch, c.hxm, c.L, c.ops
+    T, H, I = 2048, 4096, 11008
+    x = torch.randn(T, H, device=c.dev).half()
+    gamma = (1 + 0.1 * torch.randn(H, device=c.dev)).half()
+    Wg = torch.randint(-127, 128, (I, H), dtype=torch.int8, device=c.dev)
+    Wu = torch.randint(-127, 128, (I, H), dtype=torch.int8, device=c.dev)
+    Wd = torch.randint(-127, 128, (H, I), dtype=torch.int8, device=c.dev)
+    sc_h, sc_i = 1 / math.sqrt(H * 127 ** 2 / 3), 1 / math.sqrt(I * 127 ** 2 / 3)
+    sg = ((torch.rand(I, device=c.dev) + 0.5) * sc_h).half().float()
+    su = ((torch.rand(I, device=c.dev) + 0.5) * sc_h).half().float()
+    sd = ((torch.rand(H, device=c.dev) + 0.5) * sc_i).half().float()
+    Wgu, sgu = ops.swiglu_pack(Wg, Wu, sg, su)
+    xn = torch.empty_like(x)
+    h = torch.empty(T, I, dtype=torch.float16, device=c.dev)
+    y = torch.empty(T, H, dtype=torch.float16, device=c.dev)
+    ops.rms_norm(x, (H,), gamma, eps=1e-6, out=xn)
+    cfg_gu, _ = ops.tune_w8a16(xn, Wgu, sgu, h, swiglu=True, reps=5)
+    cfg_d, _ = ops.tune_w8a16(h, Wd, sd, y, reps=5)
+    st = c.stream
+    px, pg, pxn, ph, py = x.data_ptr(), gamma.data_ptr(), xn.data_ptr(), h.data_ptr(), y.data_ptr()
+    pgu, psgu, pwd, psd = Wgu.data_ptr(), sgu.data_ptr(), Wd.data_ptr(), sd.data_ptr()
+
+    def norm(_):
+        hxm.check(L.hxm_rmsnorm_rows(px, H, pg, pxn, H, T, H, 1e-6, hxm.F16, st),
+                  "hxm_rmsnorm_rows")
+
+    def gateup(_):
+        hxm.check(L.hxm_gemm_w8a16_swiglu(pxn, H, pgu, psgu, ph, I, T, I, H, None, st),
+                  "hxm_gemm_w8a16_swiglu")
+
+    def down(_):
+        hxm.check(L.hxm_gemm_w8a16(ph, I, pwd, I, psd, py, H, T, H, I, None, st),
+                  "hxm_gemm_w8a16")
+
+    def block(i):
+        norm(i), gateup(i), down(i)
+    steps, warm = 50, 5
+    t_blk, _ = c.time_ms(block, steps, warm)
+    t_norm, _ = c.time_ms(norm, steps, warm)
+    t_gu, _ = c.time_ms(gateup, steps, warm)
+    t_d, _ = c.time_ms(down, steps, warm)
+    f_gu, f_d = 2.0 * T * H * (2 * I), 2.0 * T * I * H
+    flops = f_gu + f_d
+    tf = flops / (t_blk * 1e-3) / 1e12
+    return {"swiglu_ffn_2048x4096x11008": {
+        "us": t_blk * 1e3, "TFLOPS": tf, "mfma_frac": tf / PEAK_F16_TFLOPS,
+        "gemm_flops": flops,
+        "stages_us": {"rmsnorm": t_norm * 1e3, "gate_up_swiglu": t_gu * 1e3, "down": t_d * 1e3},
+        "stage_TFLOPS": {"gate_up_swiglu": f_gu / (t_gu * 1e-3) / 1e12,
+                         "down": f_d / (t_d * 1e-3) / 1e12},
+        "tuned": {"gate_up_swiglu": list(cfg_gu.as_tuple()), "down": list(cfg_d.as_tuple())}}}
+
+
 def run_copy(c):
     """A plain 256 MiB device copy (torch's elementwise copy kernel): the
     known-size reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE."""
@@ -277,7 +340,7 @@ def main() -> int:
                     help="approximate CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=["int8", "int8_i32", "f16", "gemv", "rows", "copy"])
+    ap.add_argument("--only", choices=["int8", "int8_i32", "f16", "gemv", "rows", "ffn", "copy"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build is the single-GPU kernel set of the hot "
@@ -290,7 +353,8 @@ def main() -> int:
         if args.only in ("int8", "int8_i32"):
             rec = {args.only: run_int8(c, *int8_operands(c), out_i32=args.only == "int8_i32")}
         else:
-            rec = {"f16": run_f16, "gemv": run_gemv, "rows": run_rows, "copy": run_copy}[
+            rec = {"f16": run_f16, "gemv": run_gemv, "rows": run_rows, "ffn": run_ffn,
+                   "copy": run_copy}[
                 args.only](c)
         print(json.dumps(rec), flush=True)
         return 0
@@ -303,7 +367,7 @@ def main() -> int:
     extra = {}
     if not args.no_extra:
         extra["int8_gemm_i32_out_4096"] = run_int8(c, A, Bp, rs, cs, out_i32=True)
-        for fn in (run_f16, run_gemv, run_rows):
+        for fn in (run_f16, run_gemv, run_rows, run_ffn, run_copy):
             extra.update(fn(c))
         for k, v in extra.items():
             log(k, json.dumps(v))

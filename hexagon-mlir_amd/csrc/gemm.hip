@@ -1,675 +1,15 @@
-// MFMA GEMMs on gfx950: int8 x int8 -> int32 (exact) and f16/bf16 -> fp32.
-//
-// Reference path: linalg.matmul lowered by matmul-to-hmx -> hmx-partition ->
-// weight-resident (qcom_hexagon_backend/lib/Dialect/Hmx/Transforms/
-// HmxPartitionPass.cpp:783-864: for m-tiles { pack A row-tile; for n-tiles
-// { clear acc; K batches of mma; read-out } }, weights resident across m), the
-// activation staging ring of depth 1/2 (HmxPartitionPass.cpp:253), and the
-// leaves hmx_mma_f16 / hmx_acc_store_f16 (bin/runtime/hmx/src/HMXAPI.c:36-55).
-//
-// GPU form.  C[M,N] = A[M,K] . B^T where B is the resident [N,K] image (K
-// contiguous), so both operands stream K-contiguous 16-byte chunks.
-//   * workgroup tile BM x BN; K is staged BKB bytes at a time (64 or 128) in
-//     STAGES LDS buffers, each its own __shared__ array.  Stage s+STAGES-1 is
-//     fetched by LDS-DMA (buffer_load_dwordx4 ... lds) while stage s feeds the
-//     MFMAs; an exact s_waitcnt vmcnt(N) waits for the oldest stage only.
-//     Because every buffer is a distinct object, the compiler can prove the
-//     DMA into one buffer does not alias the ds_reads of another and does not
-//     add a full vmcnt(0) drain before them;
-//   * the loads use a buffer resource per operand: each lane's 32-bit offset
-//     (row * ld + chunk * 16) is computed once and the K position rides in the
-//     scalar offset, so a stage costs no per-lane address arithmetic.  Rows
-//     past M / N use an offset beyond the resource's range and read as zero,
-//     as do K chunks past K (last stage only);
-//   * LDS rows are BKB bytes, 16-byte chunks XOR-swizzled per row so the 16
-//     lanes of a ds_read_b128 phase hit distinct banks;
-//   * each wave owns a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks
-//     (v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x16_{f16,bf16}; both take 32
-//     bytes of K per row per instruction, 16 per lane).  Fragments of k-step
-//     ks+1 are read while the MFMAs of ks issue.  The B tile is the MFMA's
-//     first operand, so each lane ends with 4 CONSECUTIVE output columns per
-//     register group: the epilogue stores 8 (f16) or 16 (int32) bytes per lane;
-//   * the tile order is XCD-aware: workgroups are dispatched round-robin over
-//     the 8 XCDs, so consecutive tile ids are remapped onto one XCD and walked
-//     in groups of 4 tile-rows, keeping each XCD's A rows and B columns in its
-//     own L2;
-//   * epilogues: int32 (optionally += C, wrapping), fp32 -> {f16, bf16, f32}
-//     (optionally += C, one rounding), or the int8 dequant
-//     f16(((float)acc * row_scale) * col_scale).
+// Host side of the MFMA GEMMs: the compiled-config tables, kernel choice
+// (tuned winner, else a default per shape), argument validation, the [K,N]
+// weight pack and the extern "C" entry points.  The kernels themselves are
+// in gemm_kernel.h, instantiated by gemm_i8.hip, gemm_f16.hip and
+// gemm_w8.hip.
 #include <cstring>
-#include <type_traits>
 #include <mutex>
 #include <vector>
 
-#include "device_util.h"
-#include "gemm_configs.h"
-#include "hxm_internal.h"
+#include "gemm_kernel.h"
 
 namespace hxm {
-
-constexpr uint32_t kOob = 0x80000000u;  // an offset past every resource's range
-
-template <int BKB>
-__device__ __forceinline__ int swz(int row) {
-  if constexpr (BKB == 128)
-    return (row & 7) ^ ((row >> 3) & 1);  // 8 chunks per row
-  else
-    return ((row >> 1) & 3) ^ ((row >> 3) & 1);  // 4 chunks per row
-}
-
-enum Epilogue {
-  kEpiI32 = 0,      // int32 out (accumulate flag honoured)
-  kEpiDequant = 1,  // int8: f16(((float)acc * rs[m]) * cs[n])
-  kEpiFloat = 2,    // f16/bf16: fp32 acc -> out dtype (accumulate honoured)
-  kEpiW8 = 3,       // f16 A x int8 B: f16(acc * cs[n])
-  kEpiSwiglu = 4    // f16 A x int8 gate/up image: f16(silu(g * sg) * (u * su))
-};
-
-// The int8-weight epilogues take B as int8 [N, K] converted to f16 in
-// registers (the W8A16 GEMM of the SwiGLU FFN).
-constexpr bool b_is_int8(int epi) { return epi == kEpiW8 || epi == kEpiSwiglu; }
-constexpr int32_t kOpW8 = HXM_OP_W8A16, kOpSwiglu = HXM_OP_W8A16_SWIGLU;  // tuning-cache keys
-
-struct GemmArgs {
-  const uint8_t* A;  // [M, K] row-major, lda_bytes
-  const uint8_t* B;  // [N, K] row-major, ldb_bytes
-  void* C;
-  int64_t lda_bytes, ldb_bytes, ldc;  // ldc in elements
-  int M, N, K_bytes;
-  int accumulate;
-  int out_dtype;  // HXM_I32, HXM_F16, HXM_BF16, HXM_F32
-  int vec_store;  // C rows allow 4-element vector stores
-  int vec8_store; // C rows allow 8-element (16-byte f16) vector stores
-  const float* row_scale;
-  const float* col_scale;
-  int group_m;  // tile-rows per group in the XCD walk
-  int n_out;    // kEpiSwiglu: output columns (gate/up channel count)
-};
-
-template <typename T>
-struct Mfma;
-
-template <>
-struct Mfma<int8_t> {
-  typedef v16i32 acc_t;
-  __device__ static __forceinline__ acc_t run(v4i32 a, v4i32 b, acc_t c) {
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma<_Float16> {
-  typedef v16f32 acc_t;
-  __device__ static __forceinline__ acc_t run(v4i32 a, v4i32 b, acc_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8f16, a),
-                                                  __builtin_bit_cast(v8f16, b),
-                                                  c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma<__bf16> {
-  typedef v16f32 acc_t;
-  __device__ static __forceinline__ acc_t run(v4i32 a, v4i32 b, acc_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-        __builtin_bit_cast(v8bf16, a), __builtin_bit_cast(v8bf16, b), c, 0, 0, 0);
-  }
-};
-
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Waits until at most N of this wave's LDS-DMA loads are in flight and all
-// its LDS reads are done, then joins the workgroup barrier.  __syncthreads()
-// would also drain every outstanding load (vmcnt(0)) and so discard the
-// prefetch; the memory clobber keeps the compiler from moving LDS accesses
-// across the barrier.
-template <int N>
-__device__ __forceinline__ void wait_and_barrier() {
-  static_assert(N >= 0 && N <= 63, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
-// Buffer resource over rows [row0, rows_valid) of a K-major operand
-// (gfx9 descriptor: 48-bit base, stride 0, num_records in bytes, data format
-// word 0x00020000).  Offsets at or past num_records read as zero.
-__device__ __forceinline__ v4i32 operand_rsrc(const uint8_t* base, int64_t ld_bytes,
-                                              int row0, int rows_valid) {
-  const int64_t rows = rows_valid > row0 ? rows_valid - row0 : 0;
-  int64_t bytes = rows * ld_bytes;
-  if (bytes > 0x7fffffff) bytes = 0x7fffffff;
-  const uint64_t a = reinterpret_cast<uint64_t>(base + static_cast<int64_t>(row0) * ld_bytes);
-  v4i32 r;
-  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
-  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>((a >> 32) & 0xffffu));
-  r[2] = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
-  r[3] = 0x00020000;
-  return r;
-}
-
-// One LDS-DMA: 16 bytes per lane from rsrc at voffset + soffset into LDS at
-// lds + lane*16.  Issued as inline asm so that the compiler's waitcnt pass
-// does not track it: every wait on these loads is the kernel's own
-// (wait_and_barrier).  Compiler-issued loads stay correct regardless, since
-// vmcnt counts in issue order and extra loads in flight only make the
-// compiler's own waits stricter.
-__device__ __forceinline__ void dma16(uint8_t* lds, v4i32 rsrc, uint32_t voffset, int soffset) {
-  // The LDS base (M0) and the scalar offset are wave-uniform by construction.
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)lds)));
-  soffset = __builtin_amdgcn_readfirstlane(soffset);
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "buffer_load_dwordx4 %1, %2, %3 offen lds"
-      :
-      : "s"(m0), "v"(voffset), "s"(rsrc), "s"(soffset)
-      : "memory", "m0");
-}
-
-// Per-lane offsets of one operand's stage loads.  Wave instruction q covers
-// LDS bytes [q*1024, q*1024+1024): lane l fills the 16 bytes of LDS row
-// q*RPI + l/CH, slot l%CH, which hold source chunk slot ^ swz(row).
-template <int ROWS, int BKB, int NW>
-struct StageLoad {
-  static constexpr int CH = BKB / 16;
-  static constexpr int RPI = 64 / CH;               // LDS rows per wave instruction
-  static constexpr int L = ROWS / RPI / NW;         // instructions per wave per stage
-  static_assert(L >= 1 && (ROWS / RPI) % NW == 0, "tile rows must split over waves");
-  uint32_t off[L];
-
-  // LDS row and source chunk (16-byte unit within the row's BKB bytes) that
-  // lane fills in instruction i.
-  __device__ static __forceinline__ int row_of(int i, int wave, int lane) {
-    return (i * NW + wave) * RPI + lane / CH;
-  }
-  __device__ static __forceinline__ int chunk_of(int i, int wave, int lane) {
-    return (lane % CH) ^ swz<BKB>(row_of(i, wave, lane));
-  }
-
-  __device__ __forceinline__ void init(int64_t ld_bytes, int rows_left, int wave, int lane) {
-#pragma unroll
-    for (int i = 0; i < L; ++i) {
-      const int row = row_of(i, wave, lane);
-      off[i] = row < rows_left ? static_cast<uint32_t>(row * ld_bytes + chunk_of(i, wave, lane) * 16)
-                               : kOob;
-    }
-  }
-
-  // Instruction i of a stage at K byte kb0; 16-byte chunks at or past
-  // K_bytes read as zero (only the last stage can straddle the end of K).
-  // The chunk is recomputed (a few VALU operations under the MFMAs) rather
-  // than kept in a register per instruction.
-  template <int I>
-  __device__ __forceinline__ void issue_one(v4i32 r, uint8_t* lds, int wave, int lane, int kb0,
-                                            int K_bytes) const {
-    const uint32_t o = kb0 + chunk_of(I, wave, lane) * 16 < K_bytes ? off[I] : kOob;
-    dma16(lds + (I * NW + wave) * 1024, r, o, kb0);
-  }
-};
-
-// One LDS-DMA of 4 bytes per lane: rsrc at voffset into LDS at lds + lane*4.
-__device__ __forceinline__ void dma4(float* lds, v4i32 rsrc, uint32_t voffset) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)lds)));
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "buffer_load_dword %1, %2, 0 offen lds"
-      :
-      : "s"(m0), "v"(voffset), "s"(rsrc)
-      : "memory", "m0");
-}
-
-// Calls f(integral_constant<int, I>) for I = B .. E-1, so every index inside
-// f is a compile-time constant (register arrays stay in registers).
-template <int B, int E, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
-}
-
-template <int BKB>
-__device__ __forceinline__ v4i32 lds_frag(const uint8_t* lds, int row, int chunk) {
-  return *reinterpret_cast<const v4i32*>(lds + row * BKB + ((chunk ^ swz<BKB>(row)) << 4));
-}
-
-template <typename T, int BM, int BN, int BKB, int STAGES, int WM, int WN, int EPI>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
-  constexpr int NW = WM * WN;
-  constexpr int TM = BM / WM, TN = BN / WN;  // wave sub-tile
-  constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 blocks per wave
-  constexpr int KS = BKB / 32;               // MFMA k-steps per stage
-  constexpr bool BQ = b_is_int8(EPI);        // B int8, converted to f16 in registers
-  constexpr int BKB_B = BQ ? BKB / 2 : BKB;  // B bytes per LDS row
-  constexpr int SB = BM * BKB + BN * BKB_B;  // bytes per stage
-  constexpr int NF = FM * FN;                // MFMA slots per k-step
-  constexpr int NR = FM + FN;                // fragment reads per k-step
-  constexpr int HALF = NF / 2;               // barrier slot of the last k-step
-  constexpr int PB = (KS - 1) * NF + HALF;   // slots of a stage before its barrier
-  static_assert(FM >= 1 && FN >= 1, "wave tile must hold a 32x32 block");
-  static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
-  static_assert(KS % 2 == 0, "fragment double buffer assumes an even k-step count");
-  using acc_t = typename Mfma<T>::acc_t;
-  using LA = StageLoad<BM, BKB, NW>;
-  using LB = StageLoad<BN, BKB_B, NW>;
-  constexpr int LPW = LA::L + LB::L;  // DMA instructions per wave per stage
-  static_assert(!BQ || std::is_same<T, _Float16>::value, "int8 B pairs with f16 A");
-  static_assert(EPI != kEpiSwiglu || TN == 128, "SwiGLU image interleaves 64-channel blocks");
-  // Epilogue scales in LDS: rows [0, QR*64), columns [QR*64, (QR+QC)*64) floats.
-  constexpr int QR = EPI == kEpiDequant ? (BM + 63) / 64 : 0;
-  constexpr int QC = EPI == kEpiDequant || BQ ? (BN + 63) / 64 : 0;
-
-  // One __shared__ object per stage (see the header comment).
-  __shared__ __attribute__((aligned(1024))) uint8_t s0[SB];
-  __shared__ __attribute__((aligned(1024))) uint8_t s1[SB];
-  __shared__ __attribute__((aligned(1024))) uint8_t s2[STAGES > 2 ? SB : 1024];
-  __shared__ __attribute__((aligned(1024))) uint8_t s3[STAGES > 3 ? SB : 1024];
-  __shared__ __attribute__((aligned(16))) float ssc[QR + QC > 0 ? (QR + QC) * 64 : 4];
-  auto buf = [&](int u) -> uint8_t* {
-    return u == 0 ? s0 : u == 1 ? s1 : u == 2 ? s2 : s3;
-  };
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform
-  const int wm = wave / WN, wn = wave % WN;
-
-  // ---- XCD-aware tile order ----
-  const int tiles_m = (g.M + BM - 1) / BM;
-  const int tiles_n = (g.N + BN - 1) / BN;
-  const int ntiles = tiles_m * tiles_n;
-  int t = blockIdx.x;
-  if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
-  const int gm = g.group_m;
-  const int per_group = gm * tiles_n;
-  const int group = t / per_group;
-  const int first_m = group * gm;
-  const int gsize = min(tiles_m - first_m, gm);
-  const int tm = first_m + (t % per_group) % gsize;
-  const int tn = (t % per_group) / gsize;
-  const int m0 = tm * BM, n0 = tn * BN;
-
-  const v4i32 ra = operand_rsrc(g.A, g.lda_bytes, m0, g.M);
-  const v4i32 rb = operand_rsrc(g.B, g.ldb_bytes, n0, g.N);
-  LA la;
-  LB lb;
-  la.init(g.lda_bytes, g.M - m0, wave, lane);
-  lb.init(g.ldb_bytes, g.N - n0, wave, lane);
-
-  // The tile's epilogue scales go to LDS by DMA ahead of the first stage, so
-  // they arrive under the prologue and cost the epilogue one LDS read each.
-  // Scales of rows / columns outside C read as zero.
-  if constexpr (QR + QC > 0) {
-    const v4i32 rr = QR ? operand_rsrc(reinterpret_cast<const uint8_t*>(g.row_scale), 4, m0, g.M)
-                        : v4i32{};
-    const v4i32 rc = operand_rsrc(reinterpret_cast<const uint8_t*>(g.col_scale), 4, n0, g.N);
-    for (int q = wave; q < QR + QC; q += NW) {
-      if (q < QR) dma4(ssc + q * 64, rr, (q * 64 + lane) * 4);
-      else dma4(ssc + q * 64, rc, ((q - QR) * 64 + lane) * 4);
-    }
-  }
-
-  acc_t acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = acc_t{};
-
-  const int KT = (g.K_bytes + BKB - 1) / BKB;
-  const int K_bytes = g.K_bytes;                    // of A
-  const int K_bytes_B = BQ ? K_bytes / 2 : K_bytes;  // of B
-
-  // DMA instruction D (A's first, then B's) of the stage at A byte kb0.
-  auto dma = [&](auto D, uint8_t* dst, int kb0) {
-    constexpr int d = decltype(D)::value;
-    if constexpr (d < LA::L) {
-      la.template issue_one<d>(ra, dst, wave, lane, kb0, K_bytes);
-    } else {
-      const int kb0_b = BQ ? kb0 / 2 : kb0;
-      lb.template issue_one<d - LA::L>(rb, dst + BM * BKB, wave, lane, kb0_b, K_bytes_B);
-    }
-  };
-  auto issue_stage = [&](int kt, uint8_t* dst) {
-    static_for<0, LPW>([&](auto D) { dma(D, dst, kt * BKB); });
-  };
-
-  // Fragments of the k-step being multiplied ([ks & 1]) and of the next one.
-  // Read R of a k-step: A block 0, the FN B blocks, then A blocks 1..FM-1 --
-  // the order the MFMA slots (i, j) = (s / FN, s % FN) first need them.
-  // With an int8 B the read brings the lane's 8 bytes (K range
-  // [16ks + 8hi, +8) of its row) into braw, and cvt_b turns them into the f16
-  // fragment one MFMA slot before its first use.
-  v4i32 af[2][FM], bf[2][FN];
-  uint2 braw[2][BQ ? FN : 1];
-  const int r32 = lane & 31, hi = lane >> 5;
-  auto read = [&](auto R, int dstb, const uint8_t* stage, int ks) {
-    constexpr int r = decltype(R)::value;
-    constexpr bool is_b = r >= 1 && r <= FN;
-    constexpr int idx = r == 0 ? 0 : is_b ? r - 1 : r - FN;
-    if constexpr (is_b && BQ) {
-      const int row = idx * 32 + r32;
-      braw[dstb][idx] = *reinterpret_cast<const uint2*>(
-          stage + BM * BKB + (wn * TN + row) * BKB_B + ((ks ^ swz<BKB_B>(row)) << 4) + hi * 8);
-    } else if constexpr (is_b) {
-      bf[dstb][idx] = lds_frag<BKB>(stage + (BM + wn * TN) * BKB, idx * 32 + r32, ks * 2 + hi);
-    } else {
-      af[dstb][idx] = lds_frag<BKB>(stage + (wm * TM) * BKB, idx * 32 + r32, ks * 2 + hi);
-    }
-  };
-  auto cvt_b = [&](int b, int j) {
-    if constexpr (BQ) bf[b][j] = __builtin_bit_cast(v4i32, i8x8_to_f16(braw[b][j].x, braw[b][j].y));
-  };
-
-  // Every stage slot issues its DMAs, also past the end of K: a stage at or
-  // past K_bytes reads zeros (see issue_one) into a buffer no later stage
-  // uses, so the number of stages in flight is the same at every wait and
-  // the instruction stream has no branches for the compiler's waitcnt
-  // analysis to merge.
-
-  // DMA schedule.  Stage j goes to buffer j % STAGES, which is free from the
-  // barrier of iteration j-STAGES on (every read of stage j-STAGES precedes
-  // that barrier) and must have landed at the barrier of iteration j-1.
-  // Instruction d of stage j issues at position dv(d) of iteration
-  // j-STAGES+1, counted from its first slot; a negative position is a slot
-  // after the barrier of the iteration before.  With two stages the
-  // instructions are packed into the first two thirds of the window so the
-  // last ones land before the wait; with more stages they are spread over
-  // the whole window.
-  constexpr int SLOTS = KS * NF;             // MFMA slots per stage
-  constexpr int POST = SLOTS - PB;           // slots after the barrier
-  constexpr int DW = STAGES == 2 ? (2 * SLOTS) / 3 : SLOTS;
-  static_assert(((LPW - 1) * DW) / LPW - POST < PB, "DMA window ends before the barrier");
-  constexpr int NEG = [] {                   // instructions issued a stage early
-    int n = 0;
-    for (int d = 0; d < LPW; ++d) n += (d * DW) / LPW - POST < 0;
-    return n;
-  }();
-  static_assert((STAGES - 2) * LPW + NEG <= 63, "vmcnt range");
-
-  // One stage.  Its KS*NF MFMA slots run in a fixed order (a scheduling
-  // barrier closes each slot).  Spread over the slots: the DMA instructions
-  // (above), and the fragment reads of k-step ks+1.  At slot HALF of the
-  // last k-step the wave waits for stage kt+1 (stages kt+2 .. kt+STAGES-1 may
-  // stay in flight); the barrier also tells it that every wave is done
-  // reading stage kt, whose buffer the early DMAs of stage kt+STAGES then
-  // refill.  It then reads stage kt+1's first fragments under the remaining
-  // MFMAs.
-  auto stage = [&](auto U, int kt) {
-    constexpr int u = decltype(U)::value;
-    const uint8_t* cur = buf(u);
-    const uint8_t* nxt = buf((u + 1) % STAGES);
-    uint8_t* dbuf = buf((u + STAGES - 1) % STAGES);  // stage kt+STAGES-1
-    uint8_t* ebuf = buf(u);                          // stage kt+STAGES (early part)
-    const int kbd = (kt + STAGES - 1) * BKB;
-    static_for<0, KS>([&](auto KSI) {
-      constexpr int ks = decltype(KSI)::value;
-      constexpr int cb = ks & 1;
-      static_for<0, NF>([&](auto SI) {
-        constexpr int sl = decltype(SI)::value;
-        constexpr int slot = ks * NF + sl;
-        if constexpr (ks == KS - 1 && sl == HALF) wait_and_barrier<(STAGES - 2) * LPW>();
-        static_for<0, LPW>([&](auto D) {
-          constexpr int v = (decltype(D)::value * DW) / LPW - POST;
-          if constexpr (v >= 0 && v == slot) dma(D, dbuf, kbd);
-          if constexpr (v < 0 && SLOTS + v == slot) dma(D, ebuf, kbd + BKB);
-        });
-        static_for<0, NR>([&](auto R) {
-          constexpr int r = decltype(R)::value;
-          if constexpr (ks < KS - 1) {
-            if constexpr ((r * NF) / NR == sl) read(R, cb ^ 1, cur, ks + 1);
-          } else {
-            if constexpr (HALF + (r * (NF - HALF)) / NR == sl) read(R, cb ^ 1, nxt, 0);
-          }
-        });
-        constexpr int i = sl / FN, j = sl % FN;
-        acc[i][j] = Mfma<T>::run(bf[cb][j], af[cb][i], acc[i][j]);
-        // int8 B: convert fragment sl+1 of this k-step under this MFMA, and
-        // fragment 0 of the next k-step under the last one.
-        if constexpr (BQ && sl + 1 < FN) cvt_b(cb, sl + 1);
-        if constexpr (BQ && sl == NF - 1) cvt_b(cb ^ 1, 0);
-        __builtin_amdgcn_sched_barrier(0);
-      });
-    });
-  };
-
-  if (KT > 0) {
-    // Prologue: stages 0 .. STAGES-2, the early part of stage STAGES-1, then
-    // the first k-step's fragments.
-    static_for<0, STAGES - 1>([&](auto Pi) {
-      issue_stage(decltype(Pi)::value, buf(decltype(Pi)::value));
-    });
-    static_for<0, LPW>([&](auto D) {
-      if constexpr ((decltype(D)::value * DW) / LPW - POST < 0)
-        dma(D, buf(STAGES - 1), (STAGES - 1) * BKB);
-    });
-    wait_and_barrier<(STAGES - 2) * LPW + NEG>();
-    static_for<0, NR>([&](auto R) { read(R, 0, buf(0), 0); });
-    cvt_b(0, 0);
-
-    // Main loop, unrolled by STAGES so every buffer choice is static.
-    for (int kt0 = 0; kt0 < KT; kt0 += STAGES) {
-      static_for<0, STAGES>([&](auto U) {
-        const int kt = kt0 + decltype(U)::value;
-        if (kt < KT) stage(U, kt);
-      });
-    }
-  }
-
-  // ---- epilogue ----
-  // Lane l holds, for block (i, j) and register group q = v/4, row
-  // m = i*32 + l%32 of the wave tile and the four consecutive columns
-  // j*32 + 8q + 4*(l/32) + 0..3.  The tile is written through LDS one 32-row
-  // block at a time: each lane stages its 4-element runs as 32-bit words
-  // (int32, or the fp32 accumulator) in a padded [32][TN+4] array, and the
-  // wave reads back row-contiguous 16-byte runs, applies the output
-  // conversion (the dequant scales come from LDS) and stores whole rows.
-  // Keeping the register-to-LDS copy a plain move keeps the accumulators in
-  // AGPRs through the epilogue.
-  constexpr int kPad = TN + 4;                 // staging row stride (words)
-  constexpr int kStageWords = 32 * kPad;       // one wave's 32-row block
-  constexpr int kWavesPerBuf = (NW + STAGES - 1) / STAGES;
-  static_assert(kWavesPerBuf * kStageWords * 4 <= SB, "epilogue staging must fit a stage");
-  const int mw = m0 + wm * TM, nw = n0 + wn * TN;
-
-  wait_and_barrier<0>();  // stage buffers free; scales landed and visible
-  float* stg = reinterpret_cast<float*>(buf(wave % STAGES)) + (wave / STAGES) * kStageWords;
-
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    // 1. registers -> LDS (row r32, 4 consecutive columns per group)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        v4f32 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if constexpr (EPI == kEpiFloat || BQ) {
-            w[e] = acc[i][j][q * 4 + e];
-          } else {
-            // int32 bits.  Copy the element out first: clang lowers
-            // __builtin_bit_cast of an ext-vector element expression as a
-            // read of element 0.
-            const int32_t a = acc[i][j][q * 4 + e];
-            w[e] = __builtin_bit_cast(float, a);
-          }
-        }
-        *reinterpret_cast<v4f32*>(stg + r32 * kPad + j * 32 + q * 8 + hi * 4) = w;
-      }
-    // 2. LDS -> global.  The dequant output takes 8 consecutive f16 of one
-    // row per lane (16-byte stores); the other outputs 4 elements per lane.
-    if constexpr (EPI == kEpiDequant) {
-      constexpr int kRuns8 = 32 * TN / 8, kRunsPerRow8 = TN / 8;
-      static_assert(kRuns8 % 64 == 0, "8-element runs must fill the wave");
-#pragma unroll
-      for (int it = 0; it < kRuns8 / 64; ++it) {
-        const int run = it * 64 + lane;
-        const int row = run / kRunsPerRow8, col = (run % kRunsPerRow8) * 8;
-        const v4f32 w0 = *reinterpret_cast<const v4f32*>(stg + row * kPad + col);
-        const v4f32 w1 = *reinterpret_cast<const v4f32*>(stg + row * kPad + col + 4);
-        const int m = mw + i * 32 + row, n = nw + col;
-        if (m >= g.M || n >= g.N) continue;
-        // fp32, left to right, each product rounded to fp32, then one
-        // rounding to f16.  The empty asm pins the fp32 product in a
-        // register so the backend cannot fuse the last multiply and the
-        // conversion into a single-rounding v_fma_mixlo_f16.
-        const float rs = ssc[wm * TM + i * 32 + row];
-        const float* csp = ssc + QR * 64 + wn * TN + col;
-        const v4f32 c0 = *reinterpret_cast<const v4f32*>(csp);
-        const v4f32 c1 = *reinterpret_cast<const v4f32*>(csp + 4);
-        v8f16 h;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float we = e < 4 ? w0[e] : w1[e - 4];
-          const float ce = e < 4 ? c0[e] : c1[e - 4];
-          float p = (static_cast<float>(__builtin_bit_cast(int32_t, we)) * rs) * ce;
-          asm volatile("" : "+v"(p));
-          h[e] = static_cast<_Float16>(p);
-        }
-        _Float16* c = static_cast<_Float16*>(g.C) + static_cast<int64_t>(m) * g.ldc + n;
-        if (g.vec8_store && n + 8 <= g.N) {
-          __builtin_nontemporal_store(h, reinterpret_cast<v8f16*>(c));  // C is not re-read here
-        } else {
-          for (int e = 0; e < 8 && n + e < g.N; ++e) c[e] = h[e];
-        }
-      }
-      continue;
-    }
-    if constexpr (EPI == kEpiW8) {
-      // f16(acc * cs[n]): the fp32 product, then one rounding to f16.
-      constexpr int kRuns8 = 32 * TN / 8, kRunsPerRow8 = TN / 8;
-#pragma unroll
-      for (int it = 0; it < kRuns8 / 64; ++it) {
-        const int run = it * 64 + lane;
-        const int row = run / kRunsPerRow8, col = (run % kRunsPerRow8) * 8;
-        const v4f32 w0 = *reinterpret_cast<const v4f32*>(stg + row * kPad + col);
-        const v4f32 w1 = *reinterpret_cast<const v4f32*>(stg + row * kPad + col + 4);
-        const int m = mw + i * 32 + row, n = nw + col;
-        if (m >= g.M || n >= g.N) continue;
-        const float* csp = ssc + QR * 64 + wn * TN + col;
-        const v4f32 c0 = *reinterpret_cast<const v4f32*>(csp);
-        const v4f32 c1 = *reinterpret_cast<const v4f32*>(csp + 4);
-        v8f16 h;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float p = (e < 4 ? w0[e] : w1[e - 4]) * (e < 4 ? c0[e] : c1[e - 4]);
-          asm volatile("" : "+v"(p));
-          h[e] = static_cast<_Float16>(p);
-        }
-        _Float16* c = static_cast<_Float16*>(g.C) + static_cast<int64_t>(m) * g.ldc + n;
-        if (g.vec8_store && n + 8 <= g.N) {
-          __builtin_nontemporal_store(h, reinterpret_cast<v8f16*>(c));
-        } else {
-          for (int e = 0; e < 8 && n + e < g.N; ++e) c[e] = h[e];
-        }
-      }
-      continue;
-    }
-    if constexpr (EPI == kEpiSwiglu) {
-      // The wave's 128 image rows are 64 gate channels then the same 64 up
-      // channels: output column o = (n0 + wn*128)/2 + col takes the gate
-      // value from staged column col and the up value from column 64 + col.
-      // h = f16(silu(g) * u) with g = acc_g * sg, u = acc_u * su in fp32 and
-      // silu(g) = g / (1 + exp(-g)).
-      constexpr int kRunsS = 32 * 64 / 8, kRunsPerRowS = 64 / 8;
-#pragma unroll
-      for (int it = 0; it < kRunsS / 64; ++it) {
-        const int run = it * 64 + lane;
-        const int row = run / kRunsPerRowS, col = (run % kRunsPerRowS) * 8;
-        const float* sp = stg + row * kPad + col;
-        const v4f32 g0 = *reinterpret_cast<const v4f32*>(sp);
-        const v4f32 g1 = *reinterpret_cast<const v4f32*>(sp + 4);
-        const v4f32 u0 = *reinterpret_cast<const v4f32*>(sp + 64);
-        const v4f32 u1 = *reinterpret_cast<const v4f32*>(sp + 68);
-        const int m = mw + i * 32 + row, o = nw / 2 + col;
-        if (m >= g.M || o >= g.n_out) continue;
-        const float* csp = ssc + QR * 64 + wn * TN + col;
-        const v4f32 sg0 = *reinterpret_cast<const v4f32*>(csp);
-        const v4f32 sg1 = *reinterpret_cast<const v4f32*>(csp + 4);
-        const v4f32 su0 = *reinterpret_cast<const v4f32*>(csp + 64);
-        const v4f32 su1 = *reinterpret_cast<const v4f32*>(csp + 68);
-        v8f16 h;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float gv = (e < 4 ? g0[e] : g1[e - 4]) * (e < 4 ? sg0[e] : sg1[e - 4]);
-          const float uv = (e < 4 ? u0[e] : u1[e - 4]) * (e < 4 ? su0[e] : su1[e - 4]);
-          const float ex = __builtin_amdgcn_exp2f(-gv * 1.4426950408889634f);
-          h[e] = static_cast<_Float16>(gv * __builtin_amdgcn_rcpf(1.0f + ex) * uv);
-        }
-        _Float16* c = static_cast<_Float16*>(g.C) + static_cast<int64_t>(m) * g.ldc + o;
-        if (g.vec8_store && o + 8 <= g.n_out) {
-          __builtin_nontemporal_store(h, reinterpret_cast<v8f16*>(c));
-        } else {
-          for (int e = 0; e < 8 && o + e < g.n_out; ++e) c[e] = h[e];
-        }
-      }
-      continue;
-    }
-    constexpr int kRuns = 32 * TN / 4;          // 4-element runs in the block
-    constexpr int kRunsPerRow = TN / 4;
-#pragma unroll
-    for (int it = 0; it < kRuns / 64; ++it) {
-      const int run = it * 64 + lane;
-      const int row = run / kRunsPerRow, col = (run % kRunsPerRow) * 4;
-      const v4f32 w = *reinterpret_cast<const v4f32*>(stg + row * kPad + col);
-      const int m = mw + i * 32 + row, n = nw + col;
-      if (m >= g.M || n >= g.N) continue;
-      const int64_t off = static_cast<int64_t>(m) * g.ldc + n;
-      const bool full = g.vec_store && n + 4 <= g.N;
-      if constexpr (EPI == kEpiI32) {
-        int32_t* c = static_cast<int32_t*>(g.C) + off;
-        v4u32_t r = __builtin_bit_cast(v4u32_t, w);
-        if (full) {
-          if (g.accumulate) {
-            r += *reinterpret_cast<const v4u32_t*>(c);
-            *reinterpret_cast<v4u32_t*>(c) = r;
-          } else {
-            __builtin_nontemporal_store(r, reinterpret_cast<v4u32_t*>(c));
-          }
-        } else {
-          for (int e = 0; e < 4 && n + e < g.N; ++e)
-            c[e] = static_cast<int32_t>(g.accumulate ? static_cast<uint32_t>(c[e]) + r[e] : r[e]);
-        }
-      } else {
-        v4f32 r = w;
-        if (g.out_dtype == HXM_F32) {
-          float* c = static_cast<float*>(g.C) + off;
-          if (full) {
-            if (g.accumulate) r += *reinterpret_cast<const v4f32*>(c);
-            *reinterpret_cast<v4f32*>(c) = r;
-          } else {
-            for (int e = 0; e < 4 && n + e < g.N; ++e) c[e] = g.accumulate ? c[e] + r[e] : r[e];
-          }
-        } else if (g.out_dtype == HXM_F16) {
-          _Float16* c = static_cast<_Float16*>(g.C) + off;
-          if (full) {
-            if (g.accumulate) {
-              const v4f16_t o = *reinterpret_cast<const v4f16_t*>(c);
-              for (int e = 0; e < 4; ++e) r[e] += static_cast<float>(o[e]);
-            }
-            v4f16_t h;
-            for (int e = 0; e < 4; ++e) h[e] = static_cast<_Float16>(r[e]);
-            *reinterpret_cast<v4f16_t*>(c) = h;
-          } else {
-            for (int e = 0; e < 4 && n + e < g.N; ++e)
-              c[e] = static_cast<_Float16>(g.accumulate ? r[e] + static_cast<float>(c[e]) : r[e]);
-          }
-        } else {
-          __bf16* c = static_cast<__bf16*>(g.C) + off;
-          if (full) {
-            if (g.accumulate) {
-              const v4bf16_t o = *reinterpret_cast<const v4bf16_t*>(c);
-              for (int e = 0; e < 4; ++e) r[e] += static_cast<float>(o[e]);
-            }
-            v4bf16_t h;
-            for (int e = 0; e < 4; ++e) h[e] = static_cast<__bf16>(r[e]);
-            *reinterpret_cast<v4bf16_t*>(c) = h;
-          } else {
-            for (int e = 0; e < 4 && n + e < g.N; ++e)
-              c[e] = static_cast<__bf16>(g.accumulate ? r[e] + static_cast<float>(c[e]) : r[e]);
-          }
-        }
-      }
-    }
-  }
-}
 
 // Transpose [K,N] -> [N,K] (the resident weight image).  32x32 element tiles
 // through LDS.
@@ -699,47 +39,20 @@ __global__ __launch_bounds__(256) void transpose_kernel(const E* __restrict__ sr
 // Host side: the compiled-config table and dispatch.
 // ------------------------------------------------------------------------
 
-typedef void (*gemm_fn)(GemmArgs);
-
 struct KernelEntry {
   hxm_gemm_config cfg;  // bk in BYTES here; converted per dtype on the way out
   int threads;
-  gemm_fn i8_i32, i8_deq, f16, bf16;
 };
 
-#define HXM_ENTRY(BM, BN, BKB, ST, WM, WN)                                     \
-  KernelEntry{{BM, BN, BKB, WM, WN, ST, 1},                                    \
-              WM * WN * 64,                                                    \
-              gemm_kernel<int8_t, BM, BN, BKB, ST, WM, WN, kEpiI32>,           \
-              gemm_kernel<int8_t, BM, BN, BKB, ST, WM, WN, kEpiDequant>,       \
-              gemm_kernel<_Float16, BM, BN, BKB, ST, WM, WN, kEpiFloat>,       \
-              gemm_kernel<__bf16, BM, BN, BKB, ST, WM, WN, kEpiFloat>}
+#define HXM_ENTRY(BM, BN, BKB, ST, WM, WN) KernelEntry{{BM, BN, BKB, WM, WN, ST, 1}, WM * WN * 64}
 
+// Row i holds the configuration of row i of kI8Fns / kF16Fns.
 static const KernelEntry kKernels[] = {HXM_GEMM_CONFIG_LIST(HXM_ENTRY)};
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
-// W8A16 kernels: cfg.bk in A bytes (bk = BKB/2 f16 elements on the way out).
-struct W8Entry {
-  hxm_gemm_config cfg;
-  int threads;
-  gemm_fn w8, swiglu;  // swiglu is null unless the wave tile is 128 wide
-};
-
-template <int BM, int BN, int BKB, int ST, int WM, int WN>
-constexpr gemm_fn swiglu_fn() {
-  if constexpr (BN / WN == 128)
-    return gemm_kernel<_Float16, BM, BN, BKB, ST, WM, WN, kEpiSwiglu>;
-  else
-    return nullptr;
-}
-
-#define HXM_W8_ENTRY(BM, BN, BKB, ST, WM, WN)                                  \
-  W8Entry{{BM, BN, BKB, WM, WN, ST, 1},                                        \
-          WM * WN * 64,                                                        \
-          gemm_kernel<_Float16, BM, BN, BKB, ST, WM, WN, kEpiW8>,              \
-          swiglu_fn<BM, BN, BKB, ST, WM, WN>()}
-
-static const W8Entry kW8Kernels[] = {HXM_W8_CONFIG_LIST(HXM_W8_ENTRY)};
+// W8A16 kernels (row i of kW8Fns): cfg.bk in A bytes (bk = BKB/2 f16
+// elements on the way out).
+static const KernelEntry kW8Kernels[] = {HXM_W8_CONFIG_LIST(HXM_ENTRY)};
 constexpr int kNumW8Kernels = sizeof(kW8Kernels) / sizeof(kW8Kernels[0]);
 
 static int elem_bytes(int32_t dt) { return dt == HXM_I8 ? 1 : 2; }
@@ -791,13 +104,12 @@ hxm_status launch_gemm(const KernelEntry& e, int32_t ab_dtype, int epi,
                        const GemmArgs& g, hipStream_t stream) {
   const int bm = e.cfg.bm, bn = e.cfg.bn;
   const int64_t tiles = static_cast<int64_t>((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
+  const int i = static_cast<int>(&e - kKernels);
   gemm_fn fn = nullptr;
   if (ab_dtype == HXM_I8)
-    fn = (epi == kEpiDequant) ? e.i8_deq : e.i8_i32;
-  else if (ab_dtype == HXM_F16)
-    fn = e.f16;
+    fn = kI8Fns[i][epi == kEpiDequant ? 1 : 0];
   else
-    fn = e.bf16;
+    fn = kF16Fns[i][ab_dtype == HXM_F16 ? 0 : 1];
   hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(tiles)), dim3(e.threads), 0,
                      stream, g);
   return check_launch("gemm kernel");
@@ -929,16 +241,16 @@ hxm_gemm_config w8_kernel_config(int i) {
   c.bk /= 2;  // f16 elements of K per stage
   return c;
 }
-bool w8_kernel_has_swiglu(int i) { return kW8Kernels[i].swiglu != nullptr; }
+bool w8_kernel_has_swiglu(int i) { return kW8Fns[i][1] != nullptr; }
 
-static const W8Entry* find_w8_kernel(const hxm_gemm_config& c, bool swiglu) {
+static const KernelEntry* find_w8_kernel(const hxm_gemm_config& c, bool swiglu) {
   for (int i = 0; i < kNumW8Kernels; ++i) {
     const hxm_gemm_config k = w8_kernel_config(i);
     if (k.bm == c.bm && k.bn == c.bn && (c.bk == 0 || c.bk == k.bk) &&
         (c.waves_m == 0 || c.waves_m == k.waves_m) &&
         (c.waves_n == 0 || c.waves_n == k.waves_n) &&
         (c.stages == 0 || c.stages == k.stages) && (c.split_k == 0 || c.split_k == 1) &&
-        (!swiglu || kW8Kernels[i].swiglu))
+        (!swiglu || w8_kernel_has_swiglu(i)))
       return &kW8Kernels[i];
   }
   return nullptr;
@@ -950,7 +262,7 @@ hxm_gemm_config default_w8_config(int64_t M, int64_t N, bool swiglu) {
   int best = -1;
   int64_t best_tiles = -1;
   for (int i = 0; i < kNumW8Kernels; ++i) {
-    if (swiglu && !kW8Kernels[i].swiglu) continue;
+    if (swiglu && !w8_kernel_has_swiglu(i)) continue;
     const hxm_gemm_config k = w8_kernel_config(i);
     const int64_t tiles = ((M + k.bm - 1) / k.bm) * ((N + k.bn - 1) / k.bn);
     if (tiles >= 256) return k;
@@ -988,7 +300,7 @@ hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const in
   } else if (!lookup_tuned(op, M, sw ? n_out : N, K, &c)) {
     c = default_w8_config(M, N, sw);
   }
-  const W8Entry* e = find_w8_kernel(c, sw);
+  const KernelEntry* e = find_w8_kernel(c, sw);
   if (!e)
     return fail(HXM_UNSUPPORTED_SHAPE,
                 "no-kernel: no compiled W8A16 GEMM%s for bm=%d bn=%d bk=%d waves=%dx%d",
@@ -1016,7 +328,8 @@ hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const in
   g.vec_store = (reinterpret_cast<uintptr_t>(C) % 8 == 0) && ((ldc * 2) % 8 == 0);
   g.vec8_store = (reinterpret_cast<uintptr_t>(C) % 16 == 0) && ((ldc * 2) % 16 == 0);
   const int64_t tiles = ((M + e->cfg.bm - 1) / e->cfg.bm) * ((N + e->cfg.bn - 1) / e->cfg.bn);
-  hipLaunchKernelGGL(sw ? e->swiglu : e->w8, dim3(static_cast<unsigned>(tiles)),
+  const int wi = static_cast<int>(e - kW8Kernels);
+  hipLaunchKernelGGL(kW8Fns[wi][sw ? 1 : 0], dim3(static_cast<unsigned>(tiles)),
                      dim3(e->threads), 0, stream, g);
   if ((st = check_launch("w8a16 gemm kernel")) != HXM_OK) return st;
   return ok();

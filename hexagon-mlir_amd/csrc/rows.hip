@@ -13,6 +13,8 @@
 // across the wave with DPP + readlane (no LDS, no barriers) and written back
 // from registers: one HBM read and one HBM write per element.  Longer rows use
 // the streaming variant (VPL = 0) that re-reads the row per pass.
+#include <type_traits>
+
 #include "device_util.h"
 #include "hxm_internal.h"
 
@@ -83,7 +85,56 @@ struct RowArgs {
   float eps;
 };
 
-// Register-resident kernel: each lane holds VPL vectors of the row.
+// One 16-byte vector of a row in its storage type.
+template <typename T>
+using RawVec = T __attribute__((ext_vector_type(RowVec<T>::N)));
+
+// Loads the vector at column c0 in storage form, columns >= cols set to
+// `fill`.  A full aligned vector is one dwordx4 load, nontemporal (NT) for
+// the rows, which are read once; gamma and beta are shared by every row and
+// stay cacheable.
+template <typename T, bool ALIGNED, bool NT = true>
+__device__ __forceinline__ RawVec<T> load_raw(const T* __restrict__ row, int64_t c0,
+                                              int64_t cols, T fill) {
+  constexpr int N = RowVec<T>::N;
+  if (ALIGNED && c0 + N <= cols) {
+    if constexpr (NT)
+      return __builtin_nontemporal_load(reinterpret_cast<const RawVec<T>*>(row + c0));
+    else
+      return *reinterpret_cast<const RawVec<T>*>(row + c0);
+  }
+  RawVec<T> v;
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] = (c0 + j < cols) ? row[c0 + j] : fill;
+  return v;
+}
+
+template <typename T, bool ALIGNED>
+__device__ __forceinline__ void store_raw(T* __restrict__ row, int64_t c0, int64_t cols,
+                                          RawVec<T> v) {
+  constexpr int N = RowVec<T>::N;
+  if (ALIGNED && c0 + N <= cols) {
+    __builtin_nontemporal_store(v, reinterpret_cast<RawVec<T>*>(row + c0));
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (c0 + j < cols) row[c0 + j] = v[j];
+  }
+}
+
+// Makes the compiler treat the row registers as rewritten, so that each pass
+// widens the stored values again instead of keeping fp32 copies of the
+// whole row alive across passes (which would double the register count).
+template <typename T, int VPL>
+__device__ __forceinline__ void fresh(RawVec<T> (&v)[VPL]) {
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) asm volatile("" : "+v"(v[i]));
+}
+
+// Register-resident kernel: each lane holds VPL vectors of the row in the
+// storage type (f16/bf16 rows take half the registers of fp32 copies, so
+// more waves fit per SIMD and more bytes are in flight).  Values are
+// widened to fp32 as each pass reads them.
 template <typename T, int OP, int VPL, bool ALIGNED>
 __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
   constexpr int N = RowVec<T>::N;
@@ -93,91 +144,114 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
   const T* __restrict__ xr = static_cast<const T*>(a.x) + r * a.ldx;
   T* __restrict__ yr = static_cast<T*>(a.y) + r * a.ldy;
   const int64_t cols = a.cols;
+  const T* __restrict__ g = static_cast<const T*>(a.gamma);
+  const T* __restrict__ b = static_cast<const T*>(a.beta);
+  auto col0 = [&](int i) { return (static_cast<int64_t>(i) * 64 + lane) * N; };
 
-  float v[VPL][N];
-  const float fill = (OP == kSoftmax) ? -__builtin_huge_valf() : 0.0f;
+  const T fill = static_cast<T>(OP == kSoftmax ? -__builtin_huge_valf() : 0.0f);
+  RawVec<T> v[VPL];
 #pragma unroll
-  for (int i = 0; i < VPL; ++i)
-    load_vec<T, ALIGNED>(xr, (static_cast<int64_t>(i) * 64 + lane) * N, cols, fill, v[i]);
+  for (int i = 0; i < VPL; ++i) v[i] = load_raw<T, ALIGNED>(xr, col0(i), cols, fill);
+  // gamma / beta vector i, read in the output pass (cache hits: every row
+  // shares them), so no registers hold them while the row is in flight.
+  auto gamma_at = [&](int i) {
+    return g ? load_raw<T, ALIGNED, false>(g, col0(i), cols, T(0)) : RawVec<T>(T(1));
+  };
+  auto beta_at = [&](int i) {
+    return b ? load_raw<T, ALIGNED, false>(b, col0(i), cols, T(0)) : RawVec<T>(T(0));
+  };
 
   if constexpr (OP == kSoftmax) {
-    float m = -__builtin_huge_valf();
+    // The row maximum is exact in the storage type, so f16 rows take it with
+    // packed f16 max (two lanes per instruction) before widening once.
+    float m;
+    if constexpr (std::is_same<T, _Float16>::value) {
+      RawVec<T> mv = v[0];
 #pragma unroll
-    for (int i = 0; i < VPL; ++i)
+      for (int i = 1; i < VPL; ++i) mv = __builtin_elementwise_max(mv, v[i]);
+      m = tof(mv[0]);
 #pragma unroll
-      for (int j = 0; j < N; ++j) m = fmaxf(m, v[i][j]);
+      for (int j = 1; j < N; ++j) m = fmaxf(m, tof(mv[j]));
+    } else {
+      m = -__builtin_huge_valf();
+#pragma unroll
+      for (int i = 0; i < VPL; ++i)
+#pragma unroll
+        for (int j = 0; j < N; ++j) m = fmaxf(m, tof(v[i][j]));
+    }
     m = wave_reduce(m, OpMax());
+    fresh(v);
+    // exp(x - m) = 2^(x*log2(e) - m*log2(e)): one (mixed-precision) fma per
+    // element feeds the hardware exp2.  Padded -inf columns give 0.
+    constexpr float kLog2e = 1.4426950408889634f;
+    const float mb = -m * kLog2e;
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
-      for (int j = 0; j < N; ++j) {
-        v[i][j] = exp_f32(v[i][j] - m);  // padded -inf -> 0
-        s += v[i][j];
-      }
+      for (int j = 0; j < N; ++j) s += __builtin_amdgcn_exp2f(fmaf(tof(v[i][j]), kLog2e, mb));
     s = wave_reduce(s, OpSum());
+    fresh(v);
     const float inv = 1.0f / s;
 #pragma unroll
-    for (int i = 0; i < VPL; ++i)
+    for (int i = 0; i < VPL; ++i) {
+      RawVec<T> o;
 #pragma unroll
-      for (int j = 0; j < N; ++j) v[i][j] *= inv;
+      for (int j = 0; j < N; ++j)
+        o[j] = fromf<T>(__builtin_amdgcn_exp2f(fmaf(tof(v[i][j]), kLog2e, mb)) * inv);
+      store_raw<T, ALIGNED>(yr, col0(i), cols, o);
+    }
   } else if constexpr (OP == kRmsNorm) {
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
-      for (int j = 0; j < N; ++j) ss += v[i][j] * v[i][j];
+      for (int j = 0; j < N; ++j) ss += tof(v[i][j]) * tof(v[i][j]);
     ss = wave_reduce(ss, OpSum());
+    fresh(v);
     const float rstd = 1.0f / sqrtf(ss / static_cast<float>(cols) + a.eps);
-    const T* __restrict__ g = static_cast<const T*>(a.gamma);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      const int64_t c0 = (static_cast<int64_t>(i) * 64 + lane) * N;
-      float gv[N];
-      if (g) load_vec<T, ALIGNED>(g, c0, cols, 0.0f, gv);
+      const RawVec<T> gi = gamma_at(i);
+      RawVec<T> o;
 #pragma unroll
-      for (int j = 0; j < N; ++j) v[i][j] = (v[i][j] * rstd) * (g ? gv[j] : 1.0f);
+      for (int j = 0; j < N; ++j) o[j] = fromf<T>((tof(v[i][j]) * rstd) * tof(gi[j]));
+      store_raw<T, ALIGNED>(yr, col0(i), cols, o);
     }
   } else {  // kLayerNorm
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
-      for (int j = 0; j < N; ++j) s += v[i][j];
+      for (int j = 0; j < N; ++j) s += tof(v[i][j]);
     const float mean = wave_reduce(s, OpSum()) / static_cast<float>(cols);
+    fresh(v);
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      const int64_t c0 = (static_cast<int64_t>(i) * 64 + lane) * N;
 #pragma unroll
       for (int j = 0; j < N; ++j) {
-        const float d = (c0 + j < cols) ? v[i][j] - mean : 0.0f;
+        const float d = (col0(i) + j < cols) ? tof(v[i][j]) - mean : 0.0f;
         q += d * d;
       }
     }
     const float var = wave_reduce(q, OpSum()) / static_cast<float>(cols);
+    fresh(v);
     const float rstd = 1.0f / sqrtf(var + a.eps);
     if (lane == 0) {
       if (a.mean_out) a.mean_out[r] = mean;
       if (a.rstd_out) a.rstd_out[r] = rstd;
     }
-    const T* __restrict__ g = static_cast<const T*>(a.gamma);
-    const T* __restrict__ b = static_cast<const T*>(a.beta);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      const int64_t c0 = (static_cast<int64_t>(i) * 64 + lane) * N;
-      float gv[N], bv[N];
-      if (g) load_vec<T, ALIGNED>(g, c0, cols, 0.0f, gv);
-      if (b) load_vec<T, ALIGNED>(b, c0, cols, 0.0f, bv);
+      const RawVec<T> gi = gamma_at(i), bi = beta_at(i);
+      RawVec<T> o;
 #pragma unroll
       for (int j = 0; j < N; ++j)
-        v[i][j] = (v[i][j] - mean) * rstd * (g ? gv[j] : 1.0f) + (b ? bv[j] : 0.0f);
+        o[j] = fromf<T>((tof(v[i][j]) - mean) * rstd * tof(gi[j]) + tof(bi[j]));
+      store_raw<T, ALIGNED>(yr, col0(i), cols, o);
     }
   }
-
-#pragma unroll
-  for (int i = 0; i < VPL; ++i)
-    store_vec<T, ALIGNED>(yr, (static_cast<int64_t>(i) * 64 + lane) * N, cols, v[i]);
 }
 
 // Streaming kernel for rows longer than the register budget: the row is

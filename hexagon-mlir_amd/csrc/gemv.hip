@@ -66,18 +66,22 @@ __global__ __launch_bounds__(256) void pack_w8a16_kernel(const int8_t* __restric
 }
 
 // One workgroup = 16 output channels x all of K; its KW waves split each
-// K chunk of KW*SPW slabs, SPW contiguous slabs per wave.  Per chunk, every W
-// load of the wave (SPW x 16 bytes per lane) is issued first; the x rows of
-// the chunk are then staged once in LDS (row stride padded by 16 bytes so
-// the 16 rows a ds_read_b128 touches land on distinct banks) while those
-// loads are in flight.  PACKED reads the resident image (1 KiB contiguous
-// per wave instruction); otherwise W is the plain [N, K] matrix (16 rows x
-// 64 bytes per instruction).
+// K chunk of KW*SPW slabs, SPW contiguous slabs per wave.  Per chunk the
+// wave first loads its share of the x rows, then issues every weight load of
+// the chunk (SPW x 16 bytes per lane), all unconditionally (addresses are
+// clamped, so the compiler's waits stay exact).  The x rows go to LDS (row
+// stride padded by 16 bytes so the 16 rows a ds_read_b128 touches land on
+// distinct banks) behind a barrier that does not wait for the weight loads,
+// and the MFMAs then consume each slab as its load lands.  PACKED reads the resident image (1 KiB contiguous per
+// wave instruction); otherwise W is the plain [N, K] matrix (16 rows x 64
+// bytes per instruction).
 template <int KW, int SPW, bool PACKED, int MR>
 __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
   constexpr int kChunkSlabs = KW * SPW;
   constexpr int kChunkK = kChunkSlabs * 64;
   constexpr int kRowBytes = kChunkK * 2 + 16;   // padded x row in LDS
+  constexpr int kXVecs = MR * kChunkK / 8;      // 16-byte x vectors per chunk
+  constexpr int kXPerThread = (kXVecs + KW * 64 - 1) / (KW * 64);
   __shared__ __attribute__((aligned(16))) uint8_t xs[MR * kRowBytes];  // MR >= rows
   __shared__ v4f32 part[KW][64];
   const int lane = threadIdx.x & 63;
@@ -92,48 +96,59 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
   const int slabs = (g.K + 63) / 64;
   const int8_t* wrow = g.W + static_cast<int64_t>(n_ok ? n : 0) * g.ldw;
   const int8_t* wblk = g.W + static_cast<int64_t>(blockIdx.x) * slabs * 1024 + lane * 16;
+  const v4i32 zero = {0, 0, 0, 0};
 
   v4f32 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int c0 = 0; c0 < slabs; c0 += kChunkSlabs) {
-    const int s_first = c0 + wave * SPW;
+    const int kc0 = c0 * 64;
+    // x[m_base .. m_base+rows, kc0 .. kc0+kChunkK), zero past K / rows.
+    v4i32 xv[kXPerThread];
+#pragma unroll
+    for (int q = 0; q < kXPerThread; ++q) {
+      const int idx = threadIdx.x + q * KW * 64;
+      const int r = idx / (kChunkK / 8), k8 = (idx % (kChunkK / 8)) * 8;
+      const bool ok = idx < kXVecs && r < rows && kc0 + k8 < g.K;
+      const v4i32 v = *reinterpret_cast<const v4i32*>(
+          g.x + (ok ? static_cast<int64_t>(m_base + r) * g.ldx + kc0 + k8 : 0));
+      xv[q] = ok ? v : zero;
+    }
     v4i32 w[SPW];
 #pragma unroll
     for (int u = 0; u < SPW; ++u) {
-      const int s = s_first + u;
+      const int s = c0 + wave * SPW + u;
       // Weights are streamed exactly once: nontemporal loads keep them from
       // displacing x and other reusable lines in the caches.
+      // Out-of-range slabs / K chunks load a valid in-range address instead
+      // and need no mask: their x is zero (staged below), and rows past N
+      // are never stored.  Keeping the loaded data unmasked lets the first
+      // MFMAs wait for their own loads only.
       if constexpr (PACKED) {
-        w[u] = s < slabs ? __builtin_nontemporal_load(reinterpret_cast<const v4i32*>(
-                               wblk + static_cast<int64_t>(s) * 1024))
-                         : v4i32{0, 0, 0, 0};
+        w[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i32*>(
+            wblk + static_cast<int64_t>(s < slabs ? s : 0) * 1024));
       } else {
         const int k = s * 64 + kq * 16;
-        w[u] = (n_ok && k < g.K)
-                   ? __builtin_nontemporal_load(reinterpret_cast<const v4i32*>(wrow + k))
-                   : v4i32{0, 0, 0, 0};
+        w[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i32*>(wrow + (k < g.K ? k : 0)));
       }
     }
-    // Stage x[m_base .. m_base+rows, c0*64 .. +kChunkK) in LDS, zero past K.
-    __syncthreads();  // the previous chunk's reads are done
-    const int kc0 = c0 * 64;
-    const int kvalid = min(kChunkK, g.K - kc0);
-    for (int idx = threadIdx.x; idx < rows * (kChunkK / 8); idx += KW * 64) {
-      const int r = idx / (kChunkK / 8), k8 = (idx % (kChunkK / 8)) * 8;
-      v4i32 v = {0, 0, 0, 0};
-      if (k8 < kvalid)
-        v = *reinterpret_cast<const v4i32*>(g.x + static_cast<int64_t>(m_base + r) * g.ldx + kc0 + k8);
-      *reinterpret_cast<v4i32*>(xs + r * kRowBytes + k8 * 2) = v;
+    // The previous chunk's LDS reads are done; then x goes to LDS.  These
+    // barriers wait for LDS operations only, never for the weight loads.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int q = 0; q < kXPerThread; ++q) {
+      const int idx = threadIdx.x + q * KW * 64;
+      if (idx < kXVecs) {
+        const int r = idx / (kChunkK / 8), k8 = (idx % (kChunkK / 8)) * 8;
+        *reinterpret_cast<v4i32*>(xs + r * kRowBytes + k8 * 2) = xv[q];
+      }
     }
-    __syncthreads();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
     for (int u = 0; u < SPW; ++u) {
       const int kl = (wave * SPW + u) * 64 + kq * 16;   // K offset inside the chunk
-      v4i32 xa = {0, 0, 0, 0}, xb = {0, 0, 0, 0};
-      if (r16 < rows) {
-        const uint8_t* px = xs + r16 * kRowBytes + kl * 2;
-        xa = *reinterpret_cast<const v4i32*>(px);
-        xb = *reinterpret_cast<const v4i32*>(px + 16);
-      }
+      const uint8_t* px = xs + (r16 < MR ? r16 : 0) * kRowBytes + kl * 2;
+      v4i32 xa = *reinterpret_cast<const v4i32*>(px);
+      v4i32 xb = *reinterpret_cast<const v4i32*>(px + 16);
+      if (r16 >= rows) xa = xb = zero;
       const v8f16 wa = i8x8_to_f16(static_cast<uint32_t>(w[u][0]), static_cast<uint32_t>(w[u][1]));
       const v8f16 wb = i8x8_to_f16(static_cast<uint32_t>(w[u][2]), static_cast<uint32_t>(w[u][3]));
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, __builtin_bit_cast(v8f16, xa), acc, 0, 0, 0);

@@ -51,6 +51,9 @@ hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Frees the resident weight images of device `dev` (resident.hip).
+hxm_status release_images(int dev);
+
 }  // namespace hxm
 
 #define HXM_HIP_TRY(expr)                                                    \

@@ -1,0 +1,201 @@
+// Content-addressed resident weight images.
+//
+// Reference: the weight-resident contract -- WeightPrepack.pack
+// (qcom_hexagon_backend/backend/hmx_weight_prepack.py:124-168: cache keyed by
+// (slot, shape, dtype, blake2b of the raw bytes); shape / dtype mismatches
+// refused; an f32 source packed to the fp16 image after -0 -> +0,
+// :185-212) and hexagon_runtime_weight_resident_v2
+// (bin/runtime/include/HexagonCAPI.h:52-53: the image is pinned for the
+// process).
+//
+// GPU form: the source bytes are hashed on the device (two 64-bit lanes,
+// each element mixed with its logical index by the SplitMix64 finaliser and
+// combined by wrapping sum / xor, so the key depends on every byte and its
+// position but not on the memory layout of a strided source); the key is
+// (kind, device, rows, cols, source dtype, hash).  A miss packs the image
+// into library-owned device memory with the same kernels as
+// hxm_prepack_weight / hxm_prepack_w8a16; a hit returns the existing image.
+// Images live until hxm_release_cache().
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "hxm_internal.h"
+
+namespace hxm {
+
+namespace {
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+// out[0] += sum of lane-1 mixes, out[1] ^= xor of lane-2 mixes, over every
+// element (r, c) of the rows x cols source (row stride ld elements).
+__global__ __launch_bounds__(256) void hash_kernel(const uint8_t* __restrict__ src, int64_t ld,
+                                                   int64_t rows, int64_t cols, int eb,
+                                                   unsigned long long* out) {
+  const int64_t n = rows * cols;
+  uint64_t s = 0, x = 0;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / cols, c = i % cols;
+    const uint8_t* p = src + (r * ld + c) * eb;
+    uint64_t v = 0;
+    for (int b = 0; b < eb; ++b) v |= static_cast<uint64_t>(p[b]) << (8 * b);
+    const uint64_t iu = static_cast<uint64_t>(i);
+    s += mix64(v ^ (iu * 0x9e3779b97f4a7c15ull));
+    x ^= mix64(v + iu * 0xd6e8feb86659fd93ull + 0x632be59bd9b4e019ull);
+  }
+  // Wave reduction, then one atomic per wave (vector memory atomics).
+  for (int off = 32; off > 0; off >>= 1) {
+    s += __shfl_xor(s, off);
+    x ^= __shfl_xor(x, off);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicAdd(&out[0], static_cast<unsigned long long>(s));
+    atomicXor(&out[1], static_cast<unsigned long long>(x));
+  }
+}
+
+__global__ void zero2_kernel(unsigned long long* p) { p[threadIdx.x] = 0; }
+
+// [K, N] fp32 (row stride ld) -> [N, K] fp16 image: -0 canonicalised to +0
+// (x + 0.0f), then IEEE round to nearest even.  32 x 32 tiles through LDS.
+__global__ __launch_bounds__(256) void f32_to_f16_image_kernel(const float* __restrict__ src,
+                                                               int64_t ld,
+                                                               _Float16* __restrict__ dst,
+                                                               int64_t K, int64_t N) {
+  __shared__ float tile[32][33];
+  const int64_t k0 = static_cast<int64_t>(blockIdx.y) * 32;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int r = ty; r < 32; r += 8) {
+    const int64_t k = k0 + r, n = n0 + tx;
+    if (k < K && n < N) tile[r][tx] = src[k * ld + n];
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    const int64_t n = n0 + r, k = k0 + tx;
+    if (n < N && k < K) dst[n * K + k] = static_cast<_Float16>(tile[tx][r] + 0.0f);
+  }
+}
+
+struct Image {
+  void* ptr = nullptr;
+  int32_t dtype = 0;
+};
+typedef std::tuple<int32_t, int, int64_t, int64_t, int32_t, uint64_t, uint64_t> ImageKey;
+std::mutex g_img_mu;
+std::map<ImageKey, Image> g_images;
+
+}  // namespace
+
+// Frees every resident image of device `dev` (called by hxm_release_cache).
+hxm_status release_images(int dev) {
+  std::lock_guard<std::mutex> lk(g_img_mu);
+  for (auto it = g_images.begin(); it != g_images.end();) {
+    if (std::get<1>(it->first) == dev) {
+      HXM_HIP_TRY(hipFree(it->second.ptr));
+      it = g_images.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  return HXM_OK;
+}
+
+}  // namespace hxm
+
+using namespace hxm;
+
+extern "C" {
+
+hxm_status hxm_resident_weight(const void* src, int64_t ld, int64_t rows, int64_t cols,
+                               int32_t src_dtype, int32_t expect_dtype,
+                               const int64_t* expect_shape, int32_t kind,
+                               const void** image, int32_t* image_dtype, void* stream) {
+  if (image) *image = nullptr;
+  if (kind != HXM_IMAGE_GEMM && kind != HXM_IMAGE_W8A16)
+    return fail(HXM_INVALID_ARG, "invalid-argument: resident_weight kind=%d", kind);
+  if (!src || !image || rows <= 0 || cols <= 0 || ld < cols)
+    return fail(HXM_INVALID_ARG, "invalid-argument: resident_weight operands/extents");
+  if (expect_dtype >= 0 && src_dtype != expect_dtype)
+    return fail(HXM_UNSUPPORTED_DTYPE, "unsupported-dtype: weight has dtype %d, expected %d",
+                src_dtype, expect_dtype);
+  if (expect_shape && (expect_shape[0] != rows || expect_shape[1] != cols))
+    return fail(HXM_INVALID_ARG,
+                "invalid-argument: weight has shape [%lld, %lld], expected [%lld, %lld]",
+                (long long)rows, (long long)cols, (long long)expect_shape[0],
+                (long long)expect_shape[1]);
+  const bool gemm = kind == HXM_IMAGE_GEMM;
+  if (gemm ? (src_dtype != HXM_I8 && src_dtype != HXM_F16 && src_dtype != HXM_BF16 &&
+              src_dtype != HXM_F32)
+           : src_dtype != HXM_I8)
+    return fail(HXM_UNSUPPORTED_DTYPE,
+                "unsupported-dtype: resident %s image from dtype %d",
+                gemm ? "GEMM" : "W8A16", src_dtype);
+  const int32_t img_dt = src_dtype == HXM_F32 ? HXM_F16 : src_dtype;
+  if (gemm && (rows * dtype_bytes(img_dt)) % 16)
+    return fail(HXM_UNSUPPORTED_SHAPE,
+                "tile-alignment: resident GEMM image needs K * elem_bytes in 16-byte "
+                "multiples (K=%lld)", (long long)rows);
+  if (!gemm && (cols % 16 || ld % 16 || !aligned16(src)))
+    return fail(HXM_UNSUPPORTED_SHAPE,
+                "tile-alignment: resident W8A16 image needs K and ldw multiples of 16 and "
+                "a 16-byte aligned source");
+  int dev = 0;
+  hxm_status st = require_device(&dev);
+  if (st != HXM_OK) return st;
+  hipStream_t s = as_stream(stream);
+
+  // Content hash (the source is read after the caller's queued work).
+  void* ws = nullptr;
+  if ((st = stream_workspace(s, 16, &ws)) != HXM_OK) return st;
+  unsigned long long* h = static_cast<unsigned long long*>(ws);
+  zero2_kernel<<<1, 2, 0, s>>>(h);
+  hash_kernel<<<1024, 256, 0, s>>>(static_cast<const uint8_t*>(src), ld, rows, cols,
+                                   static_cast<int>(dtype_bytes(src_dtype)), h);
+  if ((st = check_launch("weight hash")) != HXM_OK) return st;
+  unsigned long long hh[2] = {0, 0};
+  HXM_HIP_TRY(hipMemcpyAsync(hh, h, sizeof(hh), hipMemcpyDeviceToHost, s));
+  HXM_HIP_TRY(hipStreamSynchronize(s));
+  const ImageKey key(kind, dev, rows, cols, src_dtype, hh[0], hh[1]);
+
+  std::lock_guard<std::mutex> lk(g_img_mu);
+  auto it = g_images.find(key);
+  if (it == g_images.end()) {
+    const int64_t bytes = gemm ? rows * cols * dtype_bytes(img_dt)
+                               : hxm_w8a16_packed_bytes(rows, cols);
+    Image img;
+    img.dtype = img_dt;
+    if (hipMalloc(&img.ptr, static_cast<size_t>(bytes)) != hipSuccess)
+      return fail(HXM_OUT_OF_MEMORY, "out-of-memory: resident image of %lld bytes",
+                  (long long)bytes);
+    if (!gemm) {
+      st = hxm_prepack_w8a16(static_cast<const int8_t*>(src), ld, rows, cols,
+                             static_cast<int8_t*>(img.ptr), bytes, stream);
+    } else if (src_dtype == HXM_F32) {
+      const dim3 grid(static_cast<unsigned>((cols + 31) / 32),
+                      static_cast<unsigned>((rows + 31) / 32));
+      f32_to_f16_image_kernel<<<grid, 256, 0, s>>>(static_cast<const float*>(src), ld,
+                                                   static_cast<_Float16*>(img.ptr), rows,
+                                                   cols);
+      st = check_launch("f32 weight image");
+    } else {
+      st = hxm_prepack_weight(src, ld, img.ptr, rows, rows, cols, src_dtype, stream);
+    }
+    if (st != HXM_OK) {
+      (void)hipFree(img.ptr);
+      return st;
+    }
+    it = g_images.emplace(key, img).first;
+  }
+  *image = it->second.ptr;
+  if (image_dtype) *image_dtype = it->second.dtype;
+  return ok();
+}
+
+}  // extern "C"

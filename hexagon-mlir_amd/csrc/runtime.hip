@@ -132,13 +132,13 @@ int32_t hxm_device_count(void) {
 hxm_status hxm_release_cache(void) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return hxm::ok();
+  HXM_HIP_TRY(hipDeviceSynchronize());
+  hxm_status st = hxm::release_images(dev);
+  if (st != HXM_OK) return st;
   std::lock_guard<std::mutex> lk(hxm::g_ws_mu);
   for (auto it = hxm::g_ws.begin(); it != hxm::g_ws.end();) {
     if ((it->first >> 48) == static_cast<uint64_t>(dev)) {
-      if (it->second.ptr) {
-        HXM_HIP_TRY(hipDeviceSynchronize());
-        HXM_HIP_TRY(hipFree(it->second.ptr));
-      }
+      if (it->second.ptr) HXM_HIP_TRY(hipFree(it->second.ptr));
       it = hxm::g_ws.erase(it);
     } else {
       ++it;

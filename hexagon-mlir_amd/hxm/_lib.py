@@ -23,6 +23,7 @@ F16, BF16, F32, I8, I32 = 1, 2, 3, 4, 5
 B_KN, B_NK = 0, 1
 W_NK, W_PACKED = 0, 1
 OP_W8A16, OP_W8A16_SWIGLU = 16, 17
+IMAGE_GEMM, IMAGE_W8A16 = 0, 1
 
 
 class HxmError(RuntimeError):
@@ -80,6 +81,8 @@ SIGNATURES = {
     "hxm_w8a16_configs": (_i32, [_i32, _cfgp, _i32]),
     "hxm_tune_w8a16": (_st, [_i32, _p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32,
                              _cfgp, ctypes.c_char_p, _i64, _p]),
+    "hxm_resident_weight": (_st, [_p, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_i64), _i32,
+                                  ctypes.POINTER(_p), ctypes.POINTER(_i32), _p]),
     "hxm_softmax_rows": (_st, [_p, _i64, _p, _i64, _i64, _i64, _i32, _p]),
     "hxm_rmsnorm_rows": (_st, [_p, _i64, _p, _p, _i64, _i64, _i64, _f32, _i32, _p]),
     "hxm_layernorm_rows": (_st, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i64, _i64, _f32, _i32,

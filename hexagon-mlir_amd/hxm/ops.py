@@ -14,8 +14,8 @@ from typing import Optional, Sequence
 
 import torch
 
-from ._lib import (B_KN, B_NK, BF16, F16, F32, I8, I32, OP_W8A16, OP_W8A16_SWIGLU, W_NK,
-                   W_PACKED, GemmConfig, check, lib)
+from ._lib import (B_KN, B_NK, BF16, F16, F32, I8, I32, IMAGE_GEMM, IMAGE_W8A16, OP_W8A16,
+                   OP_W8A16_SWIGLU, W_NK, W_PACKED, GemmConfig, check, lib)
 
 _DT = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32,
        torch.int8: I8, torch.int32: I32}
@@ -294,6 +294,49 @@ def tune_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor, out: torch
                             len(buf), _stream(stream))
     check(st, "hxm_tune_w8a16")
     return best, json.loads(buf.value.decode())
+
+
+class _DeviceArray:
+    """A non-owning view of library-owned device memory for torch.as_tensor
+    (the CUDA array interface, which the ROCm build of torch accepts)."""
+
+    _TYPESTR = {I8: "|i1", F16: "<f2", BF16: "<V2", F32: "<f4"}
+
+    def __init__(self, ptr: int, shape, dtype_code: int):
+        self.__cuda_array_interface__ = {"shape": tuple(shape), "data": (ptr, False),
+                                         "typestr": self._TYPESTR[dtype_code], "version": 3,
+                                         "strides": None}
+
+
+def resident_weight(W: torch.Tensor, kind: str = "gemm", *, expect_dtype=None,
+                    expect_shape=None, stream=None) -> torch.Tensor:
+    """The content-addressed resident image of a weight, packed on first use
+    (WeightPrepack.pack, hmx_weight_prepack.py:124-168).
+
+    ``kind="gemm"``: W is B [K, N] (int8/f16/bf16, or f32 -> an f16 image);
+    returns the [N, K] image for ``b_layout="nk"``.  ``kind="w8a16"``: W is
+    int8 [N, K]; returns the flat packed GEMV image.  The returned tensor
+    views library-owned memory that stays valid until ``hxm_release_cache``.
+    ``expect_dtype`` / ``expect_shape`` are the contract: a mismatch raises."""
+    import ctypes
+    _mat(W, "W")
+    rows, cols = W.shape
+    k = {"gemm": IMAGE_GEMM, "w8a16": IMAGE_W8A16}[kind]
+    exp_dt = -1 if expect_dtype is None else _DT[expect_dtype]
+    shp = None if expect_shape is None else (ctypes.c_int64 * 2)(*expect_shape)
+    img = ctypes.c_void_p()
+    img_dt = ctypes.c_int32()
+    st = lib.hxm_resident_weight(W.data_ptr(), _ld(W), rows, cols, _code(W), exp_dt, shp, k,
+                                 ctypes.byref(img), ctypes.byref(img_dt), _stream(stream))
+    check(st, "hxm_resident_weight")
+    if k == IMAGE_GEMM:
+        if img_dt.value == BF16:   # no bf16 typestr: view the bits, then reinterpret
+            t = torch.as_tensor(_DeviceArray(img.value, (cols, rows), F16), device=W.device)
+            return t.view(torch.bfloat16)
+        return torch.as_tensor(_DeviceArray(img.value, (cols, rows), img_dt.value),
+                               device=W.device)
+    nbytes = lib.hxm_w8a16_packed_bytes(rows, cols)
+    return torch.as_tensor(_DeviceArray(img.value, (nbytes,), I8), device=W.device)
 
 
 def _rows(x: torch.Tensor):

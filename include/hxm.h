@@ -93,9 +93,10 @@ const char* hxm_version(void);
 /* Number of gfx950 devices visible (0 when none); touches the HIP runtime. */
 int32_t hxm_device_count(void);
 
-/* Frees every library-owned buffer (per-stream pack workspaces) on the
- * current device.  Replaces the process-lifetime VTCM release of
- * bin/runtime/include/HexagonCAPI.h:38-57. */
+/* Frees every library-owned buffer (per-stream pack workspaces and resident
+ * weight images) on the current device, after synchronising it.  Replaces
+ * the process-lifetime VTCM release of bin/runtime/include/HexagonCAPI.h
+ * :38-57. */
 hxm_status hxm_release_cache(void);
 
 /* ---- admission (HmxTarget::queryContraction, HmxTarget.h:195-218) ----- */
@@ -192,6 +193,33 @@ int64_t hxm_w8a16_packed_bytes(int64_t N, int64_t K);
 hxm_status hxm_prepack_w8a16(const int8_t* W, int64_t ldw, int64_t N,
                              int64_t K, int8_t* out, int64_t out_bytes,
                              void* stream);
+
+/* ---- content-addressed resident weights (WeightPrepack.pack,
+ *      backend/hmx_weight_prepack.py:124-212; hexagon_runtime_weight_resident_v2,
+ *      bin/runtime/include/HexagonCAPI.h:52-53) ---- */
+
+typedef enum hxm_image_kind {
+  HXM_IMAGE_GEMM = 0,  /* src B [K,N] (rows = K, cols = N) -> the [N,K] image of
+                          hxm_prepack_weight; I8/F16/BF16 keep their dtype, an F32
+                          source becomes an F16 image (-0 -> +0, then RNE) */
+  HXM_IMAGE_W8A16 = 1  /* src W [N,K] int8 (rows = N, cols = K) -> the packed
+                          image of hxm_prepack_w8a16 */
+} hxm_image_kind;
+
+/* Returns (in *image) the library-owned resident image of src, packing it on
+ * the first call for this content and reusing it afterwards: the cache key
+ * is (kind, device, rows, cols, src_dtype, a 128-bit hash of every source
+ * element and its position), so equal content at another address hits and a
+ * one-element change misses.  expect_dtype >= 0 and expect_shape (rows,
+ * cols) != NULL are the caller's contract: a mismatch is refused
+ * ("unsupported-dtype" / "invalid-argument") before anything is packed.
+ * *image_dtype receives the image dtype.  Synchronises `stream` once (the
+ * hash is read back).  Images stay valid until hxm_release_cache(). */
+hxm_status hxm_resident_weight(const void* src, int64_t ld, int64_t rows,
+                               int64_t cols, int32_t src_dtype,
+                               int32_t expect_dtype, const int64_t* expect_shape,
+                               int32_t kind, const void** image,
+                               int32_t* image_dtype, void* stream);
 
 /* ---- SwiGLU FFN block (RMSNorm -> int8-weight gate/up
  *      GEMMs -> SiLU*mul -> down GEMM).  The reference composes it from the

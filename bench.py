@@ -12,14 +12,16 @@ Also reported under "extra" (not the headline): the int32-output int8 GEMM,
 the fp16 256^3 matmul (launch-bound), W8A16 GEMV M in {1,4,16} and softmax /
 RMSNorm rows on f16 [8192 x 4096] (HBM-bound: timed while rotating buffer
 sets larger than the 256 MB Infinity Cache), the SwiGLU FFN block (tokens
-2048, hidden 4096, intermediate 11008; tiles autotuned per GEMM) and a plain
-256 MiB device copy (the practical HBM copy rate next to the nominal peak).
+2048, hidden 4096, intermediate 11008; tiles autotuned per GEMM), a plain
+256 MiB device copy (the practical HBM copy rate next to the nominal peak),
+and for context the vendor library (hipBLASLt via torch._int_mm /
+torch.matmul) on the 4096^3 shapes next to this library's f16 4096^3 matmul.
 
 cpu_baseline: the C restatement in oracle/ (OpenMP over the host cores)
 timed on a bounded row sample of the same GEMM.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-       python bench.py --only {int8,int8_i32,f16,gemv,rows,ffn,copy}  (one workload,
+       python bench.py --only {int8,int8_i32,f16,gemv,rows,ffn,copy,vendor}  (one workload,
        for rocprofv3 runs; prints that workload's record)
 """
 from __future__ import annotations
@@ -241,6 +243,36 @@ def run_ffn(c):
         "tuned": {"gate_up_swiglu": list(cfg_gu.as_tuple()), "down": list(cfg_d.as_tuple())}}}
 
 
+def run_vendor(c):
+    """Context, not the product: the vendor library (hipBLASLt behind
+    torch._int_mm / torch.matmul) on the same shapes, next to this library's
+    f16 4096^3 matmul with a resident B."""
+    torch, hxm, L = c.torch, c.hxm, c.L
+    n = 4096
+    A = torch.randint(-127, 128, (n, n), dtype=torch.int8, device=c.dev)
+    Bt = torch.randint(-127, 128, (n, n), dtype=torch.int8, device=c.dev).t()  # column-major
+    Ah = (torch.rand(n, n, device=c.dev) * 2 - 1).half()
+    Bh = (torch.rand(n, n, device=c.dev) * 2 - 1).half()
+    Bnk = Bh.t().contiguous()                       # resident [N, K] image of B
+    Ch = torch.empty(n, n, dtype=torch.float16, device=c.dev)
+    out = {}
+    ms, _ = c.time_ms(lambda i: torch._int_mm(A, Bt), 100, 10)
+    out["vendor_int_mm_4096"] = {"us": ms * 1e3, "TOPS": 2 * n ** 3 / (ms * 1e-3) / 1e12,
+                                 "what": "torch._int_mm (hipBLASLt), int8 -> int32, B column-major"}
+    ms, _ = c.time_ms(lambda i: torch.matmul(Ah, Bnk.t()), 100, 10)
+    out["vendor_f16_matmul_4096"] = {"us": ms * 1e3, "TFLOPS": 2 * n ** 3 / (ms * 1e-3) / 1e12,
+                                     "what": "torch.matmul (hipBLASLt), f16, B = [N,K] transposed view"}
+    pa, pb, pc, st = Ah.data_ptr(), Bnk.data_ptr(), Ch.data_ptr(), c.stream
+
+    def f16(_):
+        hxm.check(L.hxm_matmul(pa, n, pb, n, hxm.B_NK, pc, n, n, n, n, hxm.F16, hxm.F16, 0,
+                               None, st), "hxm_matmul")
+    ms, _ = c.time_ms(f16, 100, 10)
+    out["f16_matmul_4096"] = {"us": ms * 1e3, "TFLOPS": 2 * n ** 3 / (ms * 1e-3) / 1e12,
+                              "mfma_frac": 2 * n ** 3 / (ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS}
+    return out
+
+
 def run_copy(c):
     """A plain 256 MiB device copy (torch's elementwise copy kernel): the
     known-size reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE."""
@@ -340,7 +372,8 @@ def main() -> int:
                     help="approximate CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=["int8", "int8_i32", "f16", "gemv", "rows", "ffn", "copy"])
+    ap.add_argument("--only", choices=["int8", "int8_i32", "f16", "gemv", "rows", "ffn", "copy",
+                                       "vendor"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build is the single-GPU kernel set of the hot "
@@ -354,7 +387,7 @@ def main() -> int:
             rec = {args.only: run_int8(c, *int8_operands(c), out_i32=args.only == "int8_i32")}
         else:
             rec = {"f16": run_f16, "gemv": run_gemv, "rows": run_rows, "ffn": run_ffn,
-                   "copy": run_copy}[
+                   "copy": run_copy, "vendor": run_vendor}[
                 args.only](c)
         print(json.dumps(rec), flush=True)
         return 0
@@ -367,7 +400,7 @@ def main() -> int:
     extra = {}
     if not args.no_extra:
         extra["int8_gemm_i32_out_4096"] = run_int8(c, A, Bp, rs, cs, out_i32=True)
-        for fn in (run_f16, run_gemv, run_rows, run_ffn, run_copy):
+        for fn in (run_f16, run_gemv, run_rows, run_ffn, run_copy, run_vendor):
             extra.update(fn(c))
         for k, v in extra.items():
             log(k, json.dumps(v))

@@ -469,9 +469,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   wait_and_barrier<0>();  // stage buffers free; scales landed and visible
   float* stg = reinterpret_cast<float*>(buf(wave % STAGES)) + (wave / STAGES) * kStageWords;
 
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    // 1. registers -> LDS (row r32, 4 consecutive columns per group)
+  // A tile wholly inside C with 16-byte aligned rows takes a branch-free
+  // path (one wave per SIMD: nothing hides a per-run LDS round trip).
+  const bool full8 = g.vec8_store && m0 + BM <= g.M && n0 + BN <= g.N;
+
+  // 1. registers -> LDS: block row i, lane row r32, 4 consecutive columns
+  // per register group, as raw 32-bit words.
+  auto stage_block = [&](int i) {
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -491,6 +495,115 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         }
         *reinterpret_cast<v4f32*>(stg + r32 * kPad + j * 32 + q * 8 + hi * 4) = w;
       }
+  };
+
+  // Full tiles: one straight-line sequence over all block rows, every LDS
+  // read of a block issued before its arithmetic.  With 8-element runs a
+  // lane's columns are the same in every pass, col8 = (lane % kRpr8) * 8, so
+  // its column scales are read once.
+  if constexpr (EPI == kEpiDequant || EPI == kEpiW8) {
+    if (full8) {
+      constexpr int kRpr8 = TN / 8;            // 8-element runs per staged row
+      constexpr int kRowsIt8 = 64 / kRpr8;     // rows one pass of the wave covers
+      constexpr int kIt8 = 32 / kRowsIt8;      // passes per 32-row block
+      static_assert(64 % kRpr8 == 0 && kIt8 >= 1, "8-element runs must tile the wave");
+      const int col8 = (lane % kRpr8) * 8, rsub8 = lane / kRpr8;
+      const float* csp = ssc + QR * 64 + wn * TN + col8;
+      const v4f32 cs8[2] = {*reinterpret_cast<const v4f32*>(csp),
+                            *reinterpret_cast<const v4f32*>(csp + 4)};
+      const int64_t step = static_cast<int64_t>(kRowsIt8) * g.ldc;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        stage_block(i);
+        v4f32 w0[kIt8], w1[kIt8];
+        float rsv[kIt8];
+#pragma unroll
+        for (int it = 0; it < kIt8; ++it) {
+          const int row = it * kRowsIt8 + rsub8;
+          w0[it] = *reinterpret_cast<const v4f32*>(stg + row * kPad + col8);
+          w1[it] = *reinterpret_cast<const v4f32*>(stg + row * kPad + col8 + 4);
+          rsv[it] = EPI == kEpiDequant ? ssc[wm * TM + i * 32 + row] : 1.0f;
+        }
+        _Float16* c = static_cast<_Float16*>(g.C) +
+                      static_cast<int64_t>(mw + i * 32 + rsub8) * g.ldc + nw + col8;
+#pragma unroll
+        for (int it = 0; it < kIt8; ++it) {
+          v8f16 h;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float we = e < 4 ? w0[it][e] : w1[it][e - 4];
+            const float ce = cs8[e / 4][e % 4];
+            // Same spellings as the general path below.
+            float p;
+            if constexpr (EPI == kEpiDequant)
+              p = (static_cast<float>(__builtin_bit_cast(int32_t, we)) * rsv[it]) * ce;
+            else
+              p = we * ce;
+            asm volatile("" : "+v"(p));
+            h[e] = static_cast<_Float16>(p);
+          }
+          __builtin_nontemporal_store(h, reinterpret_cast<v8f16*>(c + it * step));
+        }
+      }
+      return;
+    }
+  }
+  if constexpr (EPI == kEpiI32 || EPI == kEpiFloat) {
+    // Full tile, plain overwrite: 4-element runs, no per-run checks, one
+    // row address per block.
+    if (g.vec_store && !g.accumulate && m0 + BM <= g.M && n0 + BN <= g.N) {
+      constexpr int kRunsPerRow = TN / 4;
+      constexpr int kIt4 = 32 * TN / 4 / 64;
+      constexpr int kRowsIt4 = 64 / kRunsPerRow;
+      static_assert(64 % kRunsPerRow == 0, "4-element runs must tile the wave");
+      const int col = (lane % kRunsPerRow) * 4, rsub = lane / kRunsPerRow;
+      const int64_t step = static_cast<int64_t>(kRowsIt4) * g.ldc;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        stage_block(i);
+        v4f32 wv[kIt4];
+#pragma unroll
+        for (int it = 0; it < kIt4; ++it)
+          wv[it] = *reinterpret_cast<const v4f32*>(stg + (it * kRowsIt4 + rsub) * kPad + col);
+        const int64_t off0 = static_cast<int64_t>(mw + i * 32 + rsub) * g.ldc + nw + col;
+        if constexpr (EPI == kEpiI32) {
+          int32_t* c = static_cast<int32_t*>(g.C) + off0;
+#pragma unroll
+          for (int it = 0; it < kIt4; ++it)
+            __builtin_nontemporal_store(__builtin_bit_cast(v4u32_t, wv[it]),
+                                        reinterpret_cast<v4u32_t*>(c + it * step));
+        } else if (g.out_dtype == HXM_F32) {
+          float* c = static_cast<float*>(g.C) + off0;
+#pragma unroll
+          for (int it = 0; it < kIt4; ++it) *reinterpret_cast<v4f32*>(c + it * step) = wv[it];
+        } else if (g.out_dtype == HXM_F16) {
+          _Float16* c = static_cast<_Float16*>(g.C) + off0;
+#pragma unroll
+          for (int it = 0; it < kIt4; ++it) {
+            v4f16_t h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = static_cast<_Float16>(wv[it][e]);
+            *reinterpret_cast<v4f16_t*>(c + it * step) = h;
+          }
+        } else {
+          __bf16* c = static_cast<__bf16*>(g.C) + off0;
+#pragma unroll
+          for (int it = 0; it < kIt4; ++it) {
+            v4bf16_t h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = static_cast<__bf16>(wv[it][e]);
+            *reinterpret_cast<v4bf16_t*>(c + it * step) = h;
+          }
+        }
+      }
+      return;
+    }
+  }
+
+  // General path: edge tiles, accumulate, unaligned rows.
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    stage_block(i);
     // 2. LDS -> global.  The dequant output takes 8 consecutive f16 of one
     // row per lane (16-byte stores); the other outputs 4 elements per lane.
     if constexpr (EPI == kEpiDequant) {
@@ -602,11 +715,21 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     }
     constexpr int kRuns = 32 * TN / 4;          // 4-element runs in the block
     constexpr int kRunsPerRow = TN / 4;
+    constexpr int kIt4 = kRuns / 64;
+    static_assert(64 % kRunsPerRow == 0, "4-element runs must tile the wave");
+    // Every run of the block is read from LDS before any is converted.
+    v4f32 wv[kIt4];
 #pragma unroll
-    for (int it = 0; it < kRuns / 64; ++it) {
+    for (int it = 0; it < kIt4; ++it) {
+      const int run = it * 64 + lane;
+      wv[it] = *reinterpret_cast<const v4f32*>(stg + (run / kRunsPerRow) * kPad +
+                                               (run % kRunsPerRow) * 4);
+    }
+#pragma unroll
+    for (int it = 0; it < kIt4; ++it) {
       const int run = it * 64 + lane;
       const int row = run / kRunsPerRow, col = (run % kRunsPerRow) * 4;
-      const v4f32 w = *reinterpret_cast<const v4f32*>(stg + row * kPad + col);
+      const v4f32 w = wv[it];
       const int m = mw + i * 32 + row, n = nw + col;
       if (m >= g.M || n >= g.N) continue;
       const int64_t off = static_cast<int64_t>(m) * g.ldc + n;

@@ -95,6 +95,18 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
   const int r16 = lane & 15;                    // W row (channel) for A; x row for B
   const int kq = lane >> 4;                     // 16-byte quarter of the 64-wide slab
   const int slabs = (g.K + 63) / 64;
+  // The per-channel scales wave 0 applies at the end, loaded before the weight
+  // stream so that no dependent memory round trip sits in the kernel's tail.
+  float sc[CB][4];
+  if (wave == 0) {
+#pragma unroll
+    for (int b = 0; b < CB; ++b)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int no = n0 + 16 * b + 4 * kq + v;
+        sc[b][v] = static_cast<float>(g.scale[no < g.N ? no : g.N - 1]);
+      }
+  }
   const int8_t* wsrc[CB];                       // per channel group
 #pragma unroll
   for (int b = 0; b < CB; ++b) {
@@ -194,10 +206,7 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int no = n0 + 16 * b + 4 * (lane >> 4) + v;
-      if (no < g.N) {
-        const float sc = static_cast<float>(g.scale[no]);
-        g.y[static_cast<int64_t>(mo) * g.ldy + no] = static_cast<_Float16>(tot[v] * sc);
-      }
+      if (no < g.N) g.y[static_cast<int64_t>(mo) * g.ldy + no] = static_cast<_Float16>(tot[v] * sc[b][v]);
     }
   }
 }

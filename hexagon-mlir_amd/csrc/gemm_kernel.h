@@ -497,53 +497,97 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
       }
   };
 
-  // Full tiles: one straight-line sequence over all block rows, every LDS
-  // read of a block issued before its arithmetic.  With 8-element runs a
-  // lane's columns are the same in every pass, col8 = (lane % kRpr8) * 8, so
-  // its column scales are read once.
-  if constexpr (EPI == kEpiDequant || EPI == kEpiW8) {
+  // Full tiles, 8-element f16 output rows: a branch-free pipeline over
+  // half-blocks (32 rows x TN/2 columns, block row i = n / 2, columns half
+  // h = n % 2) through two LDS staging buffers per wave.  Half-block n+1 is
+  // written to LDS while the VALU converts half-block n, and all LDS reads of
+  // a half-block are issued before its arithmetic.  The buffer written for
+  // n+1 was last read for n-1, earlier in program order; a wave's LDS
+  // operations complete in order, so the write never overtakes that read.
+  // With 8-element runs a lane's columns are the same in every pass,
+  // col8 = (lane % kRprH) * 8, so its column scales are read once.
+  if constexpr ((EPI == kEpiDequant || EPI == kEpiW8) && FN % 2 == 0) {
     if (full8) {
-      constexpr int kRpr8 = TN / 8;            // 8-element runs per staged row
-      constexpr int kRowsIt8 = 64 / kRpr8;     // rows one pass of the wave covers
-      constexpr int kIt8 = 32 / kRowsIt8;      // passes per 32-row block
-      static_assert(64 % kRpr8 == 0 && kIt8 >= 1, "8-element runs must tile the wave");
-      const int col8 = (lane % kRpr8) * 8, rsub8 = lane / kRpr8;
-      const float* csp = ssc + QR * 64 + wn * TN + col8;
-      const v4f32 cs8[2] = {*reinterpret_cast<const v4f32*>(csp),
-                            *reinterpret_cast<const v4f32*>(csp + 4)};
-      const int64_t step = static_cast<int64_t>(kRowsIt8) * g.ldc;
+      constexpr int TNH = TN / 2;
+      constexpr int kPadH = TNH + 4;             // staging row stride (words)
+      constexpr int kWordsH = 32 * kPadH;        // one half-block buffer
+      constexpr int kRprH = TNH / 8;             // 8-element runs per staged row
+      constexpr int kRowsItH = 64 / kRprH;       // rows one pass of the wave covers
+      constexpr int kItH = 32 / kRowsItH;        // passes per half-block
+      constexpr int NH = FM * 2;                 // half-blocks per wave
+      static_assert(64 % kRprH == 0 && kItH >= 1, "8-element runs must tile the wave");
+      static_assert(kWavesPerBuf * 2 * kWordsH * 4 <= SB, "epilogue staging must fit a stage");
+      float* hb0 = reinterpret_cast<float*>(buf(wave % STAGES)) + (wave / STAGES) * 2 * kWordsH;
+      float* hb1 = hb0 + kWordsH;
+      const int col8 = (lane % kRprH) * 8, rsub8 = lane / kRprH;
+      v4f32 csh[2][2];
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        stage_block(i);
-        v4f32 w0[kIt8], w1[kIt8];
-        float rsv[kIt8];
+      for (int h = 0; h < 2; ++h) {
+        const float* csp = ssc + QR * 64 + wn * TN + h * TNH + col8;
+        csh[h][0] = *reinterpret_cast<const v4f32*>(csp);
+        csh[h][1] = *reinterpret_cast<const v4f32*>(csp + 4);
+      }
+      // Registers -> LDS: block columns [h*FN/2, (h+1)*FN/2) of block row i.
+      auto stage_half = [&](int n, float* dst) {
+        const int i = n / 2, h = n % 2;
 #pragma unroll
-        for (int it = 0; it < kIt8; ++it) {
-          const int row = it * kRowsIt8 + rsub8;
-          w0[it] = *reinterpret_cast<const v4f32*>(stg + row * kPad + col8);
-          w1[it] = *reinterpret_cast<const v4f32*>(stg + row * kPad + col8 + 4);
-          rsv[it] = EPI == kEpiDequant ? ssc[wm * TM + i * 32 + row] : 1.0f;
+        for (int jj = 0; jj < FN / 2; ++jj)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            v4f32 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if constexpr (EPI == kEpiW8) {
+                w[e] = acc[i][h * (FN / 2) + jj][q * 4 + e];
+              } else {
+                // Copy the element out first (see stage_block).
+                const int32_t a = acc[i][h * (FN / 2) + jj][q * 4 + e];
+                w[e] = __builtin_bit_cast(float, a);
+              }
+            }
+            *reinterpret_cast<v4f32*>(dst + r32 * kPadH + jj * 32 + q * 8 + hi * 4) = w;
+          }
+      };
+      v4f32 w0[2][kItH], w1[2][kItH];
+      float rsv[2][kItH];
+      auto read_half = [&](int n, const float* src, int set) {
+#pragma unroll
+        for (int it = 0; it < kItH; ++it) {
+          const int row = it * kRowsItH + rsub8;
+          w0[set][it] = *reinterpret_cast<const v4f32*>(src + row * kPadH + col8);
+          w1[set][it] = *reinterpret_cast<const v4f32*>(src + row * kPadH + col8 + 4);
+          rsv[set][it] = EPI == kEpiDequant ? ssc[wm * TM + (n / 2) * 32 + row] : 1.0f;
         }
-        _Float16* c = static_cast<_Float16*>(g.C) +
-                      static_cast<int64_t>(mw + i * 32 + rsub8) * g.ldc + nw + col8;
+      };
+      const int64_t step = static_cast<int64_t>(kRowsItH) * g.ldc;
+      stage_half(0, hb0);
+      read_half(0, hb0, 0);
 #pragma unroll
-        for (int it = 0; it < kIt8; ++it) {
-          v8f16 h;
+      for (int n = 0; n < NH; ++n) {
+        const int cur = n & 1;
+        if (n + 1 < NH) stage_half(n + 1, cur ? hb0 : hb1);
+        const int i = n / 2, h = n % 2;
+        _Float16* c = static_cast<_Float16*>(g.C) +
+                      static_cast<int64_t>(mw + i * 32 + rsub8) * g.ldc + nw + h * TNH + col8;
+#pragma unroll
+        for (int it = 0; it < kItH; ++it) {
+          v8f16 hv;
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float we = e < 4 ? w0[it][e] : w1[it][e - 4];
-            const float ce = cs8[e / 4][e % 4];
+            const float we = e < 4 ? w0[cur][it][e] : w1[cur][it][e - 4];
+            const float ce = csh[h][e / 4][e % 4];
             // Same spellings as the general path below.
             float p;
             if constexpr (EPI == kEpiDequant)
-              p = (static_cast<float>(__builtin_bit_cast(int32_t, we)) * rsv[it]) * ce;
+              p = (static_cast<float>(__builtin_bit_cast(int32_t, we)) * rsv[cur][it]) * ce;
             else
               p = we * ce;
             asm volatile("" : "+v"(p));
-            h[e] = static_cast<_Float16>(p);
+            hv[e] = static_cast<_Float16>(p);
           }
-          __builtin_nontemporal_store(h, reinterpret_cast<v8f16*>(c + it * step));
+          __builtin_nontemporal_store(hv, reinterpret_cast<v8f16*>(c + it * step));
         }
+        if (n + 1 < NH) read_half(n + 1, cur ? hb0 : hb1, cur ^ 1);
       }
       return;
     }

@@ -224,6 +224,10 @@ hxm_status run_gemm(int32_t op, int32_t ab_dtype, int epi, const void* A,
   g.row_scale = rs;
   g.col_scale = cs;
   g.group_m = 4;
+  g.n_out = 0;
+  g.residual = nullptr;
+  g.ldr = 0;
+  g.res_vec8 = 0;
   {
     const int64_t ob = dtype_bytes(out_dtype);
     g.vec_store = (reinterpret_cast<uintptr_t>(C) % (4 * ob) == 0) && ((ldc * ob) % (4 * ob) == 0);
@@ -292,7 +296,7 @@ __global__ __launch_bounds__(256) void swiglu_pack_kernel(
 hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const int8_t* W,
                        int64_t ldw, const float* scale, void* C, int64_t ldc, int64_t M,
                        int64_t N, int64_t K, int64_t n_out, const hxm_gemm_config* cfg,
-                       hipStream_t stream) {
+                       hipStream_t stream, const void* residual = nullptr, int64_t ldr = 0) {
   const bool sw = epi == kEpiSwiglu;
   hxm_gemm_config c;
   if (cfg && cfg->bm) {
@@ -325,11 +329,14 @@ hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const in
   g.col_scale = scale;
   g.group_m = 4;
   g.n_out = static_cast<int>(n_out);
+  g.residual = static_cast<const _Float16*>(residual);
+  g.ldr = ldr;
+  g.res_vec8 = residual && (reinterpret_cast<uintptr_t>(residual) % 16 == 0) && ((ldr * 2) % 16 == 0);
   g.vec_store = (reinterpret_cast<uintptr_t>(C) % 8 == 0) && ((ldc * 2) % 8 == 0);
   g.vec8_store = (reinterpret_cast<uintptr_t>(C) % 16 == 0) && ((ldc * 2) % 16 == 0);
   const int64_t tiles = ((M + e->cfg.bm - 1) / e->cfg.bm) * ((N + e->cfg.bn - 1) / e->cfg.bn);
   const int wi = static_cast<int>(e - kW8Kernels);
-  hipLaunchKernelGGL(kW8Fns[wi][sw ? 1 : 0], dim3(static_cast<unsigned>(tiles)),
+  hipLaunchKernelGGL(kW8Fns[wi][sw ? 1 : epi == kEpiW8Res ? 2 : 0], dim3(static_cast<unsigned>(tiles)),
                      dim3(e->threads), 0, stream, g);
   if ((st = check_launch("w8a16 gemm kernel")) != HXM_OK) return st;
   return ok();
@@ -474,6 +481,35 @@ hxm_status hxm_gemm_w8a16(const void* x, int64_t ldx, const int8_t* W, int64_t l
   if (st != HXM_OK) return st;
   return run_gemm_w8(kEpiW8, kOpW8, x, ldx, W, ldw, w_scale, y, ldy, M, N, K, N, cfg,
                      as_stream(stream));
+}
+
+hxm_status hxm_gemm_w8a16_residual(const void* x, int64_t ldx, const int8_t* W, int64_t ldw,
+                                   const float* w_scale, const void* r, int64_t ldr, void* y,
+                                   int64_t ldy, int64_t M, int64_t N, int64_t K,
+                                   const hxm_gemm_config* cfg, void* stream) {
+  hxm_status st =
+      validate_w8("gemm_w8a16_residual", x, ldx, W, ldw, w_scale, y, ldy, M, N, K, N);
+  if (st != HXM_OK) return st;
+  if (M > 0 && N > 0 && !r)
+    return fail(HXM_INVALID_ARG, "invalid-argument: gemm_w8a16_residual null residual");
+  if (ldr < N)
+    return fail(HXM_INVALID_ARG, "invalid-argument: gemm_w8a16_residual ldr=%lld < N=%lld",
+                (long long)ldr, (long long)N);
+  // r is either y itself (an in-place update: every element is read by the
+  // lane that then writes it) or disjoint from y.
+  if (M > 0 && N > 0 && r != y) {
+    const uintptr_t r0 = reinterpret_cast<uintptr_t>(r), y0 = reinterpret_cast<uintptr_t>(y);
+    const uintptr_t r1 = r0 + static_cast<uintptr_t>(((M - 1) * ldr + N) * 2);
+    const uintptr_t y1 = y0 + static_cast<uintptr_t>(((M - 1) * ldy + N) * 2);
+    if (r0 < y1 && y0 < r1)
+      return fail(HXM_INVALID_ARG,
+                  "invalid-argument: gemm_w8a16_residual r overlaps y without being y");
+  }
+  if (r == y && ldr != ldy)
+    return fail(HXM_INVALID_ARG,
+                "invalid-argument: gemm_w8a16_residual in place needs ldr == ldy");
+  return run_gemm_w8(kEpiW8Res, kOpW8, x, ldx, W, ldw, w_scale, y, ldy, M, N, K, N, cfg,
+                     as_stream(stream), r, ldr);
 }
 
 int64_t hxm_swiglu_packed_rows(int64_t I) { return I < 0 ? -1 : 128 * ((I + 63) / 64); }

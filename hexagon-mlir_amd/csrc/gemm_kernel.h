@@ -60,12 +60,15 @@ enum Epilogue {
   kEpiDequant = 1,  // int8: f16(((float)acc * rs[m]) * cs[n])
   kEpiFloat = 2,    // f16/bf16: fp32 acc -> out dtype (accumulate honoured)
   kEpiW8 = 3,       // f16 A x int8 B: f16(acc * cs[n])
-  kEpiSwiglu = 4    // f16 A x int8 gate/up image: f16(silu(g * sg) * (u * su))
+  kEpiSwiglu = 4,   // f16 A x int8 gate/up image: f16(silu(g * sg) * (u * su))
+  kEpiW8Res = 5     // f16 A x int8 B: f16((acc * cs[n]) + r[m, n]), fp32 sum
 };
 
 // The int8-weight epilogues take B as int8 [N, K] converted to f16 in
 // registers (the W8A16 GEMM of the SwiGLU FFN).
-constexpr bool b_is_int8(int epi) { return epi == kEpiW8 || epi == kEpiSwiglu; }
+constexpr bool b_is_int8(int epi) {
+  return epi == kEpiW8 || epi == kEpiSwiglu || epi == kEpiW8Res;
+}
 constexpr int32_t kOpW8 = HXM_OP_W8A16, kOpSwiglu = HXM_OP_W8A16_SWIGLU;  // tuning-cache keys
 
 struct GemmArgs {
@@ -82,6 +85,9 @@ struct GemmArgs {
   const float* col_scale;
   int group_m;  // tile-rows per group in the XCD walk
   int n_out;    // kEpiSwiglu: output columns (gate/up channel count)
+  const _Float16* residual;  // kEpiW8Res: r [M, N] f16, row stride ldr
+  int64_t ldr;
+  int res_vec8;  // r rows allow 16-byte loads
 };
 
 template <typename T>
@@ -506,8 +512,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   // operations complete in order, so the write never overtakes that read.
   // With 8-element runs a lane's columns are the same in every pass,
   // col8 = (lane % kRprH) * 8, so its column scales are read once.
-  if constexpr ((EPI == kEpiDequant || EPI == kEpiW8) && FN % 2 == 0) {
-    if (full8) {
+  // kEpiW8Res adds the residual run of each output run: its loads are
+  // issued two half-blocks ahead (a ring of three register sets), so they
+  // land under the staging and arithmetic of the half-blocks in between.
+  if constexpr ((EPI == kEpiDequant || EPI == kEpiW8 || EPI == kEpiW8Res) && FN % 2 == 0) {
+    if (full8 && (EPI != kEpiW8Res || g.res_vec8)) {
       constexpr int TNH = TN / 2;
       constexpr int kPadH = TNH + 4;             // staging row stride (words)
       constexpr int kWordsH = 32 * kPadH;        // one half-block buffer
@@ -537,7 +546,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
             v4f32 w;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              if constexpr (EPI == kEpiW8) {
+              if constexpr (EPI != kEpiDequant) {
                 w[e] = acc[i][h * (FN / 2) + jj][q * 4 + e];
               } else {
                 // Copy the element out first (see stage_block).
@@ -560,11 +569,28 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         }
       };
       const int64_t step = static_cast<int64_t>(kRowsItH) * g.ldc;
+      constexpr int kRes = EPI == kEpiW8Res ? kItH : 1;
+      v8f16 rres[3][kRes];
+      const _Float16* rbase =
+          EPI == kEpiW8Res ? g.residual + static_cast<int64_t>(mw + rsub8) * g.ldr + nw + col8
+                           : nullptr;
+      auto load_res = [&](int n) {
+        if constexpr (EPI == kEpiW8Res) {
+#pragma unroll
+          for (int it = 0; it < kItH; ++it)
+            rres[n % 3][it] = *reinterpret_cast<const v8f16*>(
+                rbase + static_cast<int64_t>((n / 2) * 32 + it * kRowsItH) * g.ldr +
+                (n % 2) * TNH);
+        }
+      };
+      load_res(0);
+      if (NH > 1) load_res(1);
       stage_half(0, hb0);
       read_half(0, hb0, 0);
 #pragma unroll
       for (int n = 0; n < NH; ++n) {
         const int cur = n & 1;
+        if (n + 2 < NH) load_res(n + 2);
         if (n + 1 < NH) stage_half(n + 1, cur ? hb0 : hb1);
         const int i = n / 2, h = n % 2;
         _Float16* c = static_cast<_Float16*>(g.C) +
@@ -583,6 +609,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
             else
               p = we * ce;
             asm volatile("" : "+v"(p));
+            if constexpr (EPI == kEpiW8Res) {
+              // fp32 sum, then one rounding to f16: the pin keeps the
+              // backend from fusing the add into a mixed-precision fma.
+              p = p + static_cast<float>(rres[n % 3][it][e]);
+              asm volatile("" : "+v"(p));
+            }
             hv[e] = static_cast<_Float16>(p);
           }
           __builtin_nontemporal_store(hv, reinterpret_cast<v8f16*>(c + it * step));
@@ -687,8 +719,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
       }
       continue;
     }
-    if constexpr (EPI == kEpiW8) {
-      // f16(acc * cs[n]): the fp32 product, then one rounding to f16.
+    if constexpr (EPI == kEpiW8 || EPI == kEpiW8Res) {
+      // f16(acc * cs[n]) (+ r[m, n] in fp32 for kEpiW8Res): the fp32
+      // product, the fp32 sum, then one rounding to f16.
       constexpr int kRuns8 = 32 * TN / 8, kRunsPerRow8 = TN / 8;
 #pragma unroll
       for (int it = 0; it < kRuns8 / 64; ++it) {
@@ -701,11 +734,23 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         const float* csp = ssc + QR * 64 + wn * TN + col;
         const v4f32 c0 = *reinterpret_cast<const v4f32*>(csp);
         const v4f32 c1 = *reinterpret_cast<const v4f32*>(csp + 4);
+        v8f16 rv = {};
+        if constexpr (EPI == kEpiW8Res) {
+          const _Float16* r = g.residual + static_cast<int64_t>(m) * g.ldr + n;
+          if (g.res_vec8 && n + 8 <= g.N)
+            rv = *reinterpret_cast<const v8f16*>(r);
+          else
+            for (int e = 0; e < 8 && n + e < g.N; ++e) rv[e] = r[e];
+        }
         v8f16 h;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           float p = (e < 4 ? w0[e] : w1[e - 4]) * (e < 4 ? c0[e] : c1[e - 4]);
           asm volatile("" : "+v"(p));
+          if constexpr (EPI == kEpiW8Res) {
+            p = p + static_cast<float>(rv[e]);
+            asm volatile("" : "+v"(p));
+          }
           h[e] = static_cast<_Float16>(p);
         }
         _Float16* c = static_cast<_Float16*>(g.C) + static_cast<int64_t>(m) * g.ldc + n;
@@ -843,6 +888,6 @@ typedef void (*gemm_fn)(GemmArgs);
 // HXM_GEMM_CONFIG_LIST; row i of kW8Fns is entry i of HXM_W8_CONFIG_LIST.
 extern const gemm_fn kI8Fns[][2];   // {kEpiI32, kEpiDequant}
 extern const gemm_fn kF16Fns[][2];  // {f16, bf16} operands, kEpiFloat
-extern const gemm_fn kW8Fns[][2];   // {kEpiW8, kEpiSwiglu (null unless TN == 128)}
+extern const gemm_fn kW8Fns[][3];   // {kEpiW8, kEpiSwiglu (null unless TN == 128), kEpiW8Res}
 
 }  // namespace hxm

@@ -1,5 +1,5 @@
-// W8A16 GEMM kernels (f16 x int8 weights: per-channel scale and fused
-// SwiGLU epilogues) for every entry of HXM_W8_CONFIG_LIST.
+// W8A16 GEMM kernels (f16 x int8 weights: per-channel scale, fused SwiGLU
+// and residual-add epilogues) for every entry of HXM_W8_CONFIG_LIST.
 #include "gemm_kernel.h"
 
 namespace hxm {
@@ -14,9 +14,11 @@ constexpr gemm_fn swiglu_fn() {
     return nullptr;
 }
 
-#define HXM_W8_FNS(BM, BN, BKB, ST, WM, WN) \
-  {gemm_kernel<_Float16, BM, BN, BKB, ST, WM, WN, kEpiW8>, swiglu_fn<BM, BN, BKB, ST, WM, WN>()}
+#define HXM_W8_FNS(BM, BN, BKB, ST, WM, WN)                                    \
+  {gemm_kernel<_Float16, BM, BN, BKB, ST, WM, WN, kEpiW8>,                       \
+   swiglu_fn<BM, BN, BKB, ST, WM, WN>(),                                         \
+   gemm_kernel<_Float16, BM, BN, BKB, ST, WM, WN, kEpiW8Res>}
 
-extern const gemm_fn kW8Fns[][2] = {HXM_W8_CONFIG_LIST(HXM_W8_FNS)};
+extern const gemm_fn kW8Fns[][3] = {HXM_W8_CONFIG_LIST(HXM_W8_FNS)};
 
 }  // namespace hxm

@@ -41,7 +41,7 @@ hxm_gemm_config default_w8_config(int64_t M, int64_t N, bool swiglu);
 hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const int8_t* W,
                        int64_t ldw, const float* scale, void* C, int64_t ldc, int64_t M,
                        int64_t N, int64_t K, int64_t n_out, const hxm_gemm_config* cfg,
-                       hipStream_t stream);
+                       hipStream_t stream, const void* residual = nullptr, int64_t ldr = 0);
 constexpr int kEpiW8Code = 3, kEpiSwigluCode = 4;  // gemm.hip's Epilogue values
 
 // Constants of hmx_search.py :172-205 (tile edge, min rows, front-end block

@@ -75,6 +75,8 @@ SIGNATURES = {
     "hxm_w8a16_packed_bytes": (_i64, [_i64, _i64]),
     "hxm_prepack_w8a16": (_st, [_p, _i64, _i64, _i64, _p, _i64, _p]),
     "hxm_gemm_w8a16": (_st, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _cfgp, _p]),
+    "hxm_gemm_w8a16_residual": (_st, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64,
+                                      _i64, _cfgp, _p]),
     "hxm_swiglu_packed_rows": (_i64, [_i64]),
     "hxm_swiglu_pack": (_st, [_p, _p, _i64, _p, _p, _i64, _i64, _p, _p, _p]),
     "hxm_gemm_w8a16_swiglu": (_st, [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _cfgp, _p]),

@@ -193,9 +193,12 @@ def _f32_vec(t: torch.Tensor, n: int, name: str) -> torch.Tensor:
 
 
 def gemm_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor,
-               out: Optional[torch.Tensor] = None, *, config=None, stream=None) -> torch.Tensor:
+               out: Optional[torch.Tensor] = None, *, residual: Optional[torch.Tensor] = None,
+               config=None, stream=None) -> torch.Tensor:
     """y = f16((x @ W.T in fp32) * scale) for f16 x [M, K], int8 W [N, K] and
-    fp32 per-channel scale [N] (the large-M W8A16 GEMM of the FFN)."""
+    fp32 per-channel scale [N] (the large-M W8A16 GEMM of the FFN).  With an
+    f16 ``residual`` [M, N]: y = f16(fp32((x @ W.T) * scale) + residual)
+    (hxm_gemm_w8a16_residual); ``out`` may be ``residual`` itself."""
     _mat(x, "x"), _mat(W, "W")
     M, K = x.shape
     N = W.shape[0]
@@ -206,6 +209,16 @@ def gemm_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor,
         out = torch.empty((M, N), dtype=torch.float16, device=x.device)
     _mat(out, "out")
     cfg = _cfg(config)
+    if residual is not None:
+        _mat(residual, "residual")
+        if tuple(residual.shape) != (M, N) or residual.dtype != torch.float16:
+            raise ValueError(f"residual must be f16 [{M}, {N}]")
+        st = lib.hxm_gemm_w8a16_residual(x.data_ptr(), _ld(x), W.data_ptr(), _ld(W),
+                                         scale.data_ptr(), residual.data_ptr(), _ld(residual),
+                                         out.data_ptr(), _ld(out), M, N, K, _ptr_or_none(cfg),
+                                         _stream(stream))
+        check(st, "hxm_gemm_w8a16_residual")
+        return out
     st = lib.hxm_gemm_w8a16(x.data_ptr(), _ld(x), W.data_ptr(), _ld(W), scale.data_ptr(),
                             out.data_ptr(), _ld(out), M, N, K, _ptr_or_none(cfg),
                             _stream(stream))
@@ -258,13 +271,16 @@ def gemm_w8a16_swiglu(x: torch.Tensor, Wgu: torch.Tensor, sgu: torch.Tensor, I: 
 
 def swiglu_ffn(x: torch.Tensor, gamma: torch.Tensor, Wgu: torch.Tensor, sgu: torch.Tensor,
                Wd: torch.Tensor, sd: torch.Tensor, I: int, *, eps: float = 1e-6,
-               configs=(None, None), stream=None) -> torch.Tensor:
+               residual: bool = False, configs=(None, None), stream=None) -> torch.Tensor:
     """The Llama-style SwiGLU FFN block: RMSNorm -> fused gate/up GEMM with
     SiLU * mul -> down GEMM.  x f16 [T, H]; gamma f16 [H]; Wgu/sgu from
-    :func:`swiglu_pack`; Wd int8 [H, I] with fp32 scales sd [H]."""
+    :func:`swiglu_pack`; Wd int8 [H, I] with fp32 scales sd [H].  With
+    ``residual`` the down GEMM's epilogue adds x: the block returns
+    x + FFN(x)."""
     xn = rms_norm(x, (x.shape[-1],), gamma, eps=eps, stream=stream)
     h = gemm_w8a16_swiglu(xn, Wgu, sgu, I, config=configs[0], stream=stream)
-    return gemm_w8a16(h, Wd, sd, config=configs[1], stream=stream)
+    return gemm_w8a16(h, Wd, sd, residual=x if residual else None, config=configs[1],
+                      stream=stream)
 
 
 def w8a16_configs(swiglu: bool = False):

@@ -245,6 +245,21 @@ hxm_status hxm_gemm_w8a16(const void* x, int64_t ldx, const int8_t* W,
                           int64_t ldy, int64_t M, int64_t N, int64_t K,
                           const hxm_gemm_config* cfg, void* stream);
 
+/* W8A16 GEMM with a fused residual add -- the read-out that adds a resident
+ * tensor before the store (hmx_unpack_acc_f32 with residual,
+ * bin/runtime/hmx/include/HMXAPI.h:245-275; the FFN block's x + FFN(x)):
+ *   y[m,n] = rne_f16( f32( (sum_k f32(x[m,k]) * f32(W[n,k])) * f32(w_scale[n]) )
+ *                     + f32(r[m,n]) )
+ * the product and the sum each rounded to fp32, then one rounding to f16.
+ * r fp16 [M,N] (ldr >= N) is either y itself (in place, ldr == ldy) or
+ * disjoint from y ("invalid-argument" otherwise).  Everything else as
+ * hxm_gemm_w8a16 (tiles from the same tuned-winner cache). */
+hxm_status hxm_gemm_w8a16_residual(const void* x, int64_t ldx, const int8_t* W,
+                                   int64_t ldw, const float* w_scale,
+                                   const void* r, int64_t ldr, void* y,
+                                   int64_t ldy, int64_t M, int64_t N, int64_t K,
+                                   const hxm_gemm_config* cfg, void* stream);
+
 /* Rows of the fused gate/up image for I intermediate channels:
  * 128 * ceil(I / 64) (-1 for I < 0). */
 int64_t hxm_swiglu_packed_rows(int64_t I);

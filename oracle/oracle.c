@@ -19,6 +19,8 @@
  *   hxo_gemm_w8a16     the same with fp32 scales (the FFN projections of the
  *                      BASELINE SwiGLU block; int8 operands of linalg.matmul
  *                      take the HVX path, ScheduleMatmulForHVXPass.cpp:44-80).
+ *   hxo_gemm_w8a16_residual  the same plus a residual (x + FFN(x)):
+ *                      f16(f32(acc * scale) + f32(r)).
  *   hxo_swiglu_gateup  gate/up projections + SiLU * mul of that block:
  *                      h = f16(silu(g) * u), g = acc_g * sg, u = acc_u * su,
  *                      silu(g) = g / (1 + exp(-g)) evaluated in fp64.
@@ -260,6 +262,29 @@ void hxo_gemm_w8a16(const uint16_t* x, int64_t ldx, const int8_t* W, int64_t ldw
       for (int64_t k = 0; k < K; ++k)
         s += hxo_f16_to_f32(x[m * ldx + k]) * (float)W[n * ldw + k];
       y[m * ldy + n] = hxo_f32_to_f16(s * scale[n]);
+    }
+  }
+}
+
+/* y[m,n] = f16(f32(acc * scale[n]) + f32(r[m,n])) with acc the fp32 sum of
+ * hxo_gemm_w8a16: the read-out that adds a resident tensor before the store
+ * (hmx_unpack_acc_f32 with residual, bin/runtime/hmx/include/HMXAPI.h
+ * :245-275).  Product and sum each round to fp32 (no fma: -ffp-contract=off),
+ * then one rounding to f16.  r may be y (in place). */
+void hxo_gemm_w8a16_residual(const uint16_t* x, int64_t ldx, const int8_t* W, int64_t ldw,
+                             const float* scale, const uint16_t* r, int64_t ldr, uint16_t* y,
+                             int64_t ldy, int64_t M, int64_t N, int64_t K, int threads) {
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+#endif
+  for (int64_t n = 0; n < N; ++n) {
+    for (int64_t m = 0; m < M; ++m) {
+      float s = 0.0f;
+      for (int64_t k = 0; k < K; ++k)
+        s += hxo_f16_to_f32(x[m * ldx + k]) * (float)W[n * ldw + k];
+      const float p = s * scale[n];
+      y[m * ldy + n] = hxo_f32_to_f16(p + hxo_f16_to_f32(r[m * ldr + n]));
     }
   }
 }

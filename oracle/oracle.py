@@ -81,6 +81,8 @@ _SIGS = {
                           _i64, _i64, _i64, _i32]),
     "hxo_gemv_w8a16": (None, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32]),
     "hxo_gemm_w8a16": (None, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32]),
+    "hxo_gemm_w8a16_residual": (None, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64,
+                                       _i64, _i32]),
     "hxo_swiglu_gateup": (None, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64,
                                  _i32]),
     "hxo_softmax_rows": (None, [_p, _i64, _p, _i64, _i64, _i64, _i32]),
@@ -235,6 +237,23 @@ def gemm_w8a16(x_bits: np.ndarray, W: np.ndarray, scale: np.ndarray,
     return y
 
 
+def gemm_w8a16_residual(x_bits: np.ndarray, W: np.ndarray, scale: np.ndarray,
+                        r_bits: np.ndarray, threads: int = 0) -> np.ndarray:
+    """y = f16(f32((x . W^T) * scale) + r): x, r f16 bits [M,K] / [M,N], W int8 [N,K],
+    scale fp32 [N] (oracle.c hxo_gemm_w8a16_residual)."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    W = np.ascontiguousarray(W, dtype=np.int8)
+    sc = np.ascontiguousarray(scale, dtype=np.float32)
+    r = np.ascontiguousarray(r_bits, dtype=np.uint16)
+    M, K = x.shape
+    N = W.shape[0]
+    assert r.shape == (M, N)
+    y = np.zeros((M, N), dtype=np.uint16)
+    lib().hxo_gemm_w8a16_residual(_ptr(x), K, _ptr(W), K, _ptr(sc), _ptr(r), N, _ptr(y), N, M,
+                                  N, K, threads)
+    return y
+
+
 def swiglu_gateup(x_bits: np.ndarray, Wg: np.ndarray, Wu: np.ndarray, sg: np.ndarray,
                   su: np.ndarray, threads: int = 0) -> np.ndarray:
     """h = f16(silu(g) * u) with g = (x . Wg^T) * sg, u = (x . Wu^T) * su."""
@@ -252,11 +271,14 @@ def swiglu_gateup(x_bits: np.ndarray, Wg: np.ndarray, Wu: np.ndarray, sg: np.nda
 
 
 def swiglu_ffn(x_bits: np.ndarray, gamma_bits: np.ndarray, Wg, Wu, sg, su, Wd, sd,
-               eps: float = 1e-6, threads: int = 0) -> np.ndarray:
+               eps: float = 1e-6, threads: int = 0, residual: bool = False) -> np.ndarray:
     """The BASELINE SwiGLU FFN block with fp16 tensors between the stages:
-    xn = rmsnorm(x) (f16), h = swiglu_gateup(xn) (f16), y = gemm_w8a16(h, Wd)."""
+    xn = rmsnorm(x) (f16), h = swiglu_gateup(xn) (f16), y = gemm_w8a16(h, Wd);
+    with residual, y = gemm_w8a16_residual(h, Wd, r=x) = x + FFN(x)."""
     xn = rmsnorm_rows(x_bits, gamma_bits, eps, "f16")
     h = swiglu_gateup(xn, Wg, Wu, sg, su, threads)
+    if residual:
+        return gemm_w8a16_residual(h, Wd, sd, x_bits, threads)
     return gemm_w8a16(h, Wd, sd, threads)
 
 

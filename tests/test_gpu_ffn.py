@@ -84,6 +84,72 @@ def test_gemm_w8a16_strided_and_refusals(dev):
                        s.to(dev))
 
 
+@pytest.mark.parametrize("M,N,K", [(256, 256, 512), (300, 260, 1024), (33, 96, 64),
+                                   (1, 40, 16), (512, 4096, 1024)])
+def test_gemm_w8a16_residual(dev, M, N, K):
+    print(f"gemm_w8a16_residual M={M} N={N} K={K}", flush=True)
+    x, W, s = operands(M, N, K, M + N + K + 1)
+    r = (4 * torch.randn(M, N, generator=torch.Generator().manual_seed(M + N))).half()
+    y = ops.gemm_w8a16(x.to(dev), W.to(dev), s.to(dev), residual=r.to(dev))
+    ref = orc.gemm_w8a16_residual(bits(x), W.numpy(), s.numpy(), bits(r))
+    np.testing.assert_allclose(y.float().cpu().numpy(), f32(ref), **TOL)
+
+
+@pytest.mark.parametrize("cfg", ops.w8a16_configs(), ids=repr)
+def test_gemm_w8a16_residual_every_config(dev, cfg):
+    """Full tiles take the pipelined epilogue, edge tiles the general one."""
+    print(f"gemm_w8a16_residual config {cfg}", flush=True)
+    M, N, K = 520, 544, 640
+    x, W, s = operands(M, N, K, 9)
+    r = torch.randn(M, N, generator=torch.Generator().manual_seed(10)).half()
+    y = ops.gemm_w8a16(x.to(dev), W.to(dev), s.to(dev), residual=r.to(dev), config=cfg)
+    ref = orc.gemm_w8a16_residual(bits(x), W.numpy(), s.numpy(), bits(r))
+    np.testing.assert_allclose(y.float().cpu().numpy(), f32(ref), **TOL)
+
+
+def test_gemm_w8a16_residual_bit_exact_and_in_place(dev):
+    """Small integers make every sum exact, so the result must equal the
+    oracle bit for bit; the in-place form (out is the residual) gives the
+    same bits; the KAT p = 1 + 2^-20, r = 2048 shows the fp32 sum is rounded
+    before the f16 conversion (2048, not the single-rounding 2050)."""
+    g = torch.Generator().manual_seed(12)
+    M, N, K = 512, 512, 256
+    x = torch.randint(-4, 5, (M, K), generator=g).half()
+    W = torch.randint(-8, 9, (N, K), generator=g, dtype=torch.int8)
+    s = torch.full((N,), 0.125)
+    r = torch.randint(-64, 65, (M, N), generator=g).half()
+    xd, Wd, sd = x.to(dev), W.to(dev), s.to(dev)
+    y = ops.gemm_w8a16(xd, Wd, sd, residual=r.to(dev))
+    ref = orc.gemm_w8a16_residual(bits(x), W.numpy(), s.numpy(), bits(r))
+    assert np.array_equal(bits(y), ref)
+    yi = r.to(dev)
+    ops.gemm_w8a16(xd, Wd, sd, out=yi, residual=yi)
+    assert np.array_equal(bits(yi), ref)
+    xk = torch.zeros(256, 256).half()
+    xk[:, 0] = 1
+    Wk = torch.zeros(256, 256, dtype=torch.int8)
+    Wk[:, 0] = 1
+    sk = torch.full((256,), 1.0 + 2 ** -20)
+    rk = torch.full((256, 256), 2048.0).half()
+    yk = ops.gemm_w8a16(xk.to(dev), Wk.to(dev), sk.to(dev), residual=rk.to(dev))
+    assert (yk.float().cpu() == 2048.0).all()
+
+
+def test_gemm_w8a16_residual_refusals(dev):
+    x, W, s = operands(64, 128, 256, 13)
+    xd, Wd, sd = x.to(dev), W.to(dev), s.to(dev)
+    buf = torch.zeros(66, 128, dtype=torch.float16, device=dev)
+    with pytest.raises(Exception, match="overlaps"):
+        ops.gemm_w8a16(xd, Wd, sd, out=buf[1:65], residual=buf[0:64])
+    import hxm
+    L = hxm.lib
+    y = torch.empty(64, 128, dtype=torch.float16, device=dev)
+    st = L.hxm_gemm_w8a16_residual(xd.data_ptr(), 256, Wd.data_ptr(), 256, sd.data_ptr(),
+                                   buf.data_ptr(), 100, y.data_ptr(), 128, 64, 128, 256, None,
+                                   None)
+    assert st != 0 and "ldr" in hxm.last_error()
+
+
 def test_swiglu_pack_layout(dev):
     """Image rows [128c, 128c+64) = gate channels [64c, 64c+64), the next 64
     rows the same up channels; channels >= I zero rows with zero scale."""
@@ -155,10 +221,11 @@ def ffn_operands(T, H, I, seed):
     return x, gamma, Wg, Wu, Wd, sg, su, sd
 
 
-def run_ffn(dev, x, gamma, Wg, Wu, Wd, sg, su, sd):
+def run_ffn(dev, x, gamma, Wg, Wu, Wd, sg, su, sd, residual=False):
     I = Wg.shape[0]
     Wgu, sgu = ops.swiglu_pack(Wg.to(dev), Wu.to(dev), sg.to(dev), su.to(dev))
-    return ops.swiglu_ffn(x.to(dev), gamma.to(dev), Wgu, sgu, Wd.to(dev), sd.to(dev), I)
+    return ops.swiglu_ffn(x.to(dev), gamma.to(dev), Wgu, sgu, Wd.to(dev), sd.to(dev), I,
+                          residual=residual)
 
 
 def test_swiglu_ffn_block(dev):
@@ -168,6 +235,17 @@ def test_swiglu_ffn_block(dev):
     x, gamma, Wg, Wu, Wd, sg, su, sd = ops_
     ref = orc.swiglu_ffn(bits(x), bits(gamma), Wg.numpy(), Wu.numpy(), sg.numpy(),
                          su.numpy(), Wd.numpy(), sd.numpy())
+    np.testing.assert_allclose(y.float().cpu().numpy(), f32(ref), rtol=1e-2, atol=2e-3)
+
+
+def test_swiglu_ffn_block_with_residual(dev):
+    """x + FFN(x): the residual is added in the down GEMM's epilogue."""
+    T, H, I = 256, 512, 704
+    ops_ = ffn_operands(T, H, I, 22)
+    y = run_ffn(dev, *ops_, residual=True)
+    x, gamma, Wg, Wu, Wd, sg, su, sd = ops_
+    ref = orc.swiglu_ffn(bits(x), bits(gamma), Wg.numpy(), Wu.numpy(), sg.numpy(),
+                         su.numpy(), Wd.numpy(), sd.numpy(), residual=True)
     np.testing.assert_allclose(y.float().cpu().numpy(), f32(ref), rtol=1e-2, atol=2e-3)
 
 

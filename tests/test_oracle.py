@@ -196,6 +196,40 @@ def test_gemm_w8a16_vs_numpy_f64_and_small_integer_kat():
     assert np.array_equal(y3, np.array([[32.0, 64.0, 16.0]], np.float32))
 
 
+def test_gemm_w8a16_residual_pins():
+    rng = np.random.default_rng(8)
+    x = h(rng.standard_normal((9, 80)))
+    W = rng.integers(-127, 128, (13, 80)).astype(np.int8)
+    sc = rng.uniform(0.001, 0.02, 13).astype(np.float32)
+    r = h(4 * rng.standard_normal((9, 13)))
+    y = orc.f16_bits_to_f32(orc.gemm_w8a16_residual(x, W, sc, r))
+    p = (orc.f16_bits_to_f32(x).astype(np.float64) @ W.T.astype(np.float64)) * sc
+    rf = orc.f16_bits_to_f32(r).astype(np.float64)
+    # within ~1 f16 ulp of the float64 sum, measured against the magnitude of
+    # its terms (the sum can cancel)
+    assert np.all(np.abs(y - (p + rf)) <= 2 ** -10 * (np.abs(p) + np.abs(rf)) + 1e-6)
+    # a -0 residual is the identity of fp32 addition: bit for bit gemm_w8a16
+    mz = np.full((9, 13), 0x8000, np.uint16)
+    assert np.array_equal(orc.gemm_w8a16_residual(x, W, sc, mz), orc.gemm_w8a16(x, W, sc))
+    # zero weights leave the residual (0 * s + r = r exactly)
+    assert np.array_equal(orc.f16_bits_to_f32(
+        orc.gemm_w8a16_residual(x, np.zeros_like(W), sc, r)), orc.f16_bits_to_f32(r))
+    # the residual is added after the per-channel scale, per output element
+    y3 = orc.f16_bits_to_f32(orc.gemm_w8a16_residual(
+        h(np.ones((1, 32))), np.ones((3, 32), np.int8), np.array([1.0, 2.0, 0.5], np.float32),
+        h([[1.0, -2.0, 0.25]])))
+    assert np.array_equal(y3, np.array([[33.0, 62.0, 16.25]], np.float32))
+    # the sum rounds to fp32 before f16: p = 1 + 2^-20, r = 2048 -> fp32 2049,
+    # an f16 tie that goes to even, 2048; one rounding of the exact sum
+    # (a fused add-and-convert) gives 2050
+    xk = np.zeros((1, 16)); xk[0, 0] = 1.0
+    Wk = np.zeros((1, 16), np.int8); Wk[0, 0] = 1
+    yk = orc.f16_bits_to_f32(orc.gemm_w8a16_residual(
+        h(xk), Wk, np.array([1.0 + 2 ** -20], np.float32), h([[2048.0]])))
+    assert yk[0, 0] == 2048.0
+    assert np.float16(np.float64(1.0 + 2 ** -20) + 2048.0) == 2050.0
+
+
 def test_swiglu_gateup_vs_numpy_f64_and_limits():
     rng = np.random.default_rng(5)
     K = 64
@@ -238,6 +272,8 @@ def test_swiglu_ffn_composes_the_stages():
     xn = orc.rmsnorm_rows(x, gamma, 1e-6, "f16")
     hh = orc.swiglu_gateup(xn, Wg, Wu, sg, su)
     assert np.array_equal(y, orc.gemm_w8a16(hh, Wd, sd))
+    yr = orc.swiglu_ffn(x, gamma, Wg, Wu, sg, su, Wd, sd, residual=True)
+    assert np.array_equal(yr, orc.gemm_w8a16_residual(hh, Wd, sd, x))
 
 
 # ---- row reductions ----------------------------------------------------------------

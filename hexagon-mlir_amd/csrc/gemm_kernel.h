@@ -624,6 +624,84 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
       return;
     }
   }
+  // SwiGLU on full tiles: the same two-buffer half-block pipeline.  The
+  // wave's 128 image columns are 64 gate channels then the same 64 up
+  // channels, so half-block h (h = 0, 1) stages gate block h next to up
+  // block h + 2: each staged row holds 32 gate and the matching 32 up values,
+  // output channels nw/2 + 32h + 0..31.
+  if constexpr (EPI == kEpiSwiglu) {
+    if (g.vec8_store && m0 + BM <= g.M && n0 + BN <= g.N && (n0 + BN) / 2 <= g.n_out) {
+      constexpr int kPadS = 64 + 4;              // staging row stride (words)
+      constexpr int kWordsS = 32 * kPadS;        // one half-block buffer
+      constexpr int kRprS = 32 / 8;              // 8-channel runs per staged row
+      constexpr int kRowsItS = 64 / kRprS;       // rows one pass covers
+      constexpr int kItS = 32 / kRowsItS;        // passes per half-block
+      constexpr int NH = FM * 2;
+      static_assert(FN == 4, "SwiGLU wave tile is 128 columns");
+      static_assert(kWavesPerBuf * 2 * kWordsS * 4 <= SB, "epilogue staging must fit a stage");
+      float* hb0 = reinterpret_cast<float*>(buf(wave % STAGES)) + (wave / STAGES) * 2 * kWordsS;
+      float* hb1 = hb0 + kWordsS;
+      const int ch = (lane % kRprS) * 8, rsub = lane / kRprS;
+      v4f32 sgv[2][2], suv[2][2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float* sp = ssc + QR * 64 + wn * TN + h * 32 + ch;
+        sgv[h][0] = *reinterpret_cast<const v4f32*>(sp);
+        sgv[h][1] = *reinterpret_cast<const v4f32*>(sp + 4);
+        suv[h][0] = *reinterpret_cast<const v4f32*>(sp + 64);
+        suv[h][1] = *reinterpret_cast<const v4f32*>(sp + 68);
+      }
+      auto stage_sw = [&](int n, float* dst) {
+        const int i = n / 2, h = n % 2;
+#pragma unroll
+        for (int part = 0; part < 2; ++part)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            v4f32 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = acc[i][h + 2 * part][q * 4 + e];
+            *reinterpret_cast<v4f32*>(dst + r32 * kPadS + part * 32 + q * 8 + hi * 4) = w;
+          }
+      };
+      v4f32 gv[2][kItS][2], uv[2][kItS][2];
+      auto read_sw = [&](const float* src, int set) {
+#pragma unroll
+        for (int it = 0; it < kItS; ++it) {
+          const float* sp = src + (it * kRowsItS + rsub) * kPadS + ch;
+          gv[set][it][0] = *reinterpret_cast<const v4f32*>(sp);
+          gv[set][it][1] = *reinterpret_cast<const v4f32*>(sp + 4);
+          uv[set][it][0] = *reinterpret_cast<const v4f32*>(sp + 32);
+          uv[set][it][1] = *reinterpret_cast<const v4f32*>(sp + 36);
+        }
+      };
+      const int64_t step = static_cast<int64_t>(kRowsItS) * g.ldc;
+      stage_sw(0, hb0);
+      read_sw(hb0, 0);
+#pragma unroll
+      for (int n = 0; n < NH; ++n) {
+        const int cur = n & 1;
+        if (n + 1 < NH) stage_sw(n + 1, cur ? hb0 : hb1);
+        const int i = n / 2, h = n % 2;
+        _Float16* c = static_cast<_Float16*>(g.C) +
+                      static_cast<int64_t>(mw + i * 32 + rsub) * g.ldc + nw / 2 + h * 32 + ch;
+#pragma unroll
+        for (int it = 0; it < kItS; ++it) {
+          v8f16 hv;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            // Same arithmetic as the general path below.
+            const float gval = gv[cur][it][e / 4][e % 4] * sgv[h][e / 4][e % 4];
+            const float uval = uv[cur][it][e / 4][e % 4] * suv[h][e / 4][e % 4];
+            const float ex = __builtin_amdgcn_exp2f(-gval * 1.4426950408889634f);
+            hv[e] = static_cast<_Float16>(gval * __builtin_amdgcn_rcpf(1.0f + ex) * uval);
+          }
+          __builtin_nontemporal_store(hv, reinterpret_cast<v8f16*>(c + it * step));
+        }
+        if (n + 1 < NH) read_sw(cur ? hb0 : hb1, cur ^ 1);
+      }
+      return;
+    }
+  }
   if constexpr (EPI == kEpiI32 || EPI == kEpiFloat) {
     // Full tile, plain overwrite: 4-element runs, no per-run checks, one
     // row address per block.

@@ -46,14 +46,24 @@ struct KernelEntry {
 
 #define HXM_ENTRY(BM, BN, BKB, ST, WM, WN) KernelEntry{{BM, BN, BKB, WM, WN, ST, 1}, WM * WN * 64}
 
-// Row i holds the configuration of row i of kI8Fns / kF16Fns.
+// Row i holds the configuration of row i of the kI8Fns / kF16Fns tables.
 static const KernelEntry kKernels[] = {HXM_GEMM_CONFIG_LIST(HXM_ENTRY)};
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
-// W8A16 kernels (row i of kW8Fns): cfg.bk in A bytes (bk = BKB/2 f16
+// W8A16 kernels (row i of the kW8Fns tables): cfg.bk in A bytes (bk = BKB/2 f16
 // elements on the way out).
 static const KernelEntry kW8Kernels[] = {HXM_W8_CONFIG_LIST(HXM_ENTRY)};
 constexpr int kNumW8Kernels = sizeof(kW8Kernels) / sizeof(kW8Kernels[0]);
+
+// Entry e of row i of a kernel table compiled in kGemmParts parts: row i
+// lives in part i mod kGemmParts, the other parts hold null there.
+template <int E>
+static gemm_fn part_fn(const gemm_fn (*const parts[kGemmParts])[E], int i, int e) {
+  return parts[i % kGemmParts][i][e];
+}
+static const gemm_fn (*const kI8Parts[kGemmParts])[2] = {kI8Fns_p0, kI8Fns_p1, kI8Fns_p2};
+static const gemm_fn (*const kF16Parts[kGemmParts])[2] = {kF16Fns_p0, kF16Fns_p1, kF16Fns_p2};
+static const gemm_fn (*const kW8Parts[kGemmParts])[3] = {kW8Fns_p0, kW8Fns_p1, kW8Fns_p2};
 
 static int elem_bytes(int32_t dt) { return dt == HXM_I8 ? 1 : 2; }
 
@@ -81,11 +91,11 @@ const KernelEntry* find_kernel(const hxm_gemm_config& c, int32_t dt) {
 // the first entry of this preference list whose tile count still gives every
 // CU a workgroup, else the 64x64 tile.
 hxm_gemm_config default_config(int64_t M, int64_t N, int32_t dt) {
-  // bm, bn, bk bytes, stages.  The two-stage 256x256 tile is the int8
-  // choice; with f16/bf16 operands that kernel spills registers, so the
-  // four-stage tile leads there.
+  // bm, bn, bk bytes, stages.  The two-stage 256x256 tile with 128-byte K
+  // stages leads for every dtype (measured at 4096^3: f16 110 us against
+  // 112 us for the four-stage 64-byte tile, bf16 98 against 104 us).
   static const int order_i8[][4] = {{256, 256, 128, 2}, {256, 256, 64, 4}, {128, 128, 128, 2}};
-  static const int order_f16[][4] = {{256, 256, 64, 4}, {256, 128, 128, 3}, {128, 128, 128, 2}};
+  static const int order_f16[][4] = {{256, 256, 128, 2}, {256, 256, 64, 4}, {128, 128, 128, 2}};
   for (auto& o : (dt == HXM_I8 ? order_i8 : order_f16)) {
     const int64_t tiles = ((M + o[0] - 1) / o[0]) * ((N + o[1] - 1) / o[1]);
     if (tiles >= 256) {
@@ -107,9 +117,9 @@ hxm_status launch_gemm(const KernelEntry& e, int32_t ab_dtype, int epi,
   const int i = static_cast<int>(&e - kKernels);
   gemm_fn fn = nullptr;
   if (ab_dtype == HXM_I8)
-    fn = kI8Fns[i][epi == kEpiDequant ? 1 : 0];
+    fn = part_fn(kI8Parts, i, epi == kEpiDequant ? 1 : 0);
   else
-    fn = kF16Fns[i][ab_dtype == HXM_F16 ? 0 : 1];
+    fn = part_fn(kF16Parts, i, ab_dtype == HXM_F16 ? 0 : 1);
   hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(tiles)), dim3(e.threads), 0,
                      stream, g);
   return check_launch("gemm kernel");
@@ -245,7 +255,7 @@ hxm_gemm_config w8_kernel_config(int i) {
   c.bk /= 2;  // f16 elements of K per stage
   return c;
 }
-bool w8_kernel_has_swiglu(int i) { return kW8Fns[i][1] != nullptr; }
+bool w8_kernel_has_swiglu(int i) { return part_fn(kW8Parts, i, 1) != nullptr; }
 
 static const KernelEntry* find_w8_kernel(const hxm_gemm_config& c, bool swiglu) {
   for (int i = 0; i < kNumW8Kernels; ++i) {
@@ -336,7 +346,8 @@ hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const in
   g.vec8_store = (reinterpret_cast<uintptr_t>(C) % 16 == 0) && ((ldc * 2) % 16 == 0);
   const int64_t tiles = ((M + e->cfg.bm - 1) / e->cfg.bm) * ((N + e->cfg.bn - 1) / e->cfg.bn);
   const int wi = static_cast<int>(e - kW8Kernels);
-  hipLaunchKernelGGL(kW8Fns[wi][sw ? 1 : epi == kEpiW8Res ? 2 : 0], dim3(static_cast<unsigned>(tiles)),
+  hipLaunchKernelGGL(part_fn(kW8Parts, wi, sw ? 1 : epi == kEpiW8Res ? 2 : 0),
+                     dim3(static_cast<unsigned>(tiles)),
                      dim3(e->threads), 0, stream, g);
   if ((st = check_launch("w8a16 gemm kernel")) != HXM_OK) return st;
   return ok();

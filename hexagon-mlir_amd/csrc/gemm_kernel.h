@@ -154,10 +154,14 @@ __device__ __forceinline__ v4i32 operand_rsrc(const uint8_t* base, int64_t ld_by
 // (wait_and_barrier).  Compiler-issued loads stay correct regardless, since
 // vmcnt counts in issue order and extra loads in flight only make the
 // compiler's own waits stricter.
-__device__ __forceinline__ void dma16(uint8_t* lds, v4i32 rsrc, uint32_t voffset, int soffset) {
-  // The LDS base (M0) and the scalar offset are wave-uniform by construction.
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)lds)));
+// `lds` is the LDS byte address (M0).  Callers form it from the low 32 bits
+// of the stage buffer's generic address (a generic address in the shared
+// aperture carries the LDS address there): that folds to scalar constants,
+// where a cast of the generic pointer back to the LDS address space cost a
+// null check and two readfirstlanes per load in the main loop.
+__device__ __forceinline__ void dma16(uint32_t lds, v4i32 rsrc, uint32_t voffset, int soffset) {
+  // The LDS address (M0) and the scalar offset are wave-uniform by construction.
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
   soffset = __builtin_amdgcn_readfirstlane(soffset);
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
@@ -196,14 +200,18 @@ struct StageLoad {
     }
   }
 
-  // Instruction i of a stage at K byte kb0; 16-byte chunks at or past
-  // K_bytes read as zero (only the last stage can straddle the end of K).
-  // The chunk is recomputed (a few VALU operations under the MFMAs) rather
-  // than kept in a register per instruction.
-  template <int I>
-  __device__ __forceinline__ void issue_one(v4i32 r, uint8_t* lds, int wave, int lane, int kb0,
+  // Instruction i of a stage at K byte kb0 into the stage buffer at LDS
+  // address lds.  CHECK: 16-byte chunks at or past K_bytes read as zero (a
+  // per-lane test).  Without it, a stage issued past the end of K reads other
+  // bytes of the operand or, past the resource, zeros; the kernel runs the
+  // unchecked form only when K_bytes is a multiple of the stage depth, where
+  // no stage it multiplies straddles K and the stages past the end land in
+  // buffers that are never multiplied.
+  template <int I, bool CHECK>
+  __device__ __forceinline__ void issue_one(v4i32 r, uint32_t lds, int wave, int lane, int kb0,
                                             int K_bytes) const {
-    const uint32_t o = kb0 + chunk_of(I, wave, lane) * 16 < K_bytes ? off[I] : kOob;
+    uint32_t o = off[I];
+    if constexpr (CHECK) o = kb0 + chunk_of(I, wave, lane) * 16 < K_bytes ? o : kOob;
     dma16(lds + (I * NW + wave) * 1024, r, o, kb0);
   }
 };
@@ -321,17 +329,20 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   const int K_bytes_B = BQ ? K_bytes / 2 : K_bytes;  // of B
 
   // DMA instruction D (A's first, then B's) of the stage at A byte kb0.
-  auto dma = [&](auto D, uint8_t* dst, int kb0) {
+  // CHK: std::true_type / std::false_type, the K-range test of issue_one.
+  auto dma = [&](auto D, auto CHK, uint8_t* dst, int kb0) {
     constexpr int d = decltype(D)::value;
+    constexpr bool chk = decltype(CHK)::value;
+    const uint32_t l = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
     if constexpr (d < LA::L) {
-      la.template issue_one<d>(ra, dst, wave, lane, kb0, K_bytes);
+      la.template issue_one<d, chk>(ra, l, wave, lane, kb0, K_bytes);
     } else {
       const int kb0_b = BQ ? kb0 / 2 : kb0;
-      lb.template issue_one<d - LA::L>(rb, dst + BM * BKB, wave, lane, kb0_b, K_bytes_B);
+      lb.template issue_one<d - LA::L, chk>(rb, l + BM * BKB, wave, lane, kb0_b, K_bytes_B);
     }
   };
   auto issue_stage = [&](int kt, uint8_t* dst) {
-    static_for<0, LPW>([&](auto D) { dma(D, dst, kt * BKB); });
+    static_for<0, LPW>([&](auto D) { dma(D, std::true_type{}, dst, kt * BKB); });
   };
 
   // Fragments of the k-step being multiplied ([ks & 1]) and of the next one.
@@ -395,7 +406,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   // reading stage kt, whose buffer the early DMAs of stage kt+STAGES then
   // refill.  It then reads stage kt+1's first fragments under the remaining
   // MFMAs.
-  auto stage = [&](auto U, int kt) {
+  auto stage = [&](auto U, auto CHK, int kt) {
     constexpr int u = decltype(U)::value;
     const uint8_t* cur = buf(u);
     const uint8_t* nxt = buf((u + 1) % STAGES);
@@ -411,8 +422,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         if constexpr (ks == KS - 1 && sl == HALF) wait_and_barrier<(STAGES - 2) * LPW>();
         static_for<0, LPW>([&](auto D) {
           constexpr int v = (decltype(D)::value * DW) / LPW - POST;
-          if constexpr (v >= 0 && v == slot) dma(D, dbuf, kbd);
-          if constexpr (v < 0 && SLOTS + v == slot) dma(D, ebuf, kbd + BKB);
+          if constexpr (v >= 0 && v == slot) dma(D, CHK, dbuf, kbd);
+          if constexpr (v < 0 && SLOTS + v == slot) dma(D, CHK, ebuf, kbd + BKB);
         });
         static_for<0, NR>([&](auto R) {
           constexpr int r = decltype(R)::value;
@@ -441,19 +452,27 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     });
     static_for<0, LPW>([&](auto D) {
       if constexpr ((decltype(D)::value * DW) / LPW - POST < 0)
-        dma(D, buf(STAGES - 1), (STAGES - 1) * BKB);
+        dma(D, std::true_type{}, buf(STAGES - 1), (STAGES - 1) * BKB);
     });
     wait_and_barrier<(STAGES - 2) * LPW + NEG>();
     static_for<0, NR>([&](auto R) { read(R, 0, buf(0), 0); });
     cvt_b(0, 0);
 
-    // Main loop, unrolled by STAGES so every buffer choice is static.
-    for (int kt0 = 0; kt0 < KT; kt0 += STAGES) {
-      static_for<0, STAGES>([&](auto U) {
-        const int kt = kt0 + decltype(U)::value;
-        if (kt < KT) stage(U, kt);
-      });
-    }
+    // Main loop, unrolled by STAGES so every buffer choice is static.  It is
+    // compiled twice: without the per-lane K test (K_bytes a multiple of the
+    // stage depth: two VALU operations fewer per LDS-DMA) and with it.
+    auto main_loop = [&](auto CHK) {
+      for (int kt0 = 0; kt0 < KT; kt0 += STAGES) {
+        static_for<0, STAGES>([&](auto U) {
+          const int kt = kt0 + decltype(U)::value;
+          if (kt < KT) stage(U, CHK, kt);
+        });
+      }
+    };
+    if (K_bytes % BKB == 0)
+      main_loop(std::false_type{});
+    else
+      main_loop(std::true_type{});
   }
 
   // ---- epilogue ----
@@ -961,11 +980,40 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
 
 typedef void (*gemm_fn)(GemmArgs);
 
-// The compiled kernels, one table per translation unit so the three sets
-// compile in parallel.  Row i of kI8Fns / kF16Fns is entry i of
-// HXM_GEMM_CONFIG_LIST; row i of kW8Fns is entry i of HXM_W8_CONFIG_LIST.
-extern const gemm_fn kI8Fns[][2];   // {kEpiI32, kEpiDequant}
-extern const gemm_fn kF16Fns[][2];  // {f16, bf16} operands, kEpiFloat
-extern const gemm_fn kW8Fns[][3];   // {kEpiW8, kEpiSwiglu (null unless TN == 128), kEpiW8Res}
+// The compiled kernels.  Each kernel source (gemm_i8.hip, gemm_f16.hip,
+// gemm_w8.hip) is compiled kGemmParts times with HXM_PART = 0 .. kGemmParts-1
+// so the objects build in parallel: part p instantiates the configurations
+// whose list index is p mod kGemmParts and leaves null entries for the rest.
+// Row i of kI8Fns_p* / kF16Fns_p* is entry i of HXM_GEMM_CONFIG_LIST; row i
+// of kW8Fns_p* is entry i of HXM_W8_CONFIG_LIST.  The host side takes the
+// non-null entry (gemm.hip).
+constexpr int kGemmParts = 3;
+
+struct ConfigKey {
+  int bm, bn, bkb, st, wm, wn;
+};
+#define HXM_CONFIG_KEY(BM, BN, BKB, ST, WM, WN) ConfigKey{BM, BN, BKB, ST, WM, WN}
+constexpr ConfigKey kGemmKeys[] = {HXM_GEMM_CONFIG_LIST(HXM_CONFIG_KEY)};
+constexpr ConfigKey kW8Keys[] = {HXM_W8_CONFIG_LIST(HXM_CONFIG_KEY)};
+
+// Position of configuration (BM, BN, BKB, ST, WM, WN) in `keys`.
+template <int N>
+constexpr int config_index(const ConfigKey (&keys)[N], int bm, int bn, int bkb, int st, int wm,
+                           int wn) {
+  for (int i = 0; i < N; ++i)
+    if (keys[i].bm == bm && keys[i].bn == bn && keys[i].bkb == bkb && keys[i].st == st &&
+        keys[i].wm == wm && keys[i].wn == wn)
+      return i;
+  return -1;
+}
+
+#define HXM_DECLARE_PART_TABLES(P)            \
+  extern const gemm_fn kI8Fns_p##P[][2];  /* {kEpiI32, kEpiDequant} */ \
+  extern const gemm_fn kF16Fns_p##P[][2]; /* {f16, bf16} operands, kEpiFloat */ \
+  extern const gemm_fn kW8Fns_p##P[][3];  /* {kEpiW8, kEpiSwiglu (null unless TN == 128), kEpiW8Res} */
+HXM_DECLARE_PART_TABLES(0)
+HXM_DECLARE_PART_TABLES(1)
+HXM_DECLARE_PART_TABLES(2)
+static_assert(kGemmParts == 3, "one HXM_DECLARE_PART_TABLES line per part");
 
 }  // namespace hxm

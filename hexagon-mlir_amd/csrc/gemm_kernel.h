@@ -131,13 +131,16 @@ __device__ __forceinline__ void wait_and_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// Buffer resource over rows [row0, rows_valid) of a K-major operand
-// (gfx9 descriptor: 48-bit base, stride 0, num_records in bytes, data format
-// word 0x00020000).  Offsets at or past num_records read as zero.
+// Buffer resource over rows [row0, rows_valid) of a K-major operand whose
+// rows hold row_bytes valid bytes (gfx9 descriptor: 48-bit base, stride 0,
+// num_records in bytes, data format word 0x00020000).  Offsets at or past
+// num_records read as zero.  The range ends at the last valid byte of the
+// last row, (rows - 1) * ld_bytes + row_bytes: the bytes between rows lie
+// inside the operand's storage, the bytes after its last row need not.
 __device__ __forceinline__ v4i32 operand_rsrc(const uint8_t* base, int64_t ld_bytes,
-                                              int row0, int rows_valid) {
+                                              int row0, int rows_valid, int64_t row_bytes) {
   const int64_t rows = rows_valid > row0 ? rows_valid - row0 : 0;
-  int64_t bytes = rows * ld_bytes;
+  int64_t bytes = rows > 0 ? (rows - 1) * ld_bytes + row_bytes : 0;
   if (bytes > 0x7fffffff) bytes = 0x7fffffff;
   const uint64_t a = reinterpret_cast<uint64_t>(base + static_cast<int64_t>(row0) * ld_bytes);
   v4i32 r;
@@ -298,8 +301,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   const int tn = (t % per_group) / gsize;
   const int m0 = tm * BM, n0 = tn * BN;
 
-  const v4i32 ra = operand_rsrc(g.A, g.lda_bytes, m0, g.M);
-  const v4i32 rb = operand_rsrc(g.B, g.ldb_bytes, n0, g.N);
+  const v4i32 ra = operand_rsrc(g.A, g.lda_bytes, m0, g.M, g.K_bytes);
+  const v4i32 rb = operand_rsrc(g.B, g.ldb_bytes, n0, g.N, BQ ? g.K_bytes / 2 : g.K_bytes);
   LA la;
   LB lb;
   la.init(g.lda_bytes, g.M - m0, wave, lane);
@@ -309,9 +312,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   // they arrive under the prologue and cost the epilogue one LDS read each.
   // Scales of rows / columns outside C read as zero.
   if constexpr (QR + QC > 0) {
-    const v4i32 rr = QR ? operand_rsrc(reinterpret_cast<const uint8_t*>(g.row_scale), 4, m0, g.M)
+    const v4i32 rr = QR ? operand_rsrc(reinterpret_cast<const uint8_t*>(g.row_scale), 4, m0, g.M, 4)
                         : v4i32{};
-    const v4i32 rc = operand_rsrc(reinterpret_cast<const uint8_t*>(g.col_scale), 4, n0, g.N);
+    const v4i32 rc = operand_rsrc(reinterpret_cast<const uint8_t*>(g.col_scale), 4, n0, g.N, 4);
     for (int q = wave; q < QR + QC; q += NW) {
       if (q < QR) dma4(ssc + q * 64, rr, (q * 64 + lane) * 4);
       else dma4(ssc + q * 64, rc, ((q - QR) * 64 + lane) * 4);

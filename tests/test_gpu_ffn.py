@@ -45,10 +45,11 @@ def test_gemm_w8a16(dev, M, N, K):
     np.testing.assert_allclose(y.float().cpu().numpy(), f32(ref), **TOL)
 
 
+@pytest.mark.parametrize("K", [640, 656])  # K bytes a multiple of every stage depth / not
 @pytest.mark.parametrize("cfg", ops.w8a16_configs(), ids=repr)
-def test_gemm_w8a16_every_config(dev, cfg):
-    print(f"gemm_w8a16 config {cfg}", flush=True)
-    M, N, K = 300, 520, 640
+def test_gemm_w8a16_every_config(dev, cfg, K):
+    print(f"gemm_w8a16 config {cfg} K={K}", flush=True)
+    M, N = 300, 520
     x, W, s = operands(M, N, K, 7)
     y = ops.gemm_w8a16(x.to(dev), W.to(dev), s.to(dev), config=cfg)
     ref = orc.gemm_w8a16(bits(x), W.numpy(), s.numpy())

@@ -9,6 +9,8 @@
 // The reference prices configs in device pcycles parsed from a launched
 // binary; here a config is one compiled HIP kernel and its score is the
 // hipEvent time of its launches on the caller's stream.
+#include <dlfcn.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -77,6 +79,68 @@ bool lookup_tuned(int32_t op, int64_t M, int64_t N, int64_t K, hxm_gemm_config* 
   *out = it->second;
   return true;
 }
+
+// ---- persisted winners ------------------------------------------------
+// The identity a saved winner carries, after hmx_search.py:416-442
+// (tuning_key_int): the build -- a hash of this library's binary, so a
+// rebuilt library never reuses another build's results -- and the device
+// shape (its CU count: a partitioned GPU is a different machine).  Entries
+// also record the measurement protocol (reps).
+namespace {
+uint64_t fnv1a(const unsigned char* p, size_t n, uint64_t h = 1469598103934665603ull) {
+  for (size_t i = 0; i < n; ++i) {
+    h ^= p[i];
+    h *= 1099511628211ull;
+  }
+  return h;
+}
+
+// FNV-1a of the file that holds this code (the loaded libhxm.so).
+hxm_status build_id(uint64_t* out) {
+  Dl_info info;
+  if (!dladdr(reinterpret_cast<void*>(&fnv1a), &info) || !info.dli_fname)
+    return fail(HXM_INVALID_ARG, "invalid-argument: cannot locate the library binary");
+  FILE* f = std::fopen(info.dli_fname, "rb");
+  if (!f) return fail(HXM_INVALID_ARG, "invalid-argument: cannot read %s", info.dli_fname);
+  uint64_t h = 1469598103934665603ull;
+  std::vector<unsigned char> buf(1 << 16);
+  size_t n;
+  while ((n = std::fread(buf.data(), 1, buf.size(), f)) > 0) h = fnv1a(buf.data(), n, h);
+  std::fclose(f);
+  *out = h;
+  return HXM_OK;
+}
+
+int device_cus() {
+  int dev = 0;
+  hipDeviceProp_t prop;
+  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
+    return 0;
+  return prop.multiProcessorCount;
+}
+
+bool same_config(const hxm_gemm_config& a, const hxm_gemm_config& b) {
+  return a.bm == b.bm && a.bn == b.bn && a.bk == b.bk && a.waves_m == b.waves_m &&
+         a.waves_n == b.waves_n && a.stages == b.stages && a.split_k == b.split_k;
+}
+
+// True when this build compiled `c` for `op`.
+bool config_compiled(int32_t op, const hxm_gemm_config& c) {
+  if (op == HXM_I8 || op == HXM_F16 || op == HXM_BF16) {
+    for (int i = 0; i < num_kernels(); ++i)
+      if (same_config(kernel_config(i, op), c)) return true;
+  } else if (op == HXM_OP_W8A16 || op == HXM_OP_W8A16_SWIGLU) {
+    for (int i = 0; i < num_w8_kernels(); ++i)
+      if (same_config(w8_kernel_config(i), c) &&
+          (op == HXM_OP_W8A16 || w8_kernel_has_swiglu(i)))
+        return true;
+  }
+  return false;
+}
+
+std::map<TuneKey, int32_t> g_tuned_reps;  // the reps each cached winner was measured with
+constexpr const char* kCacheMagic = "hxm-tune-cache 1";
+}  // namespace
 
 // ---- device helpers for the verify gate --------------------------------
 __global__ void count_mismatch_kernel(const uint32_t* a, int64_t lda_words,
@@ -230,7 +294,10 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
   hxm_gemm_config win = champ >= 0 ? cands[champ] : control;
   {
     std::lock_guard<std::mutex> lk(g_tune_mu);
-    if (champ >= 0) g_tuned[TuneKey(op, M, N, K)] = win;
+    if (champ >= 0) {
+      g_tuned[TuneKey(op, M, N, K)] = win;
+      g_tuned_reps[TuneKey(op, M, N, K)] = reps;
+    }
     if (canary_ok && round_valid) g_canary_ref[op] = c50;
   }
   if (best) *best = win;
@@ -436,8 +503,106 @@ int32_t hxm_canary_status(int32_t present, double q20, double q50, double q80,
   return std::fabs(delta) > gate ? 3 : 0;
 }
 
+int32_t hxm_tune_cache_lookup(int32_t op, int64_t M, int64_t N, int64_t K,
+                              hxm_gemm_config* out) {
+  hxm_gemm_config c;
+  if (!lookup_tuned(op, M, N, K, &c)) return 0;
+  if (out) *out = c;
+  return 1;
+}
+
+hxm_status hxm_tune_cache_save(const char* path) {
+  if (!path || !*path) return fail(HXM_INVALID_ARG, "invalid-argument: tune_cache_save path");
+  uint64_t bid = 0;
+  hxm_status st = build_id(&bid);
+  if (st != HXM_OK) return st;
+  const int cus = device_cus();
+  const std::string tmp = std::string(path) + ".tmp";
+  FILE* f = std::fopen(tmp.c_str(), "w");
+  if (!f) return fail(HXM_INVALID_ARG, "invalid-argument: cannot write %s", tmp.c_str());
+  {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    std::fprintf(f, "%s\nbuild %016llx\ncus %d\n", kCacheMagic, (unsigned long long)bid, cus);
+    for (const auto& kv : g_tuned) {
+      const hxm_gemm_config& c = kv.second;
+      auto r = g_tuned_reps.find(kv.first);
+      std::fprintf(f, "%d %lld %lld %lld %d %d %d %d %d %d %d %d\n", std::get<0>(kv.first),
+                   (long long)std::get<1>(kv.first), (long long)std::get<2>(kv.first),
+                   (long long)std::get<3>(kv.first), c.bm, c.bn, c.bk, c.waves_m, c.waves_n,
+                   c.stages, c.split_k, r == g_tuned_reps.end() ? 0 : r->second);
+    }
+  }
+  const bool closed = std::fclose(f) == 0;
+  if (!closed || std::rename(tmp.c_str(), path) != 0) {
+    std::remove(tmp.c_str());
+    return fail(HXM_INVALID_ARG, "invalid-argument: cannot write %s", path);
+  }
+  return ok();
+}
+
+hxm_status hxm_tune_cache_load(const char* path, int32_t* loaded) {
+  if (loaded) *loaded = 0;
+  if (!path || !*path) return fail(HXM_INVALID_ARG, "invalid-argument: tune_cache_load path");
+  FILE* f = std::fopen(path, "r");
+  if (!f) return fail(HXM_INVALID_ARG, "invalid-argument: cannot open %s", path);
+  char line[256];
+  unsigned long long fbid = 0;
+  int fcus = -1;
+  const bool header = std::fgets(line, sizeof(line), f) &&
+                      std::strncmp(line, kCacheMagic, std::strlen(kCacheMagic)) == 0 &&
+                      std::fgets(line, sizeof(line), f) &&
+                      std::sscanf(line, "build %llx", &fbid) == 1 &&
+                      std::fgets(line, sizeof(line), f) && std::sscanf(line, "cus %d", &fcus) == 1;
+  if (!header) {
+    std::fclose(f);
+    return fail(HXM_INVALID_ARG, "invalid-argument: %s is not a tuning cache file", path);
+  }
+  uint64_t bid = 0;
+  hxm_status st = build_id(&bid);
+  if (st != HXM_OK) {
+    std::fclose(f);
+    return st;
+  }
+  if (fbid != bid) {
+    std::fclose(f);
+    return fail(HXM_INVALID_ARG,
+                "invalid-argument: %s holds winners of another build (%016llx, this build "
+                "%016llx); they are re-measured, not reused",
+                path, fbid, (unsigned long long)bid);
+  }
+  if ((st = require_device(nullptr)) != HXM_OK) {
+    std::fclose(f);
+    return st;
+  }
+  const int cus = device_cus();
+  if (fcus != cus) {
+    std::fclose(f);
+    return fail(HXM_INVALID_ARG,
+                "invalid-argument: %s was measured on a device with %d CUs (this one: %d)",
+                path, fcus, cus);
+  }
+  int32_t n = 0;
+  while (std::fgets(line, sizeof(line), f)) {
+    int op, reps;
+    long long M, N, K;
+    hxm_gemm_config c;
+    if (std::sscanf(line, "%d %lld %lld %lld %d %d %d %d %d %d %d %d", &op, &M, &N, &K, &c.bm,
+                    &c.bn, &c.bk, &c.waves_m, &c.waves_n, &c.stages, &c.split_k, &reps) != 12)
+      continue;
+    if (M < 0 || N < 0 || K < 0 || !config_compiled(op, c)) continue;
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    g_tuned[TuneKey(op, M, N, K)] = c;
+    g_tuned_reps[TuneKey(op, M, N, K)] = reps;
+    ++n;
+  }
+  std::fclose(f);
+  if (loaded) *loaded = n;
+  return ok();
+}
+
 void hxm_tune_cache_clear(void) {
   std::lock_guard<std::mutex> lk(g_tune_mu);
+  g_tuned_reps.clear();
   g_tuned.clear();
   g_canary_ref.clear();
 }

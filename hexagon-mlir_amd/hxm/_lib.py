@@ -106,6 +106,9 @@ SIGNATURES = {
     "hxm_tune_gemm": (_st, [_i32, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _cfgp,
                             ctypes.c_char_p, _i64, _p]),
     "hxm_tune_cache_clear": (None, []),
+    "hxm_tune_cache_lookup": (_i32, [_i32, _i64, _i64, _i64, _cfgp]),
+    "hxm_tune_cache_save": (_st, [ctypes.c_char_p]),
+    "hxm_tune_cache_load": (_st, [ctypes.c_char_p, ctypes.POINTER(_i32)]),
 }
 
 

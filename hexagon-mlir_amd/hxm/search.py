@@ -365,3 +365,27 @@ def hexagon_bench(kernel_call, quantiles=(0.5, 0.2, 0.8), *, reps: int = 3,
                 return inf
         samples.append(float(t))
     return [_quantile(samples, q) for q in quantiles]
+
+
+# ---- persisted tuning winners (C: hxm_tune_cache_save / _load / _lookup) ----
+
+def tune_cache_lookup(op: int, m: int, n: int, k: int) -> Optional[GemmConfig]:
+    """The cached tuning winner for (op, M, N, K), or None."""
+    cfg = GemmConfig()
+    return cfg if lib.hxm_tune_cache_lookup(int(op), m, n, k, ctypes.byref(cfg)) else None
+
+
+def tune_cache_save(path: str) -> None:
+    """Writes every cached winner to ``path``, keyed to this library build and
+    device (backend/hmx_search.py:416-442 keys results on the build)."""
+    from ._lib import check
+    check(lib.hxm_tune_cache_save(str(path).encode()), "hxm_tune_cache_save")
+
+
+def tune_cache_load(path: str) -> int:
+    """Adds the winners saved in ``path`` to the cache; refuses a file of
+    another build or device.  Returns how many entries were loaded."""
+    from ._lib import check
+    n = ctypes.c_int32(0)
+    check(lib.hxm_tune_cache_load(str(path).encode(), ctypes.byref(n)), "hxm_tune_cache_load")
+    return n.value

@@ -420,6 +420,25 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
 /* Forget every cached tuning winner. */
 void hxm_tune_cache_clear(void);
 
+/* The cached tuning winner for (op, M, N, K): returns 1 and writes *out
+ * (if non-NULL) when there is one, else 0.  op as in hxm_tune_gemm /
+ * hxm_tune_w8a16. */
+int32_t hxm_tune_cache_lookup(int32_t op, int64_t M, int64_t N, int64_t K,
+                              hxm_gemm_config* out);
+
+/* Persisted winners.  The reference keys its search results on the build
+ * and the measurement protocol so that no result crosses a rebuild
+ * (backend/hmx_search.py:416-442, tuning_key_int).  hxm_tune_cache_save
+ * writes every cached winner to `path` (text; replaced atomically), headed by
+ * a hash of this library's binary and the device's CU count, each entry with
+ * the reps it was measured with.  hxm_tune_cache_load adds the winners of
+ * such a file to the cache (*loaded = how many) only when both match this
+ * library and device ("invalid-argument" otherwise: results of another build
+ * or device are re-measured, not reused); entries naming a tile this build
+ * did not compile are skipped. */
+hxm_status hxm_tune_cache_save(const char* path);
+hxm_status hxm_tune_cache_load(const char* path, int32_t* loaded);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,3 +42,32 @@ def test_tune_gemm_picks_a_verified_winner(dev, dtype, M, N, K):
         bits = lambda t: t.view(torch.int16).numpy().view(np.uint16)  # noqa: E731
         ref = orc.f16_bits_to_f32(orc.matmul(bits(A), bits(B), b_nk=True))
         np.testing.assert_allclose(C, ref, rtol=1e-2, atol=1e-3)
+
+
+def test_tune_cache_save_load_round_trip(dev, tmp_path):
+    """A tuned winner survives save -> clear -> load on the same build and
+    device; an entry naming a tile this build did not compile is skipped."""
+    import hxm
+    from hxm import search as S
+    hxm.lib.hxm_tune_cache_clear()
+    M = N = K = 512
+    g = torch.Generator().manual_seed(5)
+    A = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
+    B = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+    out = torch.empty(M, N, dtype=torch.int32, device=dev)
+    best, rep = ops.tune_gemm(A, B, out, reps=3)
+    assert rep["champion"] is not None
+    win = S.tune_cache_lookup(hxm.I8, M, N, K)
+    assert win is not None and win.as_tuple() == best.as_tuple()
+    p = tmp_path / "tune.txt"
+    S.tune_cache_save(str(p))
+    with open(p, "a") as f:
+        f.write("4 1024 1024 1024 96 96 128 2 2 2 1 3\n")   # no such compiled tile
+    hxm.lib.hxm_tune_cache_clear()
+    assert S.tune_cache_lookup(hxm.I8, M, N, K) is None
+    assert S.tune_cache_load(str(p)) == 1
+    assert S.tune_cache_lookup(hxm.I8, M, N, K).as_tuple() == best.as_tuple()
+    assert S.tune_cache_lookup(hxm.I8, 1024, 1024, 1024) is None
+    C = ops.gemm_i8(A, B, b_layout="nk").cpu().numpy()     # runs the reloaded winner
+    assert np.array_equal(C, orc.gemm_i8(A.cpu().numpy(), B.cpu().numpy(), b_nk=True))
+    hxm.lib.hxm_tune_cache_clear()

@@ -212,3 +212,31 @@ def test_gpu_lattice_admits_exactly_the_compiled_configs(dtype):
     assert S.gpu_tile_verdict((256, 256, 128 // eb, 2, 2, 4, 1), dtype) == "lds-budget"
     assert S.gpu_tile_verdict((64, 64, 128, 4, 4, 2, 1), dtype) == "tile-alignment"
     assert S.gpu_tile_verdict((512, 32, 32, 1, 1, 2, 1), dtype) == "no-kernel"
+
+
+# ---- persisted tuning winners: the file contract (the device-side round trip is in
+# ---- test_gpu_search.py) ----------------------------------------------------------
+
+def test_tune_cache_file_contract(tmp_path):
+    """The file names this library build; a file of another build, a file that
+    is not a cache and a missing file are refused -- after hmx_search.py:416-442,
+    a result never crosses a rebuild."""
+    hxm.lib.hxm_tune_cache_clear()
+    assert S.tune_cache_lookup(hxm.I8, 64, 64, 64) is None
+    p = tmp_path / "tune.txt"
+    S.tune_cache_save(str(p))
+    lines = p.read_text().splitlines()
+    assert lines[0] == "hxm-tune-cache 1" and lines[1].startswith("build ")
+    assert lines[2].startswith("cus ") and len(lines) == 3     # an empty cache
+    other = tmp_path / "other.txt"
+    bid = int(lines[1].split()[1], 16)
+    other.write_text("\n".join([lines[0], "build %016x" % (bid ^ 1), lines[2],
+                                "4 64 64 64 64 64 128 2 2 2 1 5"]) + "\n")
+    with pytest.raises(hxm.HxmError, match="another build"):
+        S.tune_cache_load(str(other))
+    bad = tmp_path / "bad.txt"
+    bad.write_text("not a cache\n")
+    with pytest.raises(hxm.HxmError, match="not a tuning cache"):
+        S.tune_cache_load(str(bad))
+    with pytest.raises(hxm.HxmError, match="cannot open"):
+        S.tune_cache_load(str(tmp_path / "missing.txt"))

@@ -9,10 +9,13 @@ launch on inputs already resident in HBM.  value = 2*M*N*K / time in
 tera-ops/s (int8 ops are counted like flops in the roofline's TFLOP/s slot).
 
 Also reported under "extra" (not the headline): the int32-output int8 GEMM,
-the fp16 256^3 matmul (launch-bound), W8A16 GEMV M in {1,4,16} and softmax /
+the fp16 256^3 matmul (launch-bound), a ragged int8 GEMM (M=N=K=4000: tail
+tiles, a partial last K stage, C stored into a wider buffer), W8A16 GEMV M in
+{1,4,16} and softmax /
 RMSNorm rows on f16 [8192 x 4096] (HBM-bound: timed while rotating buffer
 sets larger than the 256 MB Infinity Cache), the SwiGLU FFN block (tokens
-2048, hidden 4096, intermediate 11008; tiles autotuned per GEMM), a plain
+2048, hidden 4096, intermediate 11008; tiles autotuned per GEMM; also with the
+residual x + FFN(x) added in the down GEMM's epilogue), a plain
 256 MiB device copy (the practical HBM copy rate next to the nominal peak),
 and for context the vendor library (hipBLASLt via torch._int_mm /
 torch.matmul) on the 4096^3 shapes next to this library's f16 4096^3 matmul.
@@ -26,7 +29,7 @@ load (the headline kernel goes from ~66 to ~56 us per launch over its first
 region sees the steady-state clock.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-       python bench.py --only {int8,int8_i32,f16,gemv,rows,ffn,copy,vendor}  (one workload,
+       python bench.py --only {int8,int8_i32,f16,ragged,gemv,rows,ffn,copy,vendor}  (one workload,
        for rocprofv3 runs; prints that workload's record)
 """
 from __future__ import annotations
@@ -229,23 +232,60 @@ def run_ffn(c):
         hxm.check(L.hxm_gemm_w8a16(ph, I, pwd, I, psd, py, H, T, H, I, None, st),
                   "hxm_gemm_w8a16")
 
+    yr = torch.empty_like(y)
+
+    def down_residual(_):  # y = x + down(h): the residual added in the down GEMM's epilogue
+        hxm.check(L.hxm_gemm_w8a16_residual(ph, I, pwd, I, psd, px, H, yr.data_ptr(), H, T, H, I,
+                                            None, st), "hxm_gemm_w8a16_residual")
+
     def block(i):
         norm(i), gateup(i), down(i)
+
+    def block_residual(i):
+        norm(i), gateup(i), down_residual(i)
     steps, warm = 50, 5
     t_blk, _ = c.time_ms(block, steps, warm)
     t_norm, _ = c.time_ms(norm, steps, warm)
     t_gu, _ = c.time_ms(gateup, steps, warm)
     t_d, _ = c.time_ms(down, steps, warm)
+    t_dr, _ = c.time_ms(down_residual, steps, warm)
+    t_blkr, _ = c.time_ms(block_residual, steps, warm)
     f_gu, f_d = 2.0 * T * H * (2 * I), 2.0 * T * I * H
     flops = f_gu + f_d
     tf = flops / (t_blk * 1e-3) / 1e12
     return {"swiglu_ffn_2048x4096x11008": {
         "us": t_blk * 1e3, "TFLOPS": tf, "mfma_frac": tf / PEAK_F16_TFLOPS,
         "gemm_flops": flops,
-        "stages_us": {"rmsnorm": t_norm * 1e3, "gate_up_swiglu": t_gu * 1e3, "down": t_d * 1e3},
+        "stages_us": {"rmsnorm": t_norm * 1e3, "gate_up_swiglu": t_gu * 1e3, "down": t_d * 1e3,
+                      "down_with_residual": t_dr * 1e3},
+        "block_with_residual_us": t_blkr * 1e3,
         "stage_TFLOPS": {"gate_up_swiglu": f_gu / (t_gu * 1e-3) / 1e12,
                          "down": f_d / (t_d * 1e-3) / 1e12},
         "tuned": {"gate_up_swiglu": list(cfg_gu.as_tuple()), "down": list(cfg_d.as_tuple())}}}
+
+
+def run_ragged(c):
+    """Tail tiles, a partial last K stage and an N-split store: int8 GEMM
+    M=N=4000, K=4000 (K bytes not a multiple of the 128-byte stage) with
+    dequant, C written into columns [0, 4000) of a [4000, 4096] buffer
+    (ldc = 4096)."""
+    torch, hxm, L = c.torch, c.hxm, c.L
+    M = N = K = 4000
+    A = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=c.dev)
+    Bp = c.ops.prepack_weight(torch.randint(-127, 128, (K, N), dtype=torch.int8, device=c.dev))
+    rs = torch.rand(M, device=c.dev) * 0.019 + 0.001
+    cs = torch.rand(N, device=c.dev) * 0.019 + 0.001
+    C = torch.empty(M, 4096, dtype=torch.float16, device=c.dev)
+    a, b, r, s, o, st = A.data_ptr(), Bp.data_ptr(), rs.data_ptr(), cs.data_ptr(), C.data_ptr(), c.stream
+
+    def step(_):
+        hxm.check(L.hxm_gemm_i8_dequant(a, K, b, K, hxm.B_NK, r, s, o, 4096, M, N, K, None, st),
+                  "hxm_gemm_i8_dequant")
+    ms, _ = c.time_ms(step, 200, 200)
+    ops_per = 2.0 * M * N * K
+    return {"int8_gemm_dequant_ragged_4000_ldc4096": {
+        "us": ms * 1e3, "TOPS": ops_per / (ms * 1e-3) / 1e12,
+        "mfma_frac": ops_per / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS}}
 
 
 def run_vendor(c):
@@ -381,8 +421,8 @@ def main() -> int:
                     help="approximate CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=["int8", "int8_i32", "f16", "gemv", "rows", "ffn", "copy",
-                                       "vendor"])
+    ap.add_argument("--only", choices=["int8", "int8_i32", "f16", "ragged", "gemv", "rows", "ffn",
+                                       "copy", "vendor"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build is the single-GPU kernel set of the hot "
@@ -395,8 +435,8 @@ def main() -> int:
         if args.only in ("int8", "int8_i32"):
             rec = {args.only: run_int8(c, *int8_operands(c), out_i32=args.only == "int8_i32")}
         else:
-            rec = {"f16": run_f16, "gemv": run_gemv, "rows": run_rows, "ffn": run_ffn,
-                   "copy": run_copy, "vendor": run_vendor}[
+            rec = {"f16": run_f16, "ragged": run_ragged, "gemv": run_gemv, "rows": run_rows,
+                   "ffn": run_ffn, "copy": run_copy, "vendor": run_vendor}[
                 args.only](c)
         print(json.dumps(rec), flush=True)
         return 0
@@ -409,7 +449,7 @@ def main() -> int:
     extra = {}
     if not args.no_extra:
         extra["int8_gemm_i32_out_4096"] = run_int8(c, A, Bp, rs, cs, out_i32=True)
-        for fn in (run_f16, run_gemv, run_rows, run_ffn, run_copy, run_vendor):
+        for fn in (run_f16, run_ragged, run_gemv, run_rows, run_ffn, run_copy, run_vendor):
             extra.update(fn(c))
         for k, v in extra.items():
             log(k, json.dumps(v))

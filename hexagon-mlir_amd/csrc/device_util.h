@@ -72,25 +72,28 @@ __device__ __forceinline__ float wave_reduce(float v, Op op) {
   return op(a, b);
 }
 
-// 8 int8 (two dwords) -> 8 exact f16.  (b ^ 0x80) | 0x6400 is the f16
-// 1024 + b + 128; subtracting 1152 leaves b exactly.
+// Two int8 -> two exact f16 (one packed word).  flipped is a dword of four
+// int8 with every sign bit inverted (x ^ 0x80808080); H selects bytes 0-1
+// (H = 0) or 2-3 (H = 1).  (b ^ 0x80) | 0x6400 is the f16 1024 + b + 128;
+// subtracting 1152 leaves b exactly.
+template <int H>
+__device__ __forceinline__ uint32_t i8x2_flipped_to_f16(uint32_t flipped) {
+  const uint32_t w =
+      __builtin_amdgcn_perm(0x64646464u, flipped, H == 0 ? 0x05010400u : 0x05030402u);
+  const v2f16 bias = {static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2f16, w) - bias);
+}
+
+// 8 int8 (two dwords) -> 8 exact f16.
 __device__ __forceinline__ v8f16 i8x8_to_f16(uint32_t lo, uint32_t hi) {
   lo ^= 0x80808080u;
   hi ^= 0x80808080u;
-  const uint32_t k64 = 0x64646464u;
-  uint32_t w0 = __builtin_amdgcn_perm(k64, lo, 0x05010400u);
-  uint32_t w1 = __builtin_amdgcn_perm(k64, lo, 0x05030402u);
-  uint32_t w2 = __builtin_amdgcn_perm(k64, hi, 0x05010400u);
-  uint32_t w3 = __builtin_amdgcn_perm(k64, hi, 0x05030402u);
-  const v2f16 bias = {static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
-  v2f16 h0 = __builtin_bit_cast(v2f16, w0) - bias;
-  v2f16 h1 = __builtin_bit_cast(v2f16, w1) - bias;
-  v2f16 h2 = __builtin_bit_cast(v2f16, w2) - bias;
-  v2f16 h3 = __builtin_bit_cast(v2f16, w3) - bias;
-  v8f16 r;
-  r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
-  r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
-  return r;
+  v4i32 r;
+  r[0] = static_cast<int>(i8x2_flipped_to_f16<0>(lo));
+  r[1] = static_cast<int>(i8x2_flipped_to_f16<1>(lo));
+  r[2] = static_cast<int>(i8x2_flipped_to_f16<0>(hi));
+  r[3] = static_cast<int>(i8x2_flipped_to_f16<1>(hi));
+  return __builtin_bit_cast(v8f16, r);
 }
 
 }  // namespace hxm

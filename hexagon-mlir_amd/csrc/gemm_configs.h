@@ -15,10 +15,13 @@
 
 // W8A16 GEMM (f16 activations x int8 [N, K] weights, BKB = A bytes per
 // stage; B rows hold BKB/2 int8).  The SwiGLU variant exists for the entries
-// whose wave tile is 128 columns wide (BN / WAVES_N == 128).
+// whose wave tile is 128 columns wide (BN / WAVES_N == 128).  The default
+// tile is the first entry that gives every CU a workgroup, so among equal
+// tile counts the entry with fewer B columns per wave (fewer int8 -> f16
+// conversions per MFMA) comes first.
 #ifndef HXM_W8_CONFIG_LIST
 #define HXM_W8_CONFIG_LIST(X)                                                   \
   X(256, 256, 128, 3, 2, 2), X(256, 256, 128, 2, 2, 2),                          \
-      X(128, 256, 128, 4, 2, 2), X(256, 128, 128, 3, 2, 2),                      \
+      X(256, 128, 128, 3, 2, 2), X(128, 256, 128, 4, 2, 2),                      \
       X(128, 128, 128, 3, 2, 2)
 #endif

@@ -352,15 +352,22 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   // Read R of a k-step: A block 0, the FN B blocks, then A blocks 1..FM-1 --
   // the order the MFMA slots (i, j) = (s / FN, s % FN) first need them.
   // With an int8 B the read brings the lane's 8 bytes (K range
-  // [16ks + 8hi, +8) of its row) into braw, and cvt_b turns them into the f16
-  // fragment one MFMA slot before its first use.
+  // [16ks + 8hi, +8) of its row) into braw, and the slots run column-major,
+  // (i, j) = (s % FM, s / FM), so B block j is first needed at slot j*FM:
+  // its conversion to f16 (cvt_word, four words) is spread over the FM slots
+  // before that, block 0's over the end of the previous k-step.  A wave is
+  // alone on its SIMD, so a conversion issued whole between two MFMAs that
+  // the second one needs (ten dependent VALU operations, longer than one
+  // MFMA) would leave the matrix core idle.  The B reads come first, then
+  // the A blocks.
   v4i32 af[2][FM], bf[2][FN];
   uint2 braw[2][BQ ? FN : 1];
+  uint32_t bflip[2][BQ ? FN : 1][2];  // braw with the sign bits inverted
   const int r32 = lane & 31, hi = lane >> 5;
   auto read = [&](auto R, int dstb, const uint8_t* stage, int ks) {
     constexpr int r = decltype(R)::value;
-    constexpr bool is_b = r >= 1 && r <= FN;
-    constexpr int idx = r == 0 ? 0 : is_b ? r - 1 : r - FN;
+    constexpr bool is_b = BQ ? r < FN : r >= 1 && r <= FN;
+    constexpr int idx = BQ ? (is_b ? r : r - FN) : r == 0 ? 0 : is_b ? r - 1 : r - FN;
     if constexpr (is_b && BQ) {
       const int row = idx * 32 + r32;
       braw[dstb][idx] = *reinterpret_cast<const uint2*>(
@@ -371,8 +378,33 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
       af[dstb][idx] = lds_frag<BKB>(stage + (wm * TM) * BKB, idx * 32 + r32, ks * 2 + hi);
     }
   };
-  auto cvt_b = [&](int b, int j) {
-    if constexpr (BQ) bf[b][j] = __builtin_bit_cast(v4i32, i8x8_to_f16(braw[b][j].x, braw[b][j].y));
+  // Word P of B block j's f16 fragment (elements 2P, 2P+1) from braw[b][j].
+  auto cvt_word = [&](auto P, int b, int j) {
+    constexpr int p = decltype(P)::value;
+    if constexpr (BQ) {
+      if constexpr (p % 2 == 0)
+        bflip[b][j][p / 2] = (p == 0 ? braw[b][j].x : braw[b][j].y) ^ 0x80808080u;
+      bf[b][j][p] = static_cast<int>(i8x2_flipped_to_f16<p % 2>(bflip[b][j][p / 2]));
+    }
+  };
+  // The conversion words issued in slot sl of k-step ks (multiplying buffer
+  // cb): words of blocks 1..FN-1 of this k-step in the FM slots before their
+  // first use, words of block 0 of the next k-step in the last FM slots (in
+  // the last k-step of a stage, whose reads of the next stage start at the
+  // barrier, in its last two slots).
+  auto cvt_slot = [&](auto KSI, auto SI, int cb) {
+    constexpr int ks = decltype(KSI)::value, sl = decltype(SI)::value;
+    if constexpr (BQ) {
+      static_for<0, 4>([&](auto P) {
+        constexpr int p = decltype(P)::value;
+        static_for<1, FN>([&](auto J) {
+          constexpr int j = decltype(J)::value;
+          if constexpr ((j - 1) * FM + (p * FM) / 4 == sl) cvt_word(P, cb, j);
+        });
+        constexpr int s0 = ks == KS - 1 ? NF - 2 + p / 2 : (FN - 1) * FM + (p * FM) / 4;
+        if constexpr (s0 == sl) cvt_word(P, cb ^ 1, 0);
+      });
+    }
   };
 
   // Every stage slot issues its DMAs, also past the end of K: a stage at or
@@ -436,12 +468,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
             if constexpr (HALF + (r * (NF - HALF)) / NR == sl) read(R, cb ^ 1, nxt, 0);
           }
         });
-        constexpr int i = sl / FN, j = sl % FN;
+        constexpr int i = BQ ? sl % FM : sl / FN, j = BQ ? sl / FM : sl % FN;
         acc[i][j] = Mfma<T>::run(bf[cb][j], af[cb][i], acc[i][j]);
-        // int8 B: convert fragment sl+1 of this k-step under this MFMA, and
-        // fragment 0 of the next k-step under the last one.
-        if constexpr (BQ && sl + 1 < FN) cvt_b(cb, sl + 1);
-        if constexpr (BQ && sl == NF - 1) cvt_b(cb ^ 1, 0);
+        cvt_slot(KSI, SI, cb);
         __builtin_amdgcn_sched_barrier(0);
       });
     });
@@ -459,7 +488,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     });
     wait_and_barrier<(STAGES - 2) * LPW + NEG>();
     static_for<0, NR>([&](auto R) { read(R, 0, buf(0), 0); });
-    cvt_b(0, 0);
+    static_for<0, 4>([&](auto P) { cvt_word(P, 0, 0); });
 
     // Main loop, unrolled by STAGES so every buffer choice is static.  It is
     // compiled twice: without the per-lane K test (K_bytes a multiple of the

@@ -527,7 +527,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   float* stg = reinterpret_cast<float*>(buf(wave % STAGES)) + (wave / STAGES) * kStageWords;
 
   // A tile wholly inside C with 16-byte aligned rows takes a branch-free
-  // path (one wave per SIMD: nothing hides a per-run LDS round trip).
+  // path (one wave per SIMD: nothing hides a per-run LDS round trip).  A tile
+  // that crosses M or N takes the same path with a predicate on each run's
+  // store (and residual load) when N is a multiple of the run length, so
+  // that every run lies wholly inside or wholly outside C.
   const bool full8 = g.vec8_store && m0 + BM <= g.M && n0 + BN <= g.N;
 
   // 1. registers -> LDS: block row i, lane row r32, 4 consecutive columns
@@ -554,9 +557,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
       }
   };
 
-  // Full tiles, 8-element f16 output rows: a branch-free pipeline over
-  // half-blocks (32 rows x TN/2 columns, block row i = n / 2, columns half
-  // h = n % 2) through two LDS staging buffers per wave.  Half-block n+1 is
+  // 8-element f16 output rows (full tiles, or edge tiles with N % 8 == 0):
+  // a branch-free pipeline over half-blocks (32 rows x TN/2 columns, block
+  // row i = n / 2, columns half h = n % 2) through two LDS staging buffers
+  // per wave.  Half-block n+1 is
   // written to LDS while the VALU converts half-block n, and all LDS reads of
   // a half-block are issued before its arithmetic.  The buffer written for
   // n+1 was last read for n-1, earlier in program order; a wave's LDS
@@ -567,245 +571,284 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   // issued two half-blocks ahead (a ring of three register sets), so they
   // land under the staging and arithmetic of the half-blocks in between.
   if constexpr ((EPI == kEpiDequant || EPI == kEpiW8 || EPI == kEpiW8Res) && FN % 2 == 0) {
-    if (full8 && (EPI != kEpiW8Res || g.res_vec8)) {
-      constexpr int TNH = TN / 2;
-      constexpr int kPadH = TNH + 4;             // staging row stride (words)
-      constexpr int kWordsH = 32 * kPadH;        // one half-block buffer
-      constexpr int kRprH = TNH / 8;             // 8-element runs per staged row
-      constexpr int kRowsItH = 64 / kRprH;       // rows one pass of the wave covers
-      constexpr int kItH = 32 / kRowsItH;        // passes per half-block
-      constexpr int NH = FM * 2;                 // half-blocks per wave
-      static_assert(64 % kRprH == 0 && kItH >= 1, "8-element runs must tile the wave");
-      static_assert(kWavesPerBuf * 2 * kWordsH * 4 <= SB, "epilogue staging must fit a stage");
-      float* hb0 = reinterpret_cast<float*>(buf(wave % STAGES)) + (wave / STAGES) * 2 * kWordsH;
-      float* hb1 = hb0 + kWordsH;
-      const int col8 = (lane % kRprH) * 8, rsub8 = lane / kRprH;
-      v4f32 csh[2][2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const float* csp = ssc + QR * 64 + wn * TN + h * TNH + col8;
-        csh[h][0] = *reinterpret_cast<const v4f32*>(csp);
-        csh[h][1] = *reinterpret_cast<const v4f32*>(csp + 4);
-      }
-      // Registers -> LDS: block columns [h*FN/2, (h+1)*FN/2) of block row i.
-      auto stage_half = [&](int n, float* dst) {
-        const int i = n / 2, h = n % 2;
-#pragma unroll
-        for (int jj = 0; jj < FN / 2; ++jj)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            v4f32 w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              if constexpr (EPI != kEpiDequant) {
-                w[e] = acc[i][h * (FN / 2) + jj][q * 4 + e];
-              } else {
-                // Copy the element out first (see stage_block).
-                const int32_t a = acc[i][h * (FN / 2) + jj][q * 4 + e];
-                w[e] = __builtin_bit_cast(float, a);
+    const bool edge8 = !full8 && g.vec8_store && g.N % 8 == 0;
+    if ((full8 || edge8) && (EPI != kEpiW8Res || g.res_vec8)) {
+      auto pipeline = [&](auto EDGE) {
+        constexpr bool edge = decltype(EDGE)::value;
+        constexpr int TNH = TN / 2;
+        constexpr int kPadH = TNH + 4;             // staging row stride (words)
+        constexpr int kWordsH = 32 * kPadH;        // one half-block buffer
+        constexpr int kRprH = TNH / 8;             // 8-element runs per staged row
+        constexpr int kRowsItH = 64 / kRprH;       // rows one pass of the wave covers
+        constexpr int kItH = 32 / kRowsItH;        // passes per half-block
+        constexpr int NH = FM * 2;                 // half-blocks per wave
+        static_assert(64 % kRprH == 0 && kItH >= 1, "8-element runs must tile the wave");
+        static_assert(kWavesPerBuf * 2 * kWordsH * 4 <= SB, "epilogue staging must fit a stage");
+        float* hb0 = reinterpret_cast<float*>(buf(wave % STAGES)) + (wave / STAGES) * 2 * kWordsH;
+        float* hb1 = hb0 + kWordsH;
+        const int col8 = (lane % kRprH) * 8, rsub8 = lane / kRprH;
+        v4f32 csh[2][2];
+  #pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float* csp = ssc + QR * 64 + wn * TN + h * TNH + col8;
+          csh[h][0] = *reinterpret_cast<const v4f32*>(csp);
+          csh[h][1] = *reinterpret_cast<const v4f32*>(csp + 4);
+        }
+        // Registers -> LDS: block columns [h*FN/2, (h+1)*FN/2) of block row i.
+        auto stage_half = [&](int n, float* dst) {
+          const int i = n / 2, h = n % 2;
+  #pragma unroll
+          for (int jj = 0; jj < FN / 2; ++jj)
+  #pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              v4f32 w;
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                if constexpr (EPI != kEpiDequant) {
+                  w[e] = acc[i][h * (FN / 2) + jj][q * 4 + e];
+                } else {
+                  // Copy the element out first (see stage_block).
+                  const int32_t a = acc[i][h * (FN / 2) + jj][q * 4 + e];
+                  w[e] = __builtin_bit_cast(float, a);
+                }
               }
+              *reinterpret_cast<v4f32*>(dst + r32 * kPadH + jj * 32 + q * 8 + hi * 4) = w;
             }
-            *reinterpret_cast<v4f32*>(dst + r32 * kPadH + jj * 32 + q * 8 + hi * 4) = w;
+        };
+        v4f32 w0[2][kItH], w1[2][kItH];
+        float rsv[2][kItH];
+        auto read_half = [&](int n, const float* src, int set) {
+  #pragma unroll
+          for (int it = 0; it < kItH; ++it) {
+            const int row = it * kRowsItH + rsub8;
+            w0[set][it] = *reinterpret_cast<const v4f32*>(src + row * kPadH + col8);
+            w1[set][it] = *reinterpret_cast<const v4f32*>(src + row * kPadH + col8 + 4);
+            rsv[set][it] = EPI == kEpiDequant ? ssc[wm * TM + (n / 2) * 32 + row] : 1.0f;
           }
-      };
-      v4f32 w0[2][kItH], w1[2][kItH];
-      float rsv[2][kItH];
-      auto read_half = [&](int n, const float* src, int set) {
-#pragma unroll
-        for (int it = 0; it < kItH; ++it) {
-          const int row = it * kRowsItH + rsub8;
-          w0[set][it] = *reinterpret_cast<const v4f32*>(src + row * kPadH + col8);
-          w1[set][it] = *reinterpret_cast<const v4f32*>(src + row * kPadH + col8 + 4);
-          rsv[set][it] = EPI == kEpiDequant ? ssc[wm * TM + (n / 2) * 32 + row] : 1.0f;
-        }
-      };
-      const int64_t step = static_cast<int64_t>(kRowsItH) * g.ldc;
-      constexpr int kRes = EPI == kEpiW8Res ? kItH : 1;
-      v8f16 rres[3][kRes];
-      const _Float16* rbase =
-          EPI == kEpiW8Res ? g.residual + static_cast<int64_t>(mw + rsub8) * g.ldr + nw + col8
-                           : nullptr;
-      auto load_res = [&](int n) {
-        if constexpr (EPI == kEpiW8Res) {
-#pragma unroll
-          for (int it = 0; it < kItH; ++it)
-            rres[n % 3][it] = *reinterpret_cast<const v8f16*>(
-                rbase + static_cast<int64_t>((n / 2) * 32 + it * kRowsItH) * g.ldr +
-                (n % 2) * TNH);
-        }
-      };
-      load_res(0);
-      if (NH > 1) load_res(1);
-      stage_half(0, hb0);
-      read_half(0, hb0, 0);
-#pragma unroll
-      for (int n = 0; n < NH; ++n) {
-        const int cur = n & 1;
-        if (n + 2 < NH) load_res(n + 2);
-        if (n + 1 < NH) stage_half(n + 1, cur ? hb0 : hb1);
-        const int i = n / 2, h = n % 2;
-        _Float16* c = static_cast<_Float16*>(g.C) +
-                      static_cast<int64_t>(mw + i * 32 + rsub8) * g.ldc + nw + h * TNH + col8;
-#pragma unroll
-        for (int it = 0; it < kItH; ++it) {
-          v8f16 hv;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float we = e < 4 ? w0[cur][it][e] : w1[cur][it][e - 4];
-            const float ce = csh[h][e / 4][e % 4];
-            // Same spellings as the general path below.
-            float p;
-            if constexpr (EPI == kEpiDequant)
-              p = (static_cast<float>(__builtin_bit_cast(int32_t, we)) * rsv[cur][it]) * ce;
-            else
-              p = we * ce;
-            asm volatile("" : "+v"(p));
-            if constexpr (EPI == kEpiW8Res) {
-              // fp32 sum, then one rounding to f16: the pin keeps the
-              // backend from fusing the add into a mixed-precision fma.
-              p = p + static_cast<float>(rres[n % 3][it][e]);
+        };
+        const int64_t step = static_cast<int64_t>(kRowsItH) * g.ldc;
+        constexpr int kRes = EPI == kEpiW8Res ? kItH : 1;
+        v8f16 rres[3][kRes];
+        const _Float16* rbase =
+            EPI == kEpiW8Res ? g.residual + static_cast<int64_t>(mw + rsub8) * g.ldr + nw + col8
+                             : nullptr;
+        auto load_res = [&](int n) {
+          if constexpr (EPI == kEpiW8Res) {
+  #pragma unroll
+            for (int it = 0; it < kItH; ++it) {
+              const int row = (n / 2) * 32 + it * kRowsItH, col = (n % 2) * TNH;
+              if (!edge || (mw + row + rsub8 < g.M && nw + col + col8 < g.N))
+                rres[n % 3][it] = *reinterpret_cast<const v8f16*>(
+                    rbase + static_cast<int64_t>(row) * g.ldr + col);
+              else
+                rres[n % 3][it] = v8f16{};
+            }
+          }
+        };
+        load_res(0);
+        if (NH > 1) load_res(1);
+        stage_half(0, hb0);
+        read_half(0, hb0, 0);
+  #pragma unroll
+        for (int n = 0; n < NH; ++n) {
+          const int cur = n & 1;
+          if (n + 2 < NH) load_res(n + 2);
+          if (n + 1 < NH) stage_half(n + 1, cur ? hb0 : hb1);
+          const int i = n / 2, h = n % 2;
+          _Float16* c = static_cast<_Float16*>(g.C) +
+                        static_cast<int64_t>(mw + i * 32 + rsub8) * g.ldc + nw + h * TNH + col8;
+  #pragma unroll
+          for (int it = 0; it < kItH; ++it) {
+            v8f16 hv;
+  #pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float we = e < 4 ? w0[cur][it][e] : w1[cur][it][e - 4];
+              const float ce = csh[h][e / 4][e % 4];
+              // Same spellings as the general path below.
+              float p;
+              if constexpr (EPI == kEpiDequant)
+                p = (static_cast<float>(__builtin_bit_cast(int32_t, we)) * rsv[cur][it]) * ce;
+              else
+                p = we * ce;
               asm volatile("" : "+v"(p));
+              if constexpr (EPI == kEpiW8Res) {
+                // fp32 sum, then one rounding to f16: the pin keeps the
+                // backend from fusing the add into a mixed-precision fma.
+                p = p + static_cast<float>(rres[n % 3][it][e]);
+                asm volatile("" : "+v"(p));
+              }
+              hv[e] = static_cast<_Float16>(p);
             }
-            hv[e] = static_cast<_Float16>(p);
+            if (!edge || (mw + i * 32 + it * kRowsItH + rsub8 < g.M && nw + h * TNH + col8 < g.N))
+              __builtin_nontemporal_store(hv, reinterpret_cast<v8f16*>(c + it * step));
           }
-          __builtin_nontemporal_store(hv, reinterpret_cast<v8f16*>(c + it * step));
+          if (n + 1 < NH) read_half(n + 1, cur ? hb0 : hb1, cur ^ 1);
         }
-        if (n + 1 < NH) read_half(n + 1, cur ? hb0 : hb1, cur ^ 1);
-      }
+      };
+      if (full8)
+        pipeline(std::false_type{});
+      else
+        pipeline(std::true_type{});
       return;
     }
   }
-  // SwiGLU on full tiles: the same two-buffer half-block pipeline.  The
-  // wave's 128 image columns are 64 gate channels then the same 64 up
-  // channels, so half-block h (h = 0, 1) stages gate block h next to up
-  // block h + 2: each staged row holds 32 gate and the matching 32 up values,
-  // output channels nw/2 + 32h + 0..31.
+  // SwiGLU (full tiles, or edge tiles with n_out % 8 == 0): the same
+  // two-buffer half-block pipeline.  The wave's 128 image columns are 64
+  // gate channels then the same 64 up channels, so half-block h (h = 0, 1)
+  // stages gate block h next to up block h + 2: each staged row holds 32
+  // gate and the matching 32 up values, output channels nw/2 + 32h + 0..31.
   if constexpr (EPI == kEpiSwiglu) {
-    if (g.vec8_store && m0 + BM <= g.M && n0 + BN <= g.N && (n0 + BN) / 2 <= g.n_out) {
-      constexpr int kPadS = 64 + 4;              // staging row stride (words)
-      constexpr int kWordsS = 32 * kPadS;        // one half-block buffer
-      constexpr int kRprS = 32 / 8;              // 8-channel runs per staged row
-      constexpr int kRowsItS = 64 / kRprS;       // rows one pass covers
-      constexpr int kItS = 32 / kRowsItS;        // passes per half-block
-      constexpr int NH = FM * 2;
-      static_assert(FN == 4, "SwiGLU wave tile is 128 columns");
-      static_assert(kWavesPerBuf * 2 * kWordsS * 4 <= SB, "epilogue staging must fit a stage");
-      float* hb0 = reinterpret_cast<float*>(buf(wave % STAGES)) + (wave / STAGES) * 2 * kWordsS;
-      float* hb1 = hb0 + kWordsS;
-      const int ch = (lane % kRprS) * 8, rsub = lane / kRprS;
-      v4f32 sgv[2][2], suv[2][2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const float* sp = ssc + QR * 64 + wn * TN + h * 32 + ch;
-        sgv[h][0] = *reinterpret_cast<const v4f32*>(sp);
-        sgv[h][1] = *reinterpret_cast<const v4f32*>(sp + 4);
-        suv[h][0] = *reinterpret_cast<const v4f32*>(sp + 64);
-        suv[h][1] = *reinterpret_cast<const v4f32*>(sp + 68);
-      }
-      auto stage_sw = [&](int n, float* dst) {
-        const int i = n / 2, h = n % 2;
-#pragma unroll
-        for (int part = 0; part < 2; ++part)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            v4f32 w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) w[e] = acc[i][h + 2 * part][q * 4 + e];
-            *reinterpret_cast<v4f32*>(dst + r32 * kPadS + part * 32 + q * 8 + hi * 4) = w;
+    const bool full_sw = g.vec8_store && m0 + BM <= g.M && n0 + BN <= g.N &&
+                         (n0 + BN) / 2 <= g.n_out;
+    if (full_sw || (g.vec8_store && g.n_out % 8 == 0)) {
+      auto pipeline = [&](auto EDGE) {
+        constexpr bool edge = decltype(EDGE)::value;
+        constexpr int kPadS = 64 + 4;              // staging row stride (words)
+        constexpr int kWordsS = 32 * kPadS;        // one half-block buffer
+        constexpr int kRprS = 32 / 8;              // 8-channel runs per staged row
+        constexpr int kRowsItS = 64 / kRprS;       // rows one pass covers
+        constexpr int kItS = 32 / kRowsItS;        // passes per half-block
+        constexpr int NH = FM * 2;
+        static_assert(FN == 4, "SwiGLU wave tile is 128 columns");
+        static_assert(kWavesPerBuf * 2 * kWordsS * 4 <= SB, "epilogue staging must fit a stage");
+        float* hb0 = reinterpret_cast<float*>(buf(wave % STAGES)) + (wave / STAGES) * 2 * kWordsS;
+        float* hb1 = hb0 + kWordsS;
+        const int ch = (lane % kRprS) * 8, rsub = lane / kRprS;
+        v4f32 sgv[2][2], suv[2][2];
+  #pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float* sp = ssc + QR * 64 + wn * TN + h * 32 + ch;
+          sgv[h][0] = *reinterpret_cast<const v4f32*>(sp);
+          sgv[h][1] = *reinterpret_cast<const v4f32*>(sp + 4);
+          suv[h][0] = *reinterpret_cast<const v4f32*>(sp + 64);
+          suv[h][1] = *reinterpret_cast<const v4f32*>(sp + 68);
+        }
+        auto stage_sw = [&](int n, float* dst) {
+          const int i = n / 2, h = n % 2;
+  #pragma unroll
+          for (int part = 0; part < 2; ++part)
+  #pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              v4f32 w;
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) w[e] = acc[i][h + 2 * part][q * 4 + e];
+              *reinterpret_cast<v4f32*>(dst + r32 * kPadS + part * 32 + q * 8 + hi * 4) = w;
+            }
+        };
+        v4f32 gv[2][kItS][2], uv[2][kItS][2];
+        auto read_sw = [&](const float* src, int set) {
+  #pragma unroll
+          for (int it = 0; it < kItS; ++it) {
+            const float* sp = src + (it * kRowsItS + rsub) * kPadS + ch;
+            gv[set][it][0] = *reinterpret_cast<const v4f32*>(sp);
+            gv[set][it][1] = *reinterpret_cast<const v4f32*>(sp + 4);
+            uv[set][it][0] = *reinterpret_cast<const v4f32*>(sp + 32);
+            uv[set][it][1] = *reinterpret_cast<const v4f32*>(sp + 36);
           }
-      };
-      v4f32 gv[2][kItS][2], uv[2][kItS][2];
-      auto read_sw = [&](const float* src, int set) {
-#pragma unroll
-        for (int it = 0; it < kItS; ++it) {
-          const float* sp = src + (it * kRowsItS + rsub) * kPadS + ch;
-          gv[set][it][0] = *reinterpret_cast<const v4f32*>(sp);
-          gv[set][it][1] = *reinterpret_cast<const v4f32*>(sp + 4);
-          uv[set][it][0] = *reinterpret_cast<const v4f32*>(sp + 32);
-          uv[set][it][1] = *reinterpret_cast<const v4f32*>(sp + 36);
+        };
+        const int64_t step = static_cast<int64_t>(kRowsItS) * g.ldc;
+        stage_sw(0, hb0);
+        read_sw(hb0, 0);
+  #pragma unroll
+        for (int n = 0; n < NH; ++n) {
+          const int cur = n & 1;
+          if (n + 1 < NH) stage_sw(n + 1, cur ? hb0 : hb1);
+          const int i = n / 2, h = n % 2;
+          _Float16* c = static_cast<_Float16*>(g.C) +
+                        static_cast<int64_t>(mw + i * 32 + rsub) * g.ldc + nw / 2 + h * 32 + ch;
+  #pragma unroll
+          for (int it = 0; it < kItS; ++it) {
+            v8f16 hv;
+  #pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              // Same arithmetic as the general path below.
+              const float gval = gv[cur][it][e / 4][e % 4] * sgv[h][e / 4][e % 4];
+              const float uval = uv[cur][it][e / 4][e % 4] * suv[h][e / 4][e % 4];
+              const float ex = __builtin_amdgcn_exp2f(-gval * 1.4426950408889634f);
+              hv[e] = static_cast<_Float16>(gval * __builtin_amdgcn_rcpf(1.0f + ex) * uval);
+            }
+            if (!edge || (mw + i * 32 + it * kRowsItS + rsub < g.M && nw / 2 + h * 32 + ch < g.n_out))
+              __builtin_nontemporal_store(hv, reinterpret_cast<v8f16*>(c + it * step));
+          }
+          if (n + 1 < NH) read_sw(cur ? hb0 : hb1, cur ^ 1);
         }
       };
-      const int64_t step = static_cast<int64_t>(kRowsItS) * g.ldc;
-      stage_sw(0, hb0);
-      read_sw(hb0, 0);
-#pragma unroll
-      for (int n = 0; n < NH; ++n) {
-        const int cur = n & 1;
-        if (n + 1 < NH) stage_sw(n + 1, cur ? hb0 : hb1);
-        const int i = n / 2, h = n % 2;
-        _Float16* c = static_cast<_Float16*>(g.C) +
-                      static_cast<int64_t>(mw + i * 32 + rsub) * g.ldc + nw / 2 + h * 32 + ch;
-#pragma unroll
-        for (int it = 0; it < kItS; ++it) {
-          v8f16 hv;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            // Same arithmetic as the general path below.
-            const float gval = gv[cur][it][e / 4][e % 4] * sgv[h][e / 4][e % 4];
-            const float uval = uv[cur][it][e / 4][e % 4] * suv[h][e / 4][e % 4];
-            const float ex = __builtin_amdgcn_exp2f(-gval * 1.4426950408889634f);
-            hv[e] = static_cast<_Float16>(gval * __builtin_amdgcn_rcpf(1.0f + ex) * uval);
-          }
-          __builtin_nontemporal_store(hv, reinterpret_cast<v8f16*>(c + it * step));
-        }
-        if (n + 1 < NH) read_sw(cur ? hb0 : hb1, cur ^ 1);
-      }
+      if (full_sw)
+        pipeline(std::false_type{});
+      else
+        pipeline(std::true_type{});
       return;
     }
   }
   if constexpr (EPI == kEpiI32 || EPI == kEpiFloat) {
-    // Full tile, plain overwrite: 4-element runs, no per-run checks, one
-    // row address per block.
-    if (g.vec_store && !g.accumulate && m0 + BM <= g.M && n0 + BN <= g.N) {
-      constexpr int kRunsPerRow = TN / 4;
-      constexpr int kIt4 = 32 * TN / 4 / 64;
-      constexpr int kRowsIt4 = 64 / kRunsPerRow;
-      static_assert(64 % kRunsPerRow == 0, "4-element runs must tile the wave");
-      const int col = (lane % kRunsPerRow) * 4, rsub = lane / kRunsPerRow;
-      const int64_t step = static_cast<int64_t>(kRowsIt4) * g.ldc;
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        stage_block(i);
-        v4f32 wv[kIt4];
-#pragma unroll
-        for (int it = 0; it < kIt4; ++it)
-          wv[it] = *reinterpret_cast<const v4f32*>(stg + (it * kRowsIt4 + rsub) * kPad + col);
-        const int64_t off0 = static_cast<int64_t>(mw + i * 32 + rsub) * g.ldc + nw + col;
-        if constexpr (EPI == kEpiI32) {
-          int32_t* c = static_cast<int32_t*>(g.C) + off0;
-#pragma unroll
+    // Plain overwrite (full tiles, or edge tiles with N % 4 == 0):
+    // 4-element runs, one row address per block, a per-run check only on
+    // edge tiles.
+    const bool full4 = g.vec_store && !g.accumulate && m0 + BM <= g.M && n0 + BN <= g.N;
+    if (full4 || (g.vec_store && !g.accumulate && g.N % 4 == 0)) {
+      auto plain = [&](auto EDGE) {
+        constexpr bool edge = decltype(EDGE)::value;
+        constexpr int kRunsPerRow = TN / 4;
+        constexpr int kIt4 = 32 * TN / 4 / 64;
+        constexpr int kRowsIt4 = 64 / kRunsPerRow;
+        static_assert(64 % kRunsPerRow == 0, "4-element runs must tile the wave");
+        const int col = (lane % kRunsPerRow) * 4, rsub = lane / kRunsPerRow;
+        const int64_t step = static_cast<int64_t>(kRowsIt4) * g.ldc;
+        // The run of pass it of block row i lies inside C (tiles crossing M or N).
+        auto in_c = [&](int i, int it) {
+          return mw + i * 32 + it * kRowsIt4 + rsub < g.M && nw + col < g.N;
+        };
+  #pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          stage_block(i);
+          v4f32 wv[kIt4];
+  #pragma unroll
           for (int it = 0; it < kIt4; ++it)
-            __builtin_nontemporal_store(__builtin_bit_cast(v4u32_t, wv[it]),
-                                        reinterpret_cast<v4u32_t*>(c + it * step));
-        } else if (g.out_dtype == HXM_F32) {
-          float* c = static_cast<float*>(g.C) + off0;
-#pragma unroll
-          for (int it = 0; it < kIt4; ++it) *reinterpret_cast<v4f32*>(c + it * step) = wv[it];
-        } else if (g.out_dtype == HXM_F16) {
-          _Float16* c = static_cast<_Float16*>(g.C) + off0;
-#pragma unroll
-          for (int it = 0; it < kIt4; ++it) {
-            v4f16_t h;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) h[e] = static_cast<_Float16>(wv[it][e]);
-            *reinterpret_cast<v4f16_t*>(c + it * step) = h;
-          }
-        } else {
-          __bf16* c = static_cast<__bf16*>(g.C) + off0;
-#pragma unroll
-          for (int it = 0; it < kIt4; ++it) {
-            v4bf16_t h;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) h[e] = static_cast<__bf16>(wv[it][e]);
-            *reinterpret_cast<v4bf16_t*>(c + it * step) = h;
+            wv[it] = *reinterpret_cast<const v4f32*>(stg + (it * kRowsIt4 + rsub) * kPad + col);
+          const int64_t off0 = static_cast<int64_t>(mw + i * 32 + rsub) * g.ldc + nw + col;
+          if constexpr (EPI == kEpiI32) {
+            int32_t* c = static_cast<int32_t*>(g.C) + off0;
+  #pragma unroll
+            for (int it = 0; it < kIt4; ++it)
+              if (!edge || in_c(i, it))
+                __builtin_nontemporal_store(__builtin_bit_cast(v4u32_t, wv[it]),
+                                            reinterpret_cast<v4u32_t*>(c + it * step));
+          } else if (g.out_dtype == HXM_F32) {
+            float* c = static_cast<float*>(g.C) + off0;
+  #pragma unroll
+            for (int it = 0; it < kIt4; ++it)
+              if (!edge || in_c(i, it)) *reinterpret_cast<v4f32*>(c + it * step) = wv[it];
+          } else if (g.out_dtype == HXM_F16) {
+            _Float16* c = static_cast<_Float16*>(g.C) + off0;
+  #pragma unroll
+            for (int it = 0; it < kIt4; ++it) {
+              v4f16_t h;
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) h[e] = static_cast<_Float16>(wv[it][e]);
+              if (!edge || in_c(i, it)) *reinterpret_cast<v4f16_t*>(c + it * step) = h;
+            }
+          } else {
+            __bf16* c = static_cast<__bf16*>(g.C) + off0;
+  #pragma unroll
+            for (int it = 0; it < kIt4; ++it) {
+              v4bf16_t h;
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) h[e] = static_cast<__bf16>(wv[it][e]);
+              if (!edge || in_c(i, it)) *reinterpret_cast<v4bf16_t*>(c + it * step) = h;
+            }
           }
         }
-      }
+      };
+      if (full4)
+        plain(std::false_type{});
+      else
+        plain(std::true_type{});
       return;
     }
   }
 
-  // General path: edge tiles, accumulate, unaligned rows.
+  // General path: accumulate, unaligned rows, edge tiles whose runs may
+  // straddle N.
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     stage_block(i);

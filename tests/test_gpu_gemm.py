@@ -66,6 +66,62 @@ def test_gemm_i8_every_config(dev, cfg, K):
     assert np.array_equal(C, orc.gemm_i8(A.numpy(), B.numpy(), b_nk=True))
 
 
+@pytest.mark.parametrize("N", [264, 260])  # 8-element runs wholly inside C / straddling N
+@pytest.mark.parametrize("cfg", S.gemm_configs(hxm.I8), ids=repr)
+def test_gemm_i8_dequant_every_config_edges(dev, cfg, N):
+    """Tiles crossing M and N in the dequant epilogue: with N a multiple of 8
+    they take the pipelined path with a per-run predicate, otherwise the
+    general path."""
+    print(f"gemm_i8_dequant config {cfg} N={N}", flush=True)
+    M, K = 300, 640
+    A = rand_i8((M, K), 31)
+    B = rand_i8((N, K), 32)
+    g = torch.Generator().manual_seed(33)
+    rs = (torch.rand(M, generator=g) * 0.019 + 0.001).float()
+    cs = (torch.rand(N, generator=g) * 0.019 + 0.001).float()
+    D = ops.gemm_i8_dequant(A.to(dev), B.to(dev), rs.to(dev), cs.to(dev), b_layout="nk",
+                            config=cfg)
+    acc = orc.gemm_i8(A.numpy(), B.numpy(), b_nk=True)
+    assert np.array_equal(bits(D), orc.dequant_f16(acc, rs.numpy(), cs.numpy()))
+
+
+def test_edge_tiles_write_only_inside_the_output_view(dev):
+    """The edge-tile epilogues (N a multiple of the run length) store into a
+    [300, 264] view of a [320, 272] buffer: the padding columns and the rows
+    past the view keep their sentinel, for the int8 dequant, int32, f16 and
+    W8A16 outputs."""
+    M, N, K = 300, 264, 256
+    A = rand_i8((M, K), 41).to(dev)
+    B = rand_i8((N, K), 42).to(dev)
+    g = torch.Generator().manual_seed(43)
+    rs = (torch.rand(M, generator=g) * 0.019 + 0.001).float().to(dev)
+    cs = (torch.rand(N, generator=g) * 0.019 + 0.001).float().to(dev)
+    for dt, run in ((torch.float16, lambda o: ops.gemm_i8_dequant(A, B, rs, cs, out=o,
+                                                                     b_layout="nk")),
+                    (torch.int32, lambda o: ops.gemm_i8(A, B, out=o, b_layout="nk"))):
+        buf = torch.full((320, 272), 7, dtype=dt, device=dev)
+        ref = run(torch.empty(M, N, dtype=dt, device=dev))
+        run(buf[:M, :N])
+        assert torch.equal(buf[:M, :N], ref)
+        assert bool((buf[:M, N:] == 7).all()) and bool((buf[M:] == 7).all())
+    Af = (torch.rand(M, K, generator=g) * 2 - 1).half().to(dev)
+    Bf = (torch.rand(N, K, generator=g) * 2 - 1).half().to(dev)
+    buf = torch.full((320, 272), 7, dtype=torch.float16, device=dev)
+    ref = ops.matmul(Af, Bf, b_layout="nk")
+    ops.matmul(Af, Bf, out=buf[:M, :N], b_layout="nk")
+    assert torch.equal(buf[:M, :N], ref)
+    assert bool((buf[:M, N:] == 7).all()) and bool((buf[M:] == 7).all())
+    W = rand_i8((N, K), 44).to(dev)
+    sw = (torch.rand(N, generator=g) * 1e-3).float().to(dev)
+    r = torch.randn(M, N, generator=g).half().to(dev)
+    for res in (None, r):
+        buf = torch.full((320, 272), 7, dtype=torch.float16, device=dev)
+        ref = ops.gemm_w8a16(Af, W, sw, residual=res)
+        ops.gemm_w8a16(Af, W, sw, out=buf[:M, :N], residual=res)
+        assert torch.equal(buf[:M, :N], ref)
+        assert bool((buf[:M, N:] == 7).all()) and bool((buf[M:] == 7).all())
+
+
 def test_gemm_i8_accumulate_and_strides(dev):
     M, N, K = 96, 80, 256
     Afull = rand_i8((M, 320), 5)

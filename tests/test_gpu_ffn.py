@@ -51,9 +51,12 @@ def test_gemm_w8a16_every_config(dev, cfg, K):
     print(f"gemm_w8a16 config {cfg} K={K}", flush=True)
     M, N = 300, 520
     x, W, s = operands(M, N, K, 7)
-    y = ops.gemm_w8a16(x.to(dev), W.to(dev), s.to(dev), config=cfg)
+    xd, Wd, sd = x.to(dev), W.to(dev), s.to(dev)
+    y = ops.gemm_w8a16(xd, Wd, sd, config=cfg)
     ref = orc.gemm_w8a16(bits(x), W.numpy(), s.numpy())
     np.testing.assert_allclose(y.float().cpu().numpy(), f32(ref), **TOL)
+    # every tile groups K into the same k-steps: bit-identical to the default
+    assert torch.equal(y, ops.gemm_w8a16(xd, Wd, sd))
 
 
 def test_gemm_w8a16_small_integers_bit_exact(dev):

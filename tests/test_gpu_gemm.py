@@ -53,11 +53,12 @@ def test_gemm_i8_golden(dev, golden):
     assert np.array_equal(bits(d), g["dequant_f16_bits"])
 
 
-@pytest.mark.parametrize("K", [640, 656])  # K bytes a multiple of every stage depth / not
+@pytest.mark.parametrize("K", [640, 656, 16])  # K bytes a multiple of every stage depth / not
 @pytest.mark.parametrize("cfg", S.gemm_configs(hxm.I8), ids=repr)
 def test_gemm_i8_every_config(dev, cfg, K):
     """Both main loops of every compiled tile: the one without the per-lane
-    K test (K a multiple of the stage depth) and the one with it."""
+    K test (K a multiple of the stage depth) and the one with it (K = 16 is
+    a single partial stage)."""
     print(f"gemm_i8 config {cfg} K={K}", flush=True)
     M, N = 300, 260
     A = rand_i8((M, K), 3)
@@ -204,18 +205,24 @@ def test_matmul_within_tolerance(dev, M, N, K, dt):
     np.testing.assert_allclose(c32, ref32, rtol=1e-4, atol=1e-4)
 
 
-@pytest.mark.parametrize("K", [640, 648])  # K bytes a multiple of every stage depth / not
+# K = 640: K bytes a multiple of every stage depth; 656: not, a whole number
+# of 16-element k-steps; 648: ends in a partial k-step.
+@pytest.mark.parametrize("K", [640, 656, 648])
 @pytest.mark.parametrize("cfg", S.gemm_configs(hxm.F16), ids=repr)
 def test_matmul_every_config(dev, cfg, K):
+    """Every tile within tolerance of the oracle and bit-identical to the
+    default tile: all tiles group K into the same 16-element k-steps."""
     print(f"matmul f16/bf16 config {cfg} K={K}", flush=True)
     M, N = 300, 260
     g = torch.Generator().manual_seed(K)
     for dt, name in ((torch.float16, "f16"), (torch.bfloat16, "bf16")):
         A = (torch.rand(M, K, generator=g) * 2 - 1).to(dt)
         B = (torch.rand(K, N, generator=g) * 2 - 1).to(dt)
-        C = ops.matmul(A.to(dev), B.t().contiguous().to(dev), b_layout="nk", config=cfg)
+        Ad, Bd = A.to(dev), B.t().contiguous().to(dev)
+        C = ops.matmul(Ad, Bd, b_layout="nk", config=cfg)
         ref = orc.to_f32(orc.matmul(bits(A), bits(B), ab_dtype=name, c_dtype=name), name)
         np.testing.assert_allclose(C.float().cpu().numpy(), ref, rtol=1e-2, atol=1e-3)
+        assert torch.equal(C, ops.matmul(Ad, Bd, b_layout="nk"))
 
 
 def test_matmul_small_integers_bit_exact(dev, golden):

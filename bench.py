@@ -169,9 +169,12 @@ def run_rows(c):
     xs = [(torch.randn(rows, cols, device=c.dev) * 2).half() for _ in range(R)]
     ys = [torch.empty_like(xs[0]) for _ in range(R)]
     gam = (1 + 0.1 * torch.randn(cols, device=c.dev)).half()
+    beta = (0.1 * torch.randn(cols, device=c.dev)).half()
+    mean = torch.empty(rows, dtype=torch.float32, device=c.dev)
+    rstd = torch.empty(rows, dtype=torch.float32, device=c.dev)
     xp = [t.data_ptr() for t in xs]
     yp = [t.data_ptr() for t in ys]
-    gp, st = gam.data_ptr(), c.stream
+    gp, bp, st = gam.data_ptr(), beta.data_ptr(), c.stream
 
     def softmax(i):
         hxm.check(L.hxm_softmax_rows(xp[i], cols, yp[i], cols, rows, cols, hxm.F16, st),
@@ -180,9 +183,15 @@ def run_rows(c):
     def rms(i):
         hxm.check(L.hxm_rmsnorm_rows(xp[i], cols, gp, yp[i], cols, rows, cols, 1e-6, hxm.F16,
                                      st), "hxm_rmsnorm_rows")
+    def layernorm(i):  # with the saved mean / rstd (layer_norm_fwd_kernel's outputs)
+        hxm.check(L.hxm_layernorm_rows(xp[i], cols, gp, bp, yp[i], cols, mean.data_ptr(),
+                                       rstd.data_ptr(), rows, cols, 1e-5, hxm.F16, st),
+                  "hxm_layernorm_rows")
     out = {}
     for name, fn, nbytes in (("softmax_f16_8192x4096", softmax, 2 * rows * cols * 2),
-                             ("rmsnorm_f16_8192x4096", rms, 2 * rows * cols * 2 + cols * 2)):
+                             ("rmsnorm_f16_8192x4096", rms, 2 * rows * cols * 2 + cols * 2),
+                             ("layernorm_f16_8192x4096", layernorm,
+                              2 * rows * cols * 2 + 2 * cols * 2 + 2 * rows * 4)):
         ms, _ = c.time_ms(fn, 200, 20, rotate=R)
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"us": ms * 1e3, "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,

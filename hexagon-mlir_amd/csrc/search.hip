@@ -583,16 +583,34 @@ hxm_status hxm_tune_cache_load(const char* path, int32_t* loaded) {
   }
   int32_t n = 0;
   while (std::fgets(line, sizeof(line), f)) {
-    int op, reps;
-    long long M, N, K;
-    hxm_gemm_config c;
-    if (std::sscanf(line, "%d %lld %lld %lld %d %d %d %d %d %d %d %d", &op, &M, &N, &K, &c.bm,
-                    &c.bn, &c.bk, &c.waves_m, &c.waves_n, &c.stages, &c.split_k, &reps) != 12)
+    // A line longer than the buffer is not an entry: skip it whole rather
+    // than parse its pieces.
+    if (!std::strchr(line, '\n') && !std::feof(f)) {
+      int ch;
+      while ((ch = std::fgetc(f)) != EOF && ch != '\n') {
+      }
       continue;
-    if (M < 0 || N < 0 || K < 0 || !config_compiled(op, c)) continue;
+    }
+    // Every field is read as 64-bit and range-checked before it narrows, so
+    // an out-of-range value cannot wrap onto a compiled configuration.
+    long long v[12];
+    if (std::sscanf(line, "%lld %lld %lld %lld %lld %lld %lld %lld %lld %lld %lld %lld", &v[0],
+                    &v[1], &v[2], &v[3], &v[4], &v[5], &v[6], &v[7], &v[8], &v[9], &v[10],
+                    &v[11]) != 12)
+      continue;
+    bool in_range = v[0] >= 0 && v[0] <= INT32_MAX && v[11] >= 1 && v[11] <= 10000;
+    for (int i = 1; i <= 3; ++i) in_range = in_range && v[i] >= 0 && v[i] <= INT32_MAX;
+    for (int i = 4; i <= 10; ++i) in_range = in_range && v[i] >= 0 && v[i] <= 4096;
+    if (!in_range) continue;
+    const int32_t op = static_cast<int32_t>(v[0]);
+    const hxm_gemm_config c = {static_cast<int32_t>(v[4]), static_cast<int32_t>(v[5]),
+                               static_cast<int32_t>(v[6]), static_cast<int32_t>(v[7]),
+                               static_cast<int32_t>(v[8]), static_cast<int32_t>(v[9]),
+                               static_cast<int32_t>(v[10])};
+    if (!config_compiled(op, c)) continue;
     std::lock_guard<std::mutex> lk(g_tune_mu);
-    g_tuned[TuneKey(op, M, N, K)] = c;
-    g_tuned_reps[TuneKey(op, M, N, K)] = reps;
+    g_tuned[TuneKey(op, v[1], v[2], v[3])] = c;
+    g_tuned_reps[TuneKey(op, v[1], v[2], v[3])] = static_cast<int32_t>(v[11]);
     ++n;
   }
   std::fclose(f);

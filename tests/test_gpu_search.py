@@ -46,7 +46,8 @@ def test_tune_gemm_picks_a_verified_winner(dev, dtype, M, N, K):
 
 def test_tune_cache_save_load_round_trip(dev, tmp_path):
     """A tuned winner survives save -> clear -> load on the same build and
-    device; an entry naming a tile this build did not compile is skipped."""
+    device; entries naming a tile this build did not compile, out-of-range fields and
+    over-long lines are skipped."""
     import hxm
     from hxm import search as S
     hxm.lib.hxm_tune_cache_clear()
@@ -61,13 +62,21 @@ def test_tune_cache_save_load_round_trip(dev, tmp_path):
     assert win is not None and win.as_tuple() == best.as_tuple()
     p = tmp_path / "tune.txt"
     S.tune_cache_save(str(p))
+    bm, bn, bk, wm, wn, st, sk = best.as_tuple()
+    cfg = f"{bm} {bn} {bk} {wm} {wn} {st} {sk}"
     with open(p, "a") as f:
         f.write("4 1024 1024 1024 96 96 128 2 2 2 1 3\n")   # no such compiled tile
+        f.write(f"4 1536 1536 1536 {bm + 2 ** 32} {bn} {bk} {wm} {wn} {st} {sk} 3\n")  # wraps
+        f.write(f"4 1536 1536 1536 {cfg} 0\n")               # reps out of range
+        f.write(f"4 -1 1536 1536 {cfg} 3\n")                 # negative extent
+        # over-long line whose tail alone would read as a valid entry
+        f.write("9" + " " * 254 + f"4 2048 2048 2048 {cfg} 3\n")
     hxm.lib.hxm_tune_cache_clear()
     assert S.tune_cache_lookup(hxm.I8, M, N, K) is None
     assert S.tune_cache_load(str(p)) == 1
     assert S.tune_cache_lookup(hxm.I8, M, N, K).as_tuple() == best.as_tuple()
-    assert S.tune_cache_lookup(hxm.I8, 1024, 1024, 1024) is None
+    for n in (1024, 1536, 2048):
+        assert S.tune_cache_lookup(hxm.I8, n, n, n) is None
     C = ops.gemm_i8(A, B, b_layout="nk").cpu().numpy()     # runs the reloaded winner
     assert np.array_equal(C, orc.gemm_i8(A.cpu().numpy(), B.cpu().numpy(), b_nk=True))
     hxm.lib.hxm_tune_cache_clear()

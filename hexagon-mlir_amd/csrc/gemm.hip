@@ -127,6 +127,25 @@ hxm_status launch_gemm(const KernelEntry& e, int32_t ab_dtype, int epi,
 
 namespace {
 
+// The kernels address a tile's rows of an operand with 32-bit offsets from
+// the tile's first row, inside a buffer resource of at most 2 GiB: the
+// kTileRowsMax rows of the tallest tile must span less than that.
+constexpr int64_t kTileRowsMax = 256;
+#define HXM_TILE_EDGE(BM, BN, BKB, ST, WM, WN) ((BM) > (BN) ? (BM) : (BN))
+constexpr int kTileEdges[] = {HXM_GEMM_CONFIG_LIST(HXM_TILE_EDGE),
+                              HXM_W8_CONFIG_LIST(HXM_TILE_EDGE)};
+#undef HXM_TILE_EDGE
+constexpr bool tile_edges_fit() {
+  for (int e : kTileEdges)
+    if (e > kTileRowsMax) return false;
+  return true;
+}
+static_assert(tile_edges_fit(), "a compiled tile is taller than kTileRowsMax");
+
+bool tile_rows_addressable(int64_t ld_bytes, int64_t row_bytes) {
+  return ld_bytes <= (INT32_MAX - row_bytes) / (kTileRowsMax - 1);
+}
+
 hxm_status validate_common(const char* op, const void* A, int64_t lda,
                            const void* B, int64_t ldb, int32_t b_layout,
                            const void* C, int64_t ldc, int64_t M, int64_t N,
@@ -143,6 +162,14 @@ hxm_status validate_common(const char* op, const void* A, int64_t lda,
                 op);
   if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K * eb > INT32_MAX / 2)
     return fail(HXM_UNSUPPORTED_SHAPE, "tile-alignment: %s extent beyond 2^30", op);
+  // A [K,N] B is packed into an [N,K] image with rows of K elements.
+  const int64_t ldb_image = b_layout == HXM_B_NK ? ldb : K;
+  if (K > 0 && (!tile_rows_addressable(lda * eb, K * eb) ||
+                !tile_rows_addressable(ldb_image * eb, K * eb)))
+    return fail(HXM_UNSUPPORTED_SHAPE,
+                "tile-alignment: %s needs %lld rows of A and of the [N,K] B image within "
+                "2 GiB (lda=%lld, ldb=%lld)",
+                op, (long long)kTileRowsMax, (long long)lda, (long long)ldb_image);
   // The MFMA kernels stream 16-byte K chunks of A and of the [N,K] image;
   // a [K,N] B is first packed by the library, so only its image is aligned.
   const bool b_nk = b_layout == HXM_B_NK;
@@ -366,6 +393,11 @@ static hxm_status validate_w8(const char* op, const void* x, int64_t ldx, const 
     return fail(HXM_INVALID_ARG, "invalid-argument: %s leading dimension too small", op);
   if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 4)
     return fail(HXM_UNSUPPORTED_SHAPE, "tile-alignment: %s extent beyond 2^29", op);
+  if (K > 0 && (!tile_rows_addressable(ldx * 2, K * 2) || !tile_rows_addressable(ldw, K)))
+    return fail(HXM_UNSUPPORTED_SHAPE,
+                "tile-alignment: %s needs %lld rows of x and of W within 2 GiB (ldx=%lld, "
+                "ldw=%lld)",
+                op, (long long)kTileRowsMax, (long long)ldx, (long long)ldw);
   if (K % 16 || (K > 0 && ((ldx * 2) % 16 || ldw % 16 || !aligned16(x) || !aligned16(W))))
     return fail(HXM_UNSUPPORTED_SHAPE,
                 "tile-alignment: %s needs K, ldw in multiples of 16 and lda in multiples "

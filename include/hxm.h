@@ -120,7 +120,10 @@ hxm_status hxm_query_contraction(int64_t M, int64_t N, int64_t K,
  * {F16, BF16, F32}.  Products accumulate in fp32 (with the prior C added
  * in fp32 when accumulate != 0) and round once to c_dtype.
  * K*sizeof(elem) must be a multiple of 16 bytes, lda/ldb likewise, and
- * A/B 16-byte aligned ("tile-alignment" otherwise); M and N are free. */
+ * A/B 16-byte aligned ("tile-alignment" otherwise); M and N are free.
+ * 256 rows of A and of the [N,K] B image must lie within 2 GiB
+ * (255 * ld * sizeof(elem) + K * sizeof(elem) < 2^31; "tile-alignment"
+ * otherwise): the kernels address a tile's rows with 32-bit offsets. */
 hxm_status hxm_matmul(const void* A, int64_t lda, const void* B, int64_t ldb,
                       int32_t b_layout, void* C, int64_t ldc, int64_t M,
                       int64_t N, int64_t K, int32_t ab_dtype, int32_t c_dtype,
@@ -131,7 +134,8 @@ hxm_status hxm_matmul(const void* A, int64_t lda, const void* B, int64_t ldb,
  * int8 on the engine, HmxTarget.h:198-200, and lowers it on the HVX
  * generic path, LinalgToLLVMPass.cpp:364-365; its result is the exact
  * integer product).  C_i32[M,N] = (accumulate ? C : 0) + A . B, wrapping
- * int32 addition.  K, lda, ldb multiples of 16; A, B 16-byte aligned. */
+ * int32 addition.  K, lda, ldb multiples of 16; A, B 16-byte aligned; the
+ * same 2 GiB span of 256 rows as hxm_matmul. */
 hxm_status hxm_gemm_i8(const int8_t* A, int64_t lda, const int8_t* B,
                        int64_t ldb, int32_t b_layout, int32_t* C, int64_t ldc,
                        int64_t M, int64_t N, int64_t K, int32_t accumulate,
@@ -238,7 +242,8 @@ enum { HXM_OP_W8A16 = 16, HXM_OP_W8A16_SWIGLU = 17 };
  * x fp16 [M,K] (ldx >= K); W int8 [N,K] (ldw >= K); w_scale fp32 [N];
  * y fp16 [M,N] (ldy >= N).  fp32 accumulation in MFMA order (tolerance
  * rtol 1e-2 / atol 1e-3).  K multiple of 16, ldx multiple of 8, ldw
- * multiple of 16, x and W 16-byte aligned.  cfg: NULL = tuned winner or the
+ * multiple of 16, x and W 16-byte aligned, and 256 rows of x and of W
+ * within 2 GiB (as for hxm_matmul).  cfg: NULL = tuned winner or the
  * default tile; else one of hxm_w8a16_configs. */
 hxm_status hxm_gemm_w8a16(const void* x, int64_t ldx, const int8_t* W,
                           int64_t ldw, const float* w_scale, void* y,

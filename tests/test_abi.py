@@ -72,6 +72,12 @@ def test_refusals_happen_before_launch():
     # an unknown B layout
     st = L.hxm_gemm_i8(16, 32, 16, 32, 7, 16, 8, 8, 8, 32, 0, None, None)
     assert st == _lib.HXM_INVALID_ARG
+    # rows 16 MiB apart: 256 rows of a tile would span 4 GiB of 32-bit offsets
+    st = L.hxm_gemm_i8(16, 1 << 24, 16, 32, hxm.B_NK, 16, 8, 8, 8, 32, 0, None, None)
+    assert st == _lib.HXM_UNSUPPORTED_SHAPE
+    assert hxm.last_error().startswith("tile-alignment") and "2 GiB" in hxm.last_error()
+    st = L.hxm_gemm_w8a16(16, 32, 16, 1 << 24, 16, 16, 8, 8, 8, 32, None, None)
+    assert st == _lib.HXM_UNSUPPORTED_SHAPE and "2 GiB" in hxm.last_error()
 
 
 @pytest.mark.skipif("_gpu_present()")

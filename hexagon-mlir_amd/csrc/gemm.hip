@@ -115,6 +115,8 @@ hxm_status launch_gemm(const KernelEntry& e, int32_t ab_dtype, int epi,
   const int bm = e.cfg.bm, bn = e.cfg.bn;
   const int64_t tiles = static_cast<int64_t>((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
   const int i = static_cast<int>(&e - kKernels);
+  hxm_status st = check_grid("gemm", tiles, e.threads);
+  if (st != HXM_OK) return st;
   gemm_fn fn = nullptr;
   if (ab_dtype == HXM_I8)
     fn = part_fn(kI8Parts, i, epi == kEpiDequant ? 1 : 0);
@@ -193,9 +195,10 @@ hxm_status resolve_b(const void* B, int64_t ldb, int32_t b_layout, int64_t K,
     *ldb_bytes_out = ldb * eb;
     return HXM_OK;
   }
-  void* ws = nullptr;
-  hxm_status st = stream_workspace(stream, static_cast<size_t>(N * K * eb), &ws);
+  hxm_status st = check_grid("weight pack", (N + 31) / 32, 256, (K + 31) / 32);
   if (st != HXM_OK) return st;
+  void* ws = nullptr;
+  if ((st = stream_workspace(stream, static_cast<size_t>(N * K * eb), &ws)) != HXM_OK) return st;
   const dim3 grid(static_cast<unsigned>((N + 31) / 32), static_cast<unsigned>((K + 31) / 32));
   if (eb == 1)
     transpose_kernel<uint8_t><<<grid, 256, 0, stream>>>(
@@ -372,6 +375,7 @@ hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const in
   g.vec_store = (reinterpret_cast<uintptr_t>(C) % 8 == 0) && ((ldc * 2) % 8 == 0);
   g.vec8_store = (reinterpret_cast<uintptr_t>(C) % 16 == 0) && ((ldc * 2) % 16 == 0);
   const int64_t tiles = ((M + e->cfg.bm - 1) / e->cfg.bm) * ((N + e->cfg.bn - 1) / e->cfg.bn);
+  if ((st = check_grid("w8a16 gemm", tiles, e->threads)) != HXM_OK) return st;
   const int wi = static_cast<int>(e - kW8Kernels);
   hipLaunchKernelGGL(part_fn(kW8Parts, wi, sw ? 1 : epi == kEpiW8Res ? 2 : 0),
                      dim3(static_cast<unsigned>(tiles)),
@@ -506,6 +510,7 @@ hxm_status hxm_prepack_weight(const void* B, int64_t ldb, void* out,
   hxm_status st = require_device(nullptr);
   if (st != HXM_OK) return st;
   if (K == 0 || N == 0) return ok();
+  if ((st = check_grid("prepack", (N + 31) / 32, 256, (K + 31) / 32)) != HXM_OK) return st;
   hipStream_t s = as_stream(stream);
   const dim3 grid(static_cast<unsigned>((N + 31) / 32), static_cast<unsigned>((K + 31) / 32));
   if (dtype == HXM_I8)
@@ -571,6 +576,7 @@ hxm_status hxm_swiglu_pack(const int8_t* Wg, const int8_t* Wu, int64_t ldw,
   if (st != HXM_OK) return st;
   if (I == 0) return ok();
   const int64_t rows = hxm_swiglu_packed_rows(I);
+  if ((st = check_grid("swiglu pack", rows, 256)) != HXM_OK) return st;
   swiglu_pack_kernel<<<static_cast<unsigned>(rows), 256, 0, as_stream(stream)>>>(
       Wg, Wu, ldw, gate_scale, up_scale, I, K, Wgu, sgu);
   return check_launch("swiglu pack");

@@ -246,6 +246,7 @@ hxm_status hxm_prepack_w8a16(const int8_t* W, int64_t ldw, int64_t N, int64_t K,
   if (N == 0 || K == 0) return ok();
   const int64_t nblocks = packed_bytes(N, K) / 1024;
   const int64_t threads = nblocks * 64;
+  if ((st = check_grid("prepack_w8a16", (threads + 255) / 256, 256)) != HXM_OK) return st;
   pack_w8a16_kernel<<<static_cast<unsigned>((threads + 255) / 256), 256, 0, as_stream(stream)>>>(
       W, ldw, static_cast<int>(N), static_cast<int>(K), out, nblocks);
   return check_launch("prepack_w8a16");
@@ -284,6 +285,9 @@ hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W, int64_t l
   // keeps more workgroups resident per CU.
   hipStream_t s = as_stream(stream);
   const bool pk = w_layout == HXM_W_PACKED;
+  const int cb = M <= 4 ? 1 : 3;
+  if ((st = check_grid("gemv_w8a16", (N + 16 * cb - 1) / (16 * cb), 512, (M + 15) / 16)) != HXM_OK)
+    return st;
   // Small M: a 4096-wide K chunk (x rows fit LDS), so at K <= 4096 each wave
   // issues all its weight loads at once and makes one memory round trip.
   if (M <= 1) {

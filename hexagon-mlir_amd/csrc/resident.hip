@@ -178,6 +178,9 @@ hxm_status hxm_resident_weight(const void* src, int64_t ld, int64_t rows, int64_
       st = hxm_prepack_w8a16(static_cast<const int8_t*>(src), ld, rows, cols,
                              static_cast<int8_t*>(img.ptr), bytes, stream);
     } else if (src_dtype == HXM_F32) {
+      if ((st = check_grid("f32 weight image", (cols + 31) / 32, 256, (rows + 31) / 32)) !=
+          HXM_OK)
+        return st;
       const dim3 grid(static_cast<unsigned>((cols + 31) / 32),
                       static_cast<unsigned>((rows + 31) / 32));
       f32_to_f16_image_kernel<<<grid, 256, 0, s>>>(static_cast<const float*>(src), ld,

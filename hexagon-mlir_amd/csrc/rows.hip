@@ -396,6 +396,8 @@ template <typename T, int OP, bool ALIGNED>
 hxm_status launch_rows_t(const RowArgs& a, hipStream_t stream) {
   constexpr int N = RowVec<T>::N;
   const int64_t vpl = (a.cols + 64 * N - 1) / (64 * N);
+  hxm_status st = check_grid("row kernel", (a.rows + kRowWaves - 1) / kRowWaves, 64 * kRowWaves);
+  if (st != HXM_OK) return st;
   const dim3 grid(static_cast<unsigned>((a.rows + kRowWaves - 1) / kRowWaves));
   const dim3 block(64 * kRowWaves);
   if (vpl <= 1)

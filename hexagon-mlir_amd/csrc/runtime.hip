@@ -40,6 +40,14 @@ hxm_status ok() {
   return HXM_OK;
 }
 
+hxm_status check_grid(const char* what, int64_t groups_x, int threads, int64_t groups_y) {
+  if (grid_fits(groups_x, threads, groups_y)) return HXM_OK;
+  return fail(HXM_UNSUPPORTED_SHAPE,
+              "tile-alignment: %s needs a grid of %lld x %lld workgroups of %d threads, beyond "
+              "the launch limit",
+              what, (long long)groups_x, (long long)groups_y, threads);
+}
+
 hxm_status check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)

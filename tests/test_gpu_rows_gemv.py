@@ -108,6 +108,24 @@ def test_rows_strided_inplace_and_edge_values(dev):
     assert ops.softmax(torch.empty(0, 32, dtype=torch.float16, device=dev)).shape == (0, 32)
 
 
+def test_grid_beyond_the_launch_limit_is_refused(dev):
+    """2^26 + 4 rows need 2^24 + 1 workgroups of 256 threads, more than 2^32
+    work-items: refused before any launch, nothing written.  The buffers hold
+    every row, so the test reads and writes in bounds whatever the launcher
+    does."""
+    import hxm
+    from hxm import _lib
+    rows = (1 << 26) + 4
+    x = torch.zeros(rows, 8, dtype=torch.float16, device=dev)
+    y = torch.full((rows, 8), 3.0, dtype=torch.float16, device=dev)
+    st = hxm.lib.hxm_softmax_rows(x.data_ptr(), 8, y.data_ptr(), 8, rows, 8, hxm.F16,
+                                  torch.cuda.current_stream().cuda_stream)
+    assert st == _lib.HXM_UNSUPPORTED_SHAPE and "launch limit" in hxm.last_error()
+    assert bool((y[-4:] == 3).all()) and bool((y[:4] == 3).all())
+    del x, y
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("M", [1, 4, 16])
 @pytest.mark.parametrize("packed", [True, False])
 def test_gemv_baseline_shape(dev, M, packed):

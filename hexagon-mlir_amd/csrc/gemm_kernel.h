@@ -267,6 +267,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   using LB = StageLoad<BN, BKB_B, NW>;
   constexpr int LPW = LA::L + LB::L;  // DMA instructions per wave per stage
   static_assert(!BQ || std::is_same<T, _Float16>::value, "int8 B pairs with f16 A");
+  // int8 B: block 0 of a stage's first k-step is read at the barrier slot
+  // NF/2 of the previous stage's last k-step and converted in its slots
+  // NF-2 and NF-1, which must not come before the read.
+  static_assert(!BQ || NF >= 4, "int8 B needs at least 4 MFMA slots per k-step");
   static_assert(EPI != kEpiSwiglu || TN == 128, "SwiGLU image interleaves 64-channel blocks");
   // Epilogue scales in LDS: rows [0, QR*64), columns [QR*64, (QR+QC)*64) floats.
   constexpr int QR = EPI == kEpiDequant ? (BM + 63) / 64 : 0;

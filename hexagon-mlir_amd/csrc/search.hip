@@ -720,4 +720,205 @@ hxm_status hxm_tune_w8a16(int32_t op, const void* x, int64_t ldx, const int8_t* 
   return tune_core(sp, reps, best, report, report_cap);
 }
 
+// ---- modeled cost: predict_tile_pcyc / rank_tile_candidates / cost_prune --
+// (hmx_search.py:778-887, :1030-1067, :916-1027).  The reference's units are
+// pack sites, engine calls and unpack sites priced by table cells; the GPU's
+// are tiles, tiles per CU and K stages, priced by the device's rates.
+
+const char* hxm_abstain_string(int32_t abstain) {
+  switch (abstain) {
+    case HXM_ABSTAIN_NONE: return "none";
+    case HXM_ABSTAIN_HEAT_BAND: return "heat-band";
+    case HXM_ABSTAIN_HEAT_CROSS: return "heat-cross-boundary";
+    case HXM_ABSTAIN_TAIL: return "tail-blocks";
+    case HXM_ABSTAIN_DTYPE: return "dtype-no-cell";
+    case HXM_ABSTAIN_MANIFEST: return "manifest-strategy-unknown";
+    case HXM_ABSTAIN_NO_CELL: return "no-applicable-cell";
+    case HXM_ABSTAIN_TABLE_MISSING: return "table-missing";
+    default: return "unknown-abstain";
+  }
+}
+
+void hxm_device_model_nominal(hxm_device_model* out) {
+  if (!out) return;
+  hxm_device_model m;
+  m.cus = 256;
+  m.tier = HXM_TIER_NOMINAL;
+  m.sclk_mhz_peak = 2400.0;
+  m.sclk_mhz_sustained = 1400.0;
+  m.hbm_gbps_peak = 8000.0;
+  m.hbm_gbps_sustained = 5000.0;
+  m.lds_fill_peak = 128.0;
+  m.lds_fill_sustained = 48.0;
+  m.launch_us = 2.5;
+  m.lds_bytes = 160 * 1024;
+  m.cache_bytes = 256ll * 1024 * 1024;
+  *out = m;
+}
+
+hxm_status hxm_device_model_query(hxm_device_model* out) {
+  if (!out) return fail(HXM_INVALID_ARG, "invalid-argument: device_model_query null output");
+  hxm_status st = require_device(nullptr);
+  if (st != HXM_OK) return st;
+  int dev = 0;
+  hipDeviceProp_t prop;
+  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
+    return fail(HXM_HIP_ERROR, "hip-error: hipGetDeviceProperties failed");
+  hxm_device_model m;
+  hxm_device_model_nominal(&m);
+  m.cus = prop.multiProcessorCount;
+  if (prop.clockRate > 0) m.sclk_mhz_peak = prop.clockRate / 1000.0;  // kHz
+  if (m.sclk_mhz_sustained > m.sclk_mhz_peak) m.sclk_mhz_sustained = m.sclk_mhz_peak;
+  if (prop.maxSharedMemoryPerMultiProcessor > 0)
+    m.lds_bytes = static_cast<int64_t>(prop.maxSharedMemoryPerMultiProcessor);
+  m.tier = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? HXM_TIER_CURRENT
+                                                            : HXM_TIER_UNKNOWN;
+  *out = m;
+  return ok();
+}
+
+int32_t hxm_predict_tile_time(int64_t M, int64_t N, int64_t K, const hxm_gemm_config* cfg,
+                              int32_t ab_dtype, int32_t out_dtype,
+                              const hxm_device_model* model, hxm_tile_prediction* out) {
+  const double nan = std::nan("");
+  hxm_tile_prediction p;
+  p.lb_us = p.ub_us = p.p50_us = nan;
+  p.units[0] = p.units[1] = p.units[2] = 0;
+  p.abstain = HXM_ABSTAIN_NONE;
+  p.tier = model ? model->tier : HXM_TIER_UNKNOWN;
+  p.heat = -1;
+  p.reserved = 0;
+  auto done = [&](int32_t a) {
+    p.abstain = a;
+    if (out) *out = p;
+    return a;
+  };
+  const int64_t eb = ab_dtype == HXM_I8 ? 1 : (ab_dtype == HXM_F16 || ab_dtype == HXM_BF16) ? 2 : 0;
+  const int64_t ob = out_dtype == HXM_I32 || out_dtype == HXM_F32 ? 4
+                     : (out_dtype == HXM_F16 || out_dtype == HXM_BF16) ? 2 : 0;
+  if (!eb || !ob) return done(HXM_ABSTAIN_DTYPE);
+  if (!model) return done(HXM_ABSTAIN_TABLE_MISSING);
+  if (!cfg || cfg->bm <= 0 || cfg->bn <= 0 || cfg->bk <= 0 || M <= 0 || N <= 0 || K <= 0)
+    return done(HXM_ABSTAIN_NO_CELL);
+  if (M % cfg->bm || N % cfg->bn || K % cfg->bk) return done(HXM_ABSTAIN_TAIL);
+  // Heat: the operands (A + B) and the whole footprint (A + B + C) are each
+  // cache-resident at or below half the last-level cache, HBM-bound at or
+  // above all of it; the band between is unmeasured, and the two footprints
+  // on opposite sides leave the class undetermined.
+  const double cache = static_cast<double>(model->cache_bytes);
+  if (!(cache > 0.0)) return done(HXM_ABSTAIN_NO_CELL);
+  const double in_bytes = (static_cast<double>(M) * K + static_cast<double>(K) * N) * eb;
+  const double all_bytes = in_bytes + static_cast<double>(M) * N * ob;
+  auto heat_of = [&](double b) { return b <= 0.5 * cache ? 0 : b >= cache ? 1 : 2; };
+  const int h_in = heat_of(in_bytes), h_all = heat_of(all_bytes);
+  if (h_in == 2 || h_all == 2) return done(HXM_ABSTAIN_HEAT_BAND);
+  if (h_in != h_all) return done(HXM_ABSTAIN_HEAT_CROSS);
+  p.heat = h_in;
+  const double rates[] = {model->sclk_mhz_peak, model->sclk_mhz_sustained, model->hbm_gbps_peak,
+                          model->hbm_gbps_sustained, model->lds_fill_peak,
+                          model->lds_fill_sustained};
+  for (double r : rates)
+    if (!(r > 0.0) || !is_fin(r)) return done(HXM_ABSTAIN_NO_CELL);
+  if (model->cus <= 0 || !(model->launch_us >= 0.0) || !is_fin(model->launch_us) ||
+      model->lds_bytes <= 0)
+    return done(HXM_ABSTAIN_NO_CELL);
+  // Only a compiled, LDS-legal kernel has a price.
+  if (hxm_gpu_tile_verdict(cfg, ab_dtype, model->lds_bytes) != HXM_REASON_OK)
+    return done(HXM_ABSTAIN_NO_CELL);
+
+  const int64_t bm = cfg->bm, bn = cfg->bn, bk = cfg->bk;
+  const int64_t stages = cfg->stages > 0 ? cfg->stages : 2;
+  const int64_t tiles = (M / bm) * (N / bn);
+  const int64_t per_cu = (tiles + model->cus - 1) / model->cus;
+  p.units[0] = tiles;
+  p.units[1] = per_cu;
+  p.units[2] = K / bk;
+  // MFMA ops per clock per SIMD (4 SIMDs per CU): 2048 int8, 1024 f16/bf16.
+  const double simd_rate = eb == 1 ? 2048.0 : 1024.0;
+  const double waves = std::min<int64_t>(4, static_cast<int64_t>(cfg->waves_m) * cfg->waves_n);
+  const int64_t wg_lds = std::max<int64_t>(1, model->lds_bytes / (stages * (bm + bn) * bk * eb));
+  const double tile_ops = 2.0 * bm * bn * K;
+  const double fill_bytes = static_cast<double>(bm + bn) * K * eb;  // L2 -> LDS per tile
+  // Lower bound: the busiest CU's share at peak rates, perfect overlap.
+  const double c_all = per_cu * tile_ops / (4.0 * simd_rate);
+  const double c_conc =
+      static_cast<double>((per_cu + wg_lds - 1) / wg_lds) * tile_ops / (waves * simd_rate);
+  const double s_lb = per_cu * fill_bytes / model->lds_fill_peak;
+  double lb = std::max(std::max(c_all, c_conc), s_lb) / model->sclk_mhz_peak;  // cycles/MHz = us
+  if (p.heat == 1) lb = std::max(lb, all_bytes / (model->hbm_gbps_peak * 1e3));
+  // Upper bound: sustained rates, each tile of a CU after the previous, the
+  // MFMA, LDS fill and HBM streams added with no overlap credit.
+  const double c_ub = per_cu * tile_ops / (waves * simd_rate);
+  const double s_ub = per_cu * fill_bytes / model->lds_fill_sustained;
+  const double ub = model->launch_us + (c_ub + s_ub) / model->sclk_mhz_sustained +
+                    all_bytes / (model->hbm_gbps_sustained * 1e3);
+  p.lb_us = lb;
+  p.ub_us = ub;
+  p.p50_us = 0.5 * (lb + ub);
+  return done(HXM_ABSTAIN_NONE);
+}
+
+int32_t hxm_rank_tile_candidates(int64_t M, int64_t N, int64_t K, int32_t ab_dtype,
+                                 int32_t out_dtype, const hxm_gemm_config* cands, int32_t n,
+                                 const hxm_device_model* model, int32_t* order) {
+  if (n <= 0) return 0;
+  if (!cands || !order) return -1;
+  struct Key {
+    int abst;
+    double lb;
+    int64_t spans;
+    std::tuple<int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t> cfg;
+  };
+  std::vector<Key> keys(n);
+  std::vector<int32_t> idx(n);
+  for (int32_t i = 0; i < n; ++i) {
+    const hxm_gemm_config& c = cands[i];
+    hxm_tile_prediction p;
+    const int32_t a = hxm_predict_tile_time(M, N, K, &c, ab_dtype, out_dtype, model, &p);
+    int64_t spans = 0;
+    if (c.bm > 0 && c.bn > 0 && c.bk > 0)
+      spans = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ((K + c.bk - 1) / c.bk);
+    keys[i] = Key{a != HXM_ABSTAIN_NONE ? 1 : 0, a != HXM_ABSTAIN_NONE ? 0.0 : p.lb_us, spans,
+                  std::make_tuple(c.bm, c.bn, c.bk, c.waves_m, c.waves_n, c.stages, c.split_k)};
+    idx[i] = i;
+  }
+  std::stable_sort(idx.begin(), idx.end(), [&](int32_t x, int32_t y) {
+    const Key& a = keys[x];
+    const Key& b = keys[y];
+    return std::tie(a.abst, a.lb, a.spans, a.cfg) < std::tie(b.abst, b.lb, b.spans, b.cfg);
+  });
+  for (int32_t i = 0; i < n; ++i) order[i] = idx[i];
+  return n;
+}
+
+int32_t hxm_cost_prune(const hxm_tile_prediction* preds, const hxm_gemm_config* cands,
+                       int32_t n, int32_t control, const int32_t* vouched, double margin,
+                       double env_lo, double env_hi, int32_t* kept, double* threshold_out) {
+  if (n < 0 || (n > 0 && (!preds || !cands || !kept)) || !(env_lo > 0.0) || !(env_hi > 0.0) ||
+      std::isnan(margin) || margin < 0.0)
+    return -2;
+  const double threshold = (1.0 + margin) * env_hi / env_lo;
+  if (threshold_out) *threshold_out = threshold;
+  auto cfg_key = [&](int32_t i) {
+    const hxm_gemm_config& c = cands[i];
+    return std::make_tuple(c.bm, c.bn, c.bk, c.waves_m, c.waves_n, c.stages, c.split_k);
+  };
+  int32_t champ = -1;
+  for (int32_t i = 0; i < n; ++i) {
+    if (preds[i].abstain != HXM_ABSTAIN_NONE) continue;
+    if (champ < 0 || preds[i].p50_us < preds[champ].p50_us ||
+        (preds[i].p50_us == preds[champ].p50_us && cfg_key(i) < cfg_key(champ)))
+      champ = i;
+  }
+  for (int32_t i = 0; i < n; ++i) {
+    if (champ < 0) kept[i] = 6;
+    else if (i == control) kept[i] = 2;
+    else if (preds[i].abstain != HXM_ABSTAIN_NONE) kept[i] = 3;
+    else if (vouched && !vouched[i]) kept[i] = 4;
+    else if (preds[i].tier != HXM_TIER_CURRENT) kept[i] = 5;
+    else kept[i] = preds[i].lb_us > threshold * preds[champ].ub_us ? 0 : 1;
+  }
+  return champ;
+}
+
 }  // extern "C"

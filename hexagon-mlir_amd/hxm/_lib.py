@@ -49,6 +49,24 @@ class GemmConfig(ctypes.Structure):
                 % self.as_tuple())
 
 
+class DeviceModel(ctypes.Structure):
+    """hxm_device_model: the rates the cost model prices a config with."""
+    _fields_ = [("cus", ctypes.c_int32), ("tier", ctypes.c_int32),
+                ("sclk_mhz_peak", ctypes.c_double), ("sclk_mhz_sustained", ctypes.c_double),
+                ("hbm_gbps_peak", ctypes.c_double), ("hbm_gbps_sustained", ctypes.c_double),
+                ("lds_fill_peak", ctypes.c_double), ("lds_fill_sustained", ctypes.c_double),
+                ("launch_us", ctypes.c_double), ("lds_bytes", ctypes.c_int64),
+                ("cache_bytes", ctypes.c_int64)]
+
+
+class TilePredictionC(ctypes.Structure):
+    """hxm_tile_prediction: one config's modeled interval (microseconds)."""
+    _fields_ = [("lb_us", ctypes.c_double), ("ub_us", ctypes.c_double),
+                ("p50_us", ctypes.c_double), ("units", ctypes.c_int64 * 3),
+                ("abstain", ctypes.c_int32), ("tier", ctypes.c_int32),
+                ("heat", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -109,6 +127,17 @@ SIGNATURES = {
     "hxm_tune_cache_lookup": (_i32, [_i32, _i64, _i64, _i64, _cfgp]),
     "hxm_tune_cache_save": (_st, [ctypes.c_char_p]),
     "hxm_tune_cache_load": (_st, [ctypes.c_char_p, ctypes.POINTER(_i32)]),
+    "hxm_abstain_string": (ctypes.c_char_p, [_i32]),
+    "hxm_device_model_nominal": (None, [ctypes.POINTER(DeviceModel)]),
+    "hxm_device_model_query": (_st, [ctypes.POINTER(DeviceModel)]),
+    "hxm_predict_tile_time": (_i32, [_i64, _i64, _i64, _cfgp, _i32, _i32,
+                                     ctypes.POINTER(DeviceModel),
+                                     ctypes.POINTER(TilePredictionC)]),
+    "hxm_rank_tile_candidates": (_i32, [_i64, _i64, _i64, _i32, _i32, _cfgp, _i32,
+                                        ctypes.POINTER(DeviceModel), ctypes.POINTER(_i32)]),
+    "hxm_cost_prune": (_i32, [ctypes.POINTER(TilePredictionC), _cfgp, _i32, _i32,
+                              ctypes.POINTER(_i32), _f64, _f64, _f64, ctypes.POINTER(_i32),
+                              ctypes.POINTER(_f64)]),
 }
 
 

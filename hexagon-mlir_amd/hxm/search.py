@@ -389,3 +389,224 @@ def tune_cache_load(path: str) -> int:
     n = ctypes.c_int32(0)
     check(lib.hxm_tune_cache_load(str(path).encode(), ctypes.byref(n)), "hxm_tune_cache_load")
     return n.value
+
+
+# ---- modeled cost: ordering and the conservative prune ---------------------
+# hmx_search.predict_tile_pcyc (:778-887), rank_tile_candidates (:1030-1067),
+# cost_prune (:916-1027), manifest_abstains (:895-913).  The arithmetic is C
+# (hxm_predict_tile_time, hxm_rank_tile_candidates, hxm_cost_prune); this
+# layer shapes the reference's records.  Times are microseconds, priced from
+# a device model instead of a table of Hexagon leaf cells; the model's tier
+# ("current" = read from this process's gfx950 device) plays the part of the
+# reference's cell fingerprint tiers.
+
+ABSTAIN_HEAT_BAND = "heat-band"
+ABSTAIN_HEAT_CROSS = "heat-cross-boundary"
+ABSTAIN_TAIL = "tail-blocks"
+ABSTAIN_DTYPE = "dtype-no-cell"
+ABSTAIN_MANIFEST = "manifest-strategy-unknown"
+ABSTAIN_NO_CELL = "no-applicable-cell"
+ABSTAIN_TABLE_MISSING = "table-missing"
+_ABSTAIN_CODE = {None: 0, ABSTAIN_HEAT_BAND: 1, ABSTAIN_HEAT_CROSS: 2, ABSTAIN_TAIL: 3,
+                 ABSTAIN_DTYPE: 4, ABSTAIN_MANIFEST: 5, ABSTAIN_NO_CELL: 6,
+                 ABSTAIN_TABLE_MISSING: 7}
+
+#: The modeled/measured band and the decision margin of the pruning rule
+#: (hmx_search.py:731, :737): drop B only when lb(B) > 1.15 * 1.25/0.70 * ub(A).
+COST_ENVELOPE = (0.70, 1.25)
+PRUNE_MARGIN = 0.15
+
+TIER_UNKNOWN, TIER_CURRENT, TIER_NOMINAL = "unknown", "current", "nominal"
+_TIER = {0: TIER_UNKNOWN, 1: TIER_CURRENT, 2: TIER_NOMINAL}
+_HEAT = {0: "cache", 1: "hbm", -1: "unknown"}
+#: The priced items of one config: MFMA work, the L2 -> LDS fill, HBM bytes.
+MODEL_ITEMS = ("mfma", "lds-fill", "hbm")
+
+#: What a compiled config's "manifest" must say for cost_prune to act on it.
+MANIFEST_VERDICT_OK = REASON_OK
+
+
+class TilePrediction(NamedTuple):
+    """One config's modeled interval (hmx_search.TilePrediction's fields;
+    lb/ub/p50 in microseconds, NaN when abstaining)."""
+    tiles: tuple
+    lb: float
+    ub: float
+    p50: float
+    heat: str
+    units: tuple
+    abstain: Optional[str]
+    table_rev: str
+    lb_tiers: tuple = ()
+
+
+def nominal_model():
+    """The spec-sheet gfx950 device model (tier "nominal": never drives a drop)."""
+    from ._lib import DeviceModel
+    m = DeviceModel()
+    lib.hxm_device_model_nominal(ctypes.byref(m))
+    return m
+
+
+def device_model():
+    """The model of this process's current device (needs a GPU)."""
+    from ._lib import DeviceModel, check
+    m = DeviceModel()
+    check(lib.hxm_device_model_query(ctypes.byref(m)), "hxm_device_model_query")
+    return m
+
+
+def model_rev(model) -> str:
+    """The model's version stamp: its tier and the rates it prices with."""
+    return ("gpu-%s-%dcu-%.0f/%.0fmhz-%.0f/%.0fgbps-lds%.0f/%.0f-launch%.2f"
+            % (_TIER.get(model.tier, TIER_UNKNOWN), model.cus, model.sclk_mhz_peak,
+               model.sclk_mhz_sustained, model.hbm_gbps_peak, model.hbm_gbps_sustained,
+               model.lds_fill_peak, model.lds_fill_sustained, model.launch_us))
+
+
+def tiles_of(candidate) -> tuple:
+    """A candidate's tile tuple: a GemmConfig, an object with ``.tiles`` or a
+    bare tuple."""
+    if isinstance(candidate, GemmConfig):
+        return candidate.as_tuple()
+    return tuple(candidate.tiles if hasattr(candidate, "tiles") else candidate)
+
+
+def _config_of(candidate, dtype: int) -> GemmConfig:
+    if isinstance(candidate, GemmConfig):
+        return candidate
+    t = tiles_of(candidate)
+    if len(t) == 3:  # (BM, BN, BK): the compiled config with those tiles, if any
+        for c in gemm_configs(dtype):
+            if (c.bm, c.bn, c.bk) == t:
+                return c
+    return GemmConfig(*(list(t) + [0] * (7 - len(t)))[:7])
+
+
+def _default_out(dtype: int) -> int:
+    from ._lib import F16, I8, I32
+    return I32 if dtype == I8 else F16
+
+
+def predict_tile_time(m: int, n: int, k: int, config, *, dtype: int = 4,
+                      out_dtype: Optional[int] = None, model=None) -> TilePrediction:
+    """predict_tile_pcyc (hmx_search.py:778-887) for one compiled gfx950 config.
+
+    ``dtype`` is the operand dtype code (``_lib.I8``, ``F16`` or ``BF16``);
+    ``model`` defaults to :func:`nominal_model`."""
+    from ._lib import TilePredictionC
+    model = nominal_model() if model is None else model
+    cfg = _config_of(config, dtype)
+    out = TilePredictionC()
+    od = _default_out(dtype) if out_dtype is None else out_dtype
+    code = lib.hxm_predict_tile_time(int(m), int(n), int(k), ctypes.byref(cfg), int(dtype),
+                                     int(od), ctypes.byref(model), ctypes.byref(out))
+    abstain = None if code == 0 else lib.hxm_abstain_string(int(code)).decode()
+    tier = _TIER.get(out.tier, TIER_UNKNOWN)
+    return TilePrediction(tiles_of(config), out.lb_us, out.ub_us, out.p50_us,
+                          _HEAT.get(out.heat, "unknown"), tuple(out.units), abstain,
+                          model_rev(model), (tier,) * len(MODEL_ITEMS))
+
+
+def rank_tile_candidates(shape, legal, *, dtype: int = 4, out_dtype: Optional[int] = None,
+                         model=None) -> list:
+    """rank_tile_candidates (hmx_search.py:1030-1067): a permutation of
+    ``legal`` by (abstains last, modeled lower bound, span count, config)."""
+    m, n, k = shape
+    legal = list(legal)
+    if not legal:
+        return []
+    model = nominal_model() if model is None else model
+    cfgs = (GemmConfig * len(legal))(*[_config_of(c, dtype) for c in legal])
+    order = (ctypes.c_int32 * len(legal))()
+    od = _default_out(dtype) if out_dtype is None else out_dtype
+    got = lib.hxm_rank_tile_candidates(int(m), int(n), int(k), int(dtype), int(od), cfgs,
+                                       len(legal), ctypes.byref(model), order)
+    assert got == len(legal)
+    return [legal[order[i]] for i in range(len(legal))]
+
+
+def manifest_record(config, dtype: int, lds_budget: int = DEFAULT_LDS_BUDGET) -> dict:
+    """What the compiled-kernel table says about a config: the GPU's manifest."""
+    return {"verdict": gpu_tile_verdict(_config_of(config, dtype), dtype, lds_budget)}
+
+
+def manifest_abstains(record: Optional[Mapping[str, Any]]) -> Optional[str]:
+    """manifest_abstains (hmx_search.py:895-913): a config no manifest vouches
+    for (no record, or a verdict other than "ok") abstains."""
+    if record is None or record.get("verdict") != MANIFEST_VERDICT_OK:
+        return ABSTAIN_MANIFEST
+    return None
+
+
+def cost_prune(candidates, shape, *, control_tile=None, margin: float = PRUNE_MARGIN,
+               envelope: tuple = COST_ENVELOPE, predictions: Optional[Mapping] = None,
+               manifest_records: Optional[Mapping] = None, model=None, dtype: int = 4,
+               out_dtype: Optional[int] = None):
+    """cost_prune (hmx_search.py:916-1027): returns ``(kept, dropped, notes)``;
+    ``kept`` keeps the caller's order, ``dropped`` holds (candidate, reason)."""
+    from ._lib import TilePredictionC
+    m, n, k = shape
+    candidates = list(candidates)
+    if predictions is None:
+        predictions = {tiles_of(c): predict_tile_time(m, n, k, c, dtype=dtype,
+                                                      out_dtype=out_dtype, model=model)
+                       for c in candidates}
+    count = len(candidates)
+    preds = (TilePredictionC * max(1, count))()
+    cfgs = (GemmConfig * max(1, count))()
+    vouched = (ctypes.c_int32 * max(1, count))()
+    control_tiles = tiles_of(control_tile) if control_tile is not None else None
+    control = -1
+    for i, cand in enumerate(candidates):
+        t = tiles_of(cand)
+        p = predictions[t]
+        preds[i].lb_us, preds[i].ub_us, preds[i].p50_us = _f(p.lb), _f(p.ub), _f(p.p50)
+        preds[i].abstain = _ABSTAIN_CODE.get(p.abstain, _ABSTAIN_CODE[ABSTAIN_NO_CELL])
+        preds[i].tier = 1 if not any(tr != TIER_CURRENT for tr in p.lb_tiers) else 0
+        cfgs[i] = GemmConfig(*(list(t) + [0] * 7)[:7])
+        if manifest_records is not None:
+            vouched[i] = 1 if manifest_abstains(manifest_records.get(t)) is None else 0
+        if control < 0 and control_tiles is not None and t == control_tiles:
+            control = i
+    lo, hi = envelope
+    kept_code = (ctypes.c_int32 * max(1, count))()
+    threshold = ctypes.c_double(0.0)
+    champ = lib.hxm_cost_prune(preds, cfgs, count, control,
+                               vouched if manifest_records is not None else None,
+                               float(margin), float(lo), float(hi), kept_code,
+                               ctypes.byref(threshold))
+    if champ == -2:
+        raise ValueError("cost_prune: invalid margin or envelope")
+    if champ < 0:
+        return list(candidates), [], [
+            "cost_prune: no priced candidate -- nothing compared, nothing dropped"]
+    ch_t = tiles_of(candidates[champ])
+    ch = predictions[ch_t]
+    thr = threshold.value
+    kept, dropped = [], []
+    notes = [f"cost_prune: champion {ch_t} p50={ch.p50:.3f} lb={ch.lb:.3f} ub={ch.ub:.3f}; "
+             f"drop when lb(B) > {thr:.3f} * ub(A)"]
+    for i, cand in enumerate(candidates):
+        t = tiles_of(cand)
+        p = predictions[t]
+        code = kept_code[i]
+        if code == 0:
+            dropped.append((cand, dict(tiles=list(t), lb=p.lb, ub=p.ub,
+                                       champion_tiles=list(ch_t), champion_ub=ch.ub,
+                                       ratio=p.lb / ch.ub, threshold=thr, margin=margin,
+                                       envelope=list(envelope), table_rev=p.table_rev)))
+            continue
+        kept.append(cand)
+        if code == 2:
+            notes.append(f"cost_prune: {t} kept (control tile is the arm the winner is "
+                         "judged against)")
+        elif code == 3:
+            notes.append(f"cost_prune: {t} kept (abstain {p.abstain})")
+        elif code == 4:
+            notes.append(f"cost_prune: {t} kept (abstain {ABSTAIN_MANIFEST})")
+        elif code == 5:
+            notes.append(f"cost_prune: {t} kept (lower bound rests on {p.lb_tiers} prices: "
+                         "only a current-device model may drive a drop)")
+    notes.append(f"cost_prune: kept {len(kept)}, dropped {len(dropped)}")
+    return kept, dropped, notes

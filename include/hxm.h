@@ -444,6 +444,99 @@ int32_t hxm_tune_cache_lookup(int32_t op, int64_t M, int64_t N, int64_t K,
 hxm_status hxm_tune_cache_save(const char* path);
 hxm_status hxm_tune_cache_load(const char* path, int32_t* loaded);
 
+/* ---- modeled cost: ordering and the conservative prune ------------------
+ * hmx_search.predict_tile_pcyc (hmx_search.py:778-887), rank_tile_candidates
+ * (:1030-1067) and cost_prune (:916-1027).  The reference prices a tile from
+ * a table of measured Hexagon leaf costs qualified by a runtime fingerprint;
+ * here a GEMM config is priced from the device's own rates (MFMA ops per
+ * clock, LDS fill bytes per clock, HBM bytes per second, launch cost), and
+ * the model's tier plays the fingerprint's part: only a model read from the
+ * device this process runs on (HXM_TIER_CURRENT) may drive a drop. */
+enum { HXM_TIER_UNKNOWN = 0, HXM_TIER_CURRENT = 1, HXM_TIER_NOMINAL = 2 };
+
+typedef struct hxm_device_model {
+  int32_t cus;               /* compute units */
+  int32_t tier;              /* HXM_TIER_* */
+  double sclk_mhz_peak;      /* lower bound: MFMA and LDS fill at this clock */
+  double sclk_mhz_sustained; /* upper bound: the clock under sustained load */
+  double hbm_gbps_peak;      /* lower bound: HBM bytes at this rate */
+  double hbm_gbps_sustained; /* upper bound */
+  double lds_fill_peak;      /* bytes per clock per CU into LDS, lower bound */
+  double lds_fill_sustained; /* bytes per clock per CU into LDS, upper bound */
+  double launch_us;          /* launch cost, charged to the upper bound only */
+  int64_t lds_bytes;         /* LDS per CU */
+  int64_t cache_bytes;       /* last-level (Infinity) cache */
+} hxm_device_model;
+
+/* Abstain classes, tested in this order: dtype, model missing, tail blocks,
+ * heat band, heat cross-boundary, no price (hmx_search.py:844-866).
+ * MANIFEST is cost_prune's own class (hmx_search.py:895-913). */
+enum {
+  HXM_ABSTAIN_NONE = 0,
+  HXM_ABSTAIN_HEAT_BAND = 1,     /* "heat-band" */
+  HXM_ABSTAIN_HEAT_CROSS = 2,    /* "heat-cross-boundary" */
+  HXM_ABSTAIN_TAIL = 3,          /* "tail-blocks" */
+  HXM_ABSTAIN_DTYPE = 4,         /* "dtype-no-cell" */
+  HXM_ABSTAIN_MANIFEST = 5,      /* "manifest-strategy-unknown" */
+  HXM_ABSTAIN_NO_CELL = 6,       /* "no-applicable-cell" */
+  HXM_ABSTAIN_TABLE_MISSING = 7  /* "table-missing" */
+};
+
+typedef struct hxm_tile_prediction {
+  double lb_us, ub_us, p50_us; /* NaN when abstaining; p50 = (lb + ub) / 2 */
+  int64_t units[3];            /* tiles, tiles per CU, K stages per tile */
+  int32_t abstain;             /* HXM_ABSTAIN_* */
+  int32_t tier;                /* the model's tier */
+  int32_t heat;                /* 0 cache-resident, 1 HBM, -1 not classified */
+  int32_t reserved;
+} hxm_tile_prediction;
+
+/* Abstain code -> the reference's vocabulary string. */
+const char* hxm_abstain_string(int32_t abstain);
+
+/* The spec-sheet gfx950 model (tier HXM_TIER_NOMINAL): 256 CUs, 2.4 GHz peak
+ * and 1.4 GHz sustained clock, 8.0 / 5.0 TB/s HBM, 128 / 48 bytes per clock
+ * LDS fill, 2.5 us launch, 160 KiB LDS, 256 MiB Infinity Cache. */
+void hxm_device_model_nominal(hxm_device_model* out);
+
+/* The model of the current device: CUs, peak clock and LDS size read from
+ * it, the other rates from the nominal model; tier HXM_TIER_CURRENT on a
+ * gfx950 device, HXM_TIER_UNKNOWN on any other. */
+hxm_status hxm_device_model_query(hxm_device_model* out);
+
+/* Modeled time interval of one compiled config for C[M,N] = A[M,K] B[K,N]
+ * (ab_dtype HXM_I8 / HXM_F16 / HXM_BF16; out_dtype HXM_I32, HXM_F16,
+ * HXM_BF16 or HXM_F32 sizes the C stream).  Lower bound: the largest of the
+ * MFMA floor, the LDS fill floor and (HBM heat only) the HBM floor at peak
+ * rates.  Upper bound: launch + MFMA + LDS fill + HBM at sustained rates, no
+ * overlap credit.  Writes *out and returns out->abstain. */
+int32_t hxm_predict_tile_time(int64_t M, int64_t N, int64_t K,
+                              const hxm_gemm_config* cfg, int32_t ab_dtype,
+                              int32_t out_dtype, const hxm_device_model* model,
+                              hxm_tile_prediction* out);
+
+/* rank_tile_candidates: order[] receives a permutation of 0..n-1 sorted by
+ * (abstains last, lower bound, span count, config fields).  Returns n, or -1
+ * on a NULL array with n > 0. */
+int32_t hxm_rank_tile_candidates(int64_t M, int64_t N, int64_t K,
+                                 int32_t ab_dtype, int32_t out_dtype,
+                                 const hxm_gemm_config* cands, int32_t n,
+                                 const hxm_device_model* model, int32_t* order);
+
+/* cost_prune over given predictions: the champion A is the priced candidate
+ * with the lowest p50 (ties: config fields); candidate B is dropped only when
+ * lb(B) > (1 + margin) * env_hi / env_lo * ub(A).  kept[i] receives 0
+ * dropped, 1 kept inside the band, 2 kept as the control (index `control`,
+ * -1 for none), 3 kept abstaining, 4 kept because vouched[i] == 0 (vouched
+ * may be NULL: no manifest consulted), 5 kept because its tier is not
+ * HXM_TIER_CURRENT, 6 kept because nothing is priced.  *threshold_out (may
+ * be NULL) receives the factor.  Returns the champion's index, -1 when
+ * nothing is priced, -2 on invalid arguments. */
+int32_t hxm_cost_prune(const hxm_tile_prediction* preds,
+                       const hxm_gemm_config* cands, int32_t n, int32_t control,
+                       const int32_t* vouched, double margin, double env_lo,
+                       double env_hi, int32_t* kept, double* threshold_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -80,3 +80,42 @@ def test_tune_cache_save_load_round_trip(dev, tmp_path):
     C = ops.gemm_i8(A, B, b_layout="nk").cpu().numpy()     # runs the reloaded winner
     assert np.array_equal(C, orc.gemm_i8(A.cpu().numpy(), B.cpu().numpy(), b_nk=True))
     hxm.lib.hxm_tune_cache_clear()
+
+
+def test_cost_model_floor_holds_and_prune_keeps_the_measured_winner(dev):
+    """predict_tile_pcyc / cost_prune (hmx_search.py:778-1027) priced by this
+    device: every measured config time is at or above its modeled lower bound,
+    and the conservative prune never drops the config measured fastest."""
+    from hxm import search as S
+    from hxm._lib import I8, I32
+    model = S.device_model()
+    assert model.tier == 1 and model.cus > 0 and model.sclk_mhz_peak > 0
+    M = N = K = 4096
+    g = torch.Generator().manual_seed(11)
+    A = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
+    B = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+    out = torch.empty(M, N, dtype=torch.int32, device=dev)
+    _, rep = ops.tune_gemm(A, B, out, reps=5)
+    assert rep["unit"] == "us"
+    measured = {}
+    for c in rep["configs"]:
+        if c["q50"] is None or not c["verified"]:
+            continue
+        t = tuple(c["tiles"][:3])
+        cfg = next(x for x in S.gemm_configs(I8) if (x.bm, x.bn, x.bk) == t
+                   and x.stages == c["stages"])
+        measured[cfg.as_tuple()] = (cfg, c["q50"])
+    assert len(measured) >= 3
+    preds = {}
+    for key, (cfg, q50) in measured.items():
+        p = S.predict_tile_time(M, N, K, cfg, dtype=I8, out_dtype=I32, model=model)
+        assert p.abstain is None, (key, p.abstain)
+        print(f"{key}: measured {q50:.1f} us, model lb {p.lb:.1f} p50 {p.p50:.1f} "
+              f"ub {p.ub:.1f}", flush=True)
+        assert q50 >= p.lb, (key, q50, p.lb)
+        preds[key] = p
+    cands = [cfg for cfg, _ in measured.values()]
+    kept, dropped, notes = S.cost_prune(cands, (M, N, K), predictions=preds)
+    print(notes, flush=True)
+    fastest = min(measured.values(), key=lambda v: v[1])[0]
+    assert fastest.as_tuple() in [c.as_tuple() for c in kept]

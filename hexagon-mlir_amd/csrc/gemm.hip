@@ -74,6 +74,11 @@ hxm_gemm_config kernel_config(int i, int32_t dt) {
   return c;
 }
 
+// K splits an int8 GEMM may take (grid rows along K, exact int32 partials).
+static bool valid_split(int32_t s, int32_t dt) {
+  return s == 0 || s == 1 || (dt == HXM_I8 && (s == 2 || s == 4 || s == 8 || s == 16));
+}
+
 // A config matches when every non-zero field agrees (0 = any).
 const KernelEntry* find_kernel(const hxm_gemm_config& c, int32_t dt) {
   for (int i = 0; i < kNumKernels; ++i) {
@@ -81,7 +86,7 @@ const KernelEntry* find_kernel(const hxm_gemm_config& c, int32_t dt) {
     if (k.bm == c.bm && k.bn == c.bn && (c.bk == 0 || c.bk == k.bk) &&
         (c.waves_m == 0 || c.waves_m == k.waves_m) &&
         (c.waves_n == 0 || c.waves_n == k.waves_n) &&
-        (c.stages == 0 || c.stages == k.stages) && (c.split_k == 0 || c.split_k == 1))
+        (c.stages == 0 || c.stages == k.stages) && valid_split(c.split_k, dt))
       return &kKernels[i];
   }
   return nullptr;
@@ -115,16 +120,38 @@ hxm_status launch_gemm(const KernelEntry& e, int32_t ab_dtype, int epi,
   const int bm = e.cfg.bm, bn = e.cfg.bn;
   const int64_t tiles = static_cast<int64_t>((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
   const int i = static_cast<int>(&e - kKernels);
-  hxm_status st = check_grid("gemm", tiles, e.threads);
+  hxm_status st = check_grid("gemm", tiles, e.threads, g.split);
   if (st != HXM_OK) return st;
   gemm_fn fn = nullptr;
   if (ab_dtype == HXM_I8)
     fn = part_fn(kI8Parts, i, epi == kEpiDequant ? 1 : 0);
   else
     fn = part_fn(kF16Parts, i, ab_dtype == HXM_F16 ? 0 : 1);
-  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(tiles)), dim3(e.threads), 0,
-                     stream, g);
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(g.split)),
+                     dim3(e.threads), 0, stream, g);
   return check_launch("gemm kernel");
+}
+
+// Split-K read-out: sums the S int32 partial planes ([S, M, N], plane order,
+// exact in int32 like the unsplit accumulator) and applies the int8 GEMM's
+// epilogue: int32 out (C += sum when accumulating) or the dequant
+// f16(((float)sum * rs[m]) * cs[n]), each product rounded to fp32.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(
+    const int32_t* __restrict__ planes, int S, int64_t plane, int N, void* C, int64_t ldc,
+    int dequant, int accumulate, const float* __restrict__ rs, const float* __restrict__ cs) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= plane) return;
+  const int64_t m = i / N, n = i % N;
+  uint32_t s = 0;
+  for (int z = 0; z < S; ++z) s += static_cast<uint32_t>(planes[z * plane + i]);
+  if (dequant) {
+    float p = (static_cast<float>(static_cast<int32_t>(s)) * rs[m]) * cs[n];
+    asm volatile("" : "+v"(p));  // one rounding to fp32, then one to f16
+    static_cast<_Float16*>(C)[m * ldc + n] = static_cast<_Float16>(p);
+  } else {
+    int32_t* c = static_cast<int32_t*>(C) + m * ldc + n;
+    *c = static_cast<int32_t>(accumulate ? static_cast<uint32_t>(*c) + s : s);
+  }
 }
 
 namespace {
@@ -214,7 +241,7 @@ hxm_status resolve_b(const void* B, int64_t ldb, int32_t b_layout, int64_t K,
 
 hxm_status pick_kernel(int32_t op, int32_t ab_dtype, int64_t M, int64_t N,
                        int64_t K, const hxm_gemm_config* cfg,
-                       const KernelEntry** out) {
+                       const KernelEntry** out, int* split_out) {
   hxm_gemm_config c;
   if (cfg && cfg->bm) {
     c = *cfg;
@@ -227,6 +254,7 @@ hxm_status pick_kernel(int32_t op, int32_t ab_dtype, int64_t M, int64_t N,
                 "no-kernel: no compiled GEMM for bm=%d bn=%d bk=%d waves=%dx%d split_k=%d",
                 c.bm, c.bn, c.bk, c.waves_m, c.waves_n, c.split_k);
   *out = e;
+  *split_out = c.split_k > 1 ? c.split_k : 1;
   return HXM_OK;
 }
 
@@ -241,8 +269,11 @@ hxm_status run_gemm(int32_t op, int32_t ab_dtype, int epi, const void* A,
                     hipStream_t stream) {
   const int64_t eb = dtype_bytes(ab_dtype);
   const KernelEntry* e = nullptr;
-  hxm_status st = pick_kernel(op, ab_dtype, M, N, K, cfg, &e);
+  int split = 1;
+  hxm_status st = pick_kernel(op, ab_dtype, M, N, K, cfg, &e, &split);
   if (st != HXM_OK) return st;
+  if (split > 1 && ab_dtype != HXM_I8)
+    return fail(HXM_UNSUPPORTED_SHAPE, "no-kernel: split-K is compiled for int8 only");
   if ((st = require_device(nullptr)) != HXM_OK) return st;
   if (M == 0 || N == 0) return ok();
   const uint8_t* bk = nullptr;
@@ -272,6 +303,39 @@ hxm_status run_gemm(int32_t op, int32_t ab_dtype, int epi, const void* A,
     const int64_t ob = dtype_bytes(out_dtype);
     g.vec_store = (reinterpret_cast<uintptr_t>(C) % (4 * ob) == 0) && ((ldc * ob) % (4 * ob) == 0);
     g.vec8_store = (reinterpret_cast<uintptr_t>(C) % 16 == 0) && ((ldc * ob) % 16 == 0);
+  }
+  if (split > 1 && K > 0) {
+    // K in S slices of whole stages; workgroup row z writes int32 plane z of
+    // a library-owned [S, M, N] buffer, then one pass sums the planes.
+    const int64_t bkb = e->cfg.bk;  // stage bytes
+    const int64_t per = ((K * eb + bkb - 1) / bkb + split - 1) / split;
+    const int64_t kslice = per * bkb;
+    const int S = static_cast<int>((K * eb + kslice - 1) / kslice);
+    if (S > 1) {
+      const int64_t plane = M * N;
+      void* ws = nullptr;
+      if ((st = stream_workspace(stream, static_cast<size_t>(S * plane * 4), &ws, kWsSplitK)) !=
+          HXM_OK)
+        return st;
+      GemmArgs p = g;
+      p.C = ws;
+      p.ldc = N;
+      p.out_dtype = HXM_I32;
+      p.accumulate = 0;
+      p.row_scale = p.col_scale = nullptr;
+      p.vec_store = (N * 4) % 16 == 0;
+      p.vec8_store = (N * 4) % 16 == 0;
+      p.split = S;
+      p.kslice_bytes = static_cast<int>(kslice);
+      p.plane_elems = plane;
+      if ((st = launch_gemm(*e, ab_dtype, kEpiI32, p, stream)) != HXM_OK) return st;
+      const int64_t blocks = (plane + 255) / 256;
+      if ((st = check_grid("splitk_reduce", blocks, 256)) != HXM_OK) return st;
+      splitk_reduce_kernel<<<static_cast<unsigned>(blocks), 256, 0, stream>>>(
+          static_cast<const int32_t*>(ws), S, plane, static_cast<int>(N), C, ldc,
+          epi == kEpiDequant, accumulate, rs, cs);
+      return check_launch("splitk_reduce");
+    }
   }
   if ((st = launch_gemm(*e, ab_dtype, epi, g, stream)) != HXM_OK) return st;
   return ok();

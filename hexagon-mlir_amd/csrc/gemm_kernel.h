@@ -105,6 +105,11 @@ struct GemmArgs {
   const _Float16* residual;  // kEpiW8Res: r [M, N] f16, row stride ldr
   int64_t ldr;
   int res_vec8;  // r rows allow 16-byte loads
+  // K split over blockIdx.y: workgroup row z takes A/B bytes [z * kslice_bytes,
+  // +kslice_bytes) of K and writes its own C plane at z * plane_elems.
+  int split = 1;
+  int kslice_bytes = 0;
+  int64_t plane_elems = 0;
 };
 
 template <typename T>
@@ -306,6 +311,16 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform
   const int wm = wave / WN, wn = wave % WN;
+
+  if (g.split > 1) {  // uniform: this workgroup's K slice and C plane
+    const int z = blockIdx.y;
+    const int kb0 = z * g.kslice_bytes;  // a multiple of BKB (host)
+    g.A += kb0;
+    g.B += BQ ? kb0 / 2 : kb0;
+    g.K_bytes = min(g.kslice_bytes, g.K_bytes - kb0);
+    g.C = static_cast<char*>(g.C) +
+          static_cast<int64_t>(z) * g.plane_elems * (g.out_dtype == HXM_I32 || g.out_dtype == HXM_F32 ? 4 : 2);
+  }
 
   // ---- XCD-aware tile order ----
   const int tiles_m = (g.M + BM - 1) / BM;

@@ -54,10 +54,13 @@ hxm_status check_launch(const char* what);
 // HXM_NO_DEVICE with a reason.
 hxm_status require_device(int* device_out);
 
-// Library-owned scratch for one (device, stream) pair, grown on demand and
+// Library-owned scratch for one (device, stream, slot), grown on demand and
 // kept until hxm_release_cache().  Calls on the same stream are ordered, so
-// one buffer per stream never races with itself.
-hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out);
+// one buffer per stream never races with itself.  Slot 0 holds per-call
+// operand packs and the tuner's reference output; slot 1 the split-K
+// partial planes, so the two never overwrite or reallocate each other.
+constexpr int kWsMain = 0, kWsSplitK = 1;
+hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out, int slot = kWsMain);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

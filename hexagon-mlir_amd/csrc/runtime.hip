@@ -18,7 +18,8 @@ struct Workspace {
   size_t bytes = 0;
 };
 std::mutex g_ws_mu;
-// key: (device << 48) ^ stream pointer
+// key: ((device << 48) ^ stream pointer) | slot (stream objects are at least
+// 8-byte aligned, so the slot bit does not collide)
 std::unordered_map<uint64_t, Workspace> g_ws;
 
 std::mutex g_dev_mu;
@@ -76,11 +77,12 @@ hxm_status require_device(int* device_out) {
   return HXM_OK;
 }
 
-hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out) {
+hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out, int slot) {
   int dev = 0;
   HXM_HIP_TRY(hipGetDevice(&dev));
-  const uint64_t key = (static_cast<uint64_t>(dev) << 48) ^
-                       reinterpret_cast<uint64_t>(stream);
+  const uint64_t key = ((static_cast<uint64_t>(dev) << 48) ^
+                        reinterpret_cast<uint64_t>(stream)) |
+                       static_cast<uint64_t>(slot & 1);
   std::lock_guard<std::mutex> lk(g_ws_mu);
   Workspace& w = g_ws[key];
   if (w.bytes < bytes) {

@@ -127,8 +127,11 @@ bool same_config(const hxm_gemm_config& a, const hxm_gemm_config& b) {
 // True when this build compiled `c` for `op`.
 bool config_compiled(int32_t op, const hxm_gemm_config& c) {
   if (op == HXM_I8 || op == HXM_F16 || op == HXM_BF16) {
+    hxm_gemm_config base = c;
+    if (op == HXM_I8 && (c.split_k == 2 || c.split_k == 4 || c.split_k == 8 || c.split_k == 16))
+      base.split_k = 1;  // K splits are a launch parameter of the int8 kernels
     for (int i = 0; i < num_kernels(); ++i)
-      if (same_config(kernel_config(i, op), c)) return true;
+      if (same_config(kernel_config(i, op), base)) return true;
   } else if (op == HXM_OP_W8A16 || op == HXM_OP_W8A16_SWIGLU) {
     for (int i = 0; i < num_w8_kernels(); ++i)
       if (same_config(w8_kernel_config(i), c) &&
@@ -184,8 +187,8 @@ struct TuneSpec {
 
 void sort_configs(std::vector<hxm_gemm_config>* v) {
   std::sort(v->begin(), v->end(), [](const hxm_gemm_config& a, const hxm_gemm_config& b) {
-    return std::make_tuple(a.bm, a.bn, a.bk, a.waves_m, a.waves_n, a.stages) <
-           std::make_tuple(b.bm, b.bn, b.bk, b.waves_m, b.waves_n, b.stages);
+    return std::make_tuple(a.bm, a.bn, a.bk, a.waves_m, a.waves_n, a.stages, a.split_k) <
+           std::make_tuple(b.bm, b.bn, b.bk, b.waves_m, b.waves_n, b.stages, b.split_k);
   });
 }
 
@@ -327,7 +330,8 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
       r += std::string(i ? "," : "") + "{\"tiles\":[" + std::to_string(c.bm) + "," +
            std::to_string(c.bn) + "," + std::to_string(c.bk) + "],\"waves\":[" +
            std::to_string(c.waves_m) + "," + std::to_string(c.waves_n) +
-           "],\"stages\":" + std::to_string(c.stages) + ",\"q20\":" + num(q20[i]) + ",\"q50\":" + num(q50[i]) + ",\"q80\":" +
+           "],\"stages\":" + std::to_string(c.stages) +
+           ",\"split_k\":" + std::to_string(c.split_k > 1 ? c.split_k : 1) + ",\"q20\":" + num(q20[i]) + ",\"q50\":" + num(q50[i]) + ",\"q80\":" +
            num(q80[i]) + ",\"verified\":" + (verified[i] ? "true" : "false") +
            ",\"outcome\":\"" +
            (outcome[i] == 1 ? "takeover" : outcome[i] == 0 ? "kept" : "-") +
@@ -414,7 +418,9 @@ int32_t hxm_gpu_tile_verdict(const hxm_gemm_config* cfg, int32_t ab_dtype,
     if (k.bm == cfg->bm && k.bn == cfg->bn && k.bk == cfg->bk &&
         k.waves_m == cfg->waves_m && k.waves_n == cfg->waves_n &&
         (cfg->stages == 0 || cfg->stages == k.stages) &&
-        (cfg->split_k == 0 || cfg->split_k == 1))
+        (cfg->split_k == 0 || cfg->split_k == 1 ||
+         (ab_dtype == HXM_I8 && (cfg->split_k == 2 || cfg->split_k == 4 ||
+                                 cfg->split_k == 8 || cfg->split_k == 16))))
       return HXM_REASON_OK;
   }
   return HXM_REASON_NO_KERNEL;
@@ -652,7 +658,21 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
   sp.M = M, sp.N = N, sp.K = K;
   for (int i = 0; i < num_kernels(); ++i) {
     hxm_gemm_config c = kernel_config(i, op);
-    if (hxm_gpu_tile_verdict(&c, op, 0) == HXM_REASON_OK) sp.cands.push_back(c);
+    if (hxm_gpu_tile_verdict(&c, op, 0) != HXM_REASON_OK) continue;
+    sp.cands.push_back(c);
+    // int8 tiles that leave CUs idle also run with K split over enough
+    // workgroup rows to cover every CU (up to 16, at least one stage each).
+    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+    const int cus = device_cus();
+    if (op == HXM_I8 && cus > 0 && tiles * 2 <= cus) {
+      int32_t s = 2;
+      while (s < 16 && tiles * s < cus) s *= 2;
+      if ((K + c.bk - 1) / c.bk >= s) {
+        hxm_gemm_config sc = c;
+        sc.split_k = s;
+        sp.cands.push_back(sc);
+      }
+    }
   }
   sort_configs(&sp.cands);
   sp.control = default_config(M, N, op);
@@ -828,7 +848,10 @@ int32_t hxm_predict_tile_time(int64_t M, int64_t N, int64_t K, const hxm_gemm_co
 
   const int64_t bm = cfg->bm, bn = cfg->bn, bk = cfg->bk;
   const int64_t stages = cfg->stages > 0 ? cfg->stages : 2;
-  const int64_t tiles = (M / bm) * (N / bn);
+  // A K split runs S workgroups per tile on K/S each, and its int32 partial
+  // planes are written and read back once (a second launch sums them).
+  const int64_t S = cfg->split_k > 1 ? cfg->split_k : 1;
+  const int64_t tiles = (M / bm) * (N / bn) * S;
   const int64_t per_cu = (tiles + model->cus - 1) / model->cus;
   p.units[0] = tiles;
   p.units[1] = per_cu;
@@ -837,21 +860,23 @@ int32_t hxm_predict_tile_time(int64_t M, int64_t N, int64_t K, const hxm_gemm_co
   const double simd_rate = eb == 1 ? 2048.0 : 1024.0;
   const double waves = std::min<int64_t>(4, static_cast<int64_t>(cfg->waves_m) * cfg->waves_n);
   const int64_t wg_lds = std::max<int64_t>(1, model->lds_bytes / (stages * (bm + bn) * bk * eb));
-  const double tile_ops = 2.0 * bm * bn * K;
-  const double fill_bytes = static_cast<double>(bm + bn) * K * eb;  // L2 -> LDS per tile
+  const double tile_ops = 2.0 * bm * bn * K / S;
+  const double fill_bytes = static_cast<double>(bm + bn) * K * eb / S;  // L2 -> LDS per tile
+  const double split_bytes = S > 1 ? 2.0 * S * static_cast<double>(M) * N * 4 : 0.0;
   // Lower bound: the busiest CU's share at peak rates, perfect overlap.
   const double c_all = per_cu * tile_ops / (4.0 * simd_rate);
   const double c_conc =
       static_cast<double>((per_cu + wg_lds - 1) / wg_lds) * tile_ops / (waves * simd_rate);
   const double s_lb = per_cu * fill_bytes / model->lds_fill_peak;
   double lb = std::max(std::max(c_all, c_conc), s_lb) / model->sclk_mhz_peak;  // cycles/MHz = us
-  if (p.heat == 1) lb = std::max(lb, all_bytes / (model->hbm_gbps_peak * 1e3));
+  if (p.heat == 1) lb = std::max(lb, (all_bytes + split_bytes) / (model->hbm_gbps_peak * 1e3));
   // Upper bound: sustained rates, each tile of a CU after the previous, the
   // MFMA, LDS fill and HBM streams added with no overlap credit.
   const double c_ub = per_cu * tile_ops / (waves * simd_rate);
   const double s_ub = per_cu * fill_bytes / model->lds_fill_sustained;
-  const double ub = model->launch_us + (c_ub + s_ub) / model->sclk_mhz_sustained +
-                    all_bytes / (model->hbm_gbps_sustained * 1e3);
+  const double ub = model->launch_us * (S > 1 ? 2 : 1) +
+                    (c_ub + s_ub) / model->sclk_mhz_sustained +
+                    (all_bytes + split_bytes) / (model->hbm_gbps_sustained * 1e3);
   p.lb_us = lb;
   p.ub_us = ub;
   p.p50_us = 0.5 * (lb + ub);

@@ -236,3 +236,23 @@ def test_live_prune_on_the_nominal_model_drops_nothing_and_a_current_one_may():
     preds = [S.predict_tile_time(*shape, c, dtype=I8) for c in legal]
     best = min(range(len(legal)), key=lambda i: (preds[i].p50, legal[i].as_tuple()))
     assert legal[best] in kept
+
+
+def test_split_k_configs_are_legal_for_int8_only_and_priced_per_slice():
+    base = S.gemm_configs(I8)[0]
+    t = list(base.as_tuple())
+    for s, want in [(2, "ok"), (4, "ok"), (16, "ok"), (3, "no-kernel"), (32, "no-kernel")]:
+        t[6] = s
+        assert S.gpu_tile_verdict(GemmConfig(*t), I8) == want, s
+    f = list(S.gemm_configs(F16)[0].as_tuple())
+    f[6] = 2
+    assert S.gpu_tile_verdict(GemmConfig(*f), F16) == "no-kernel"
+    # 512^2 x 16384: 4 tiles of 256^2 leave 252 CUs idle; a 16-way K split
+    # fills 64 of them, so its floor is 16x lower
+    t[6] = 1
+    one = S.predict_tile_time(512, 512, 16384, GemmConfig(*t), dtype=I8)
+    t[6] = 16
+    sixteen = S.predict_tile_time(512, 512, 16384, GemmConfig(*t), dtype=I8)
+    assert one.abstain is None and sixteen.abstain is None
+    assert one.units == (4, 1, 128) and sixteen.units == (64, 1, 128)
+    assert sixteen.lb == pytest.approx(one.lb / 16, rel=1e-12)

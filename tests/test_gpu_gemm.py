@@ -265,3 +265,59 @@ def test_refuses_misaligned_k(dev):
     B = torch.zeros(24, 8, dtype=torch.int8, device=dev)
     with pytest.raises(hxm.HxmError, match="tile-alignment"):
         ops.gemm_i8(A, B)
+
+
+def _split(cfg, s):
+    t = list(cfg.as_tuple())
+    t[6] = s
+    return hxm.GemmConfig(*t)
+
+
+@pytest.mark.parametrize("split", [2, 4, 16])
+@pytest.mark.parametrize("cfg", S.gemm_configs(hxm.I8), ids=repr)
+def test_gemm_i8_split_k_bit_exact(dev, cfg, split):
+    """K split over workgroup rows: int32 partial planes summed in plane order
+    are exact, so every split equals the oracle bit for bit -- with K not a
+    multiple of the slice (a short last slice) and with fewer stages than
+    splits (fewer, non-empty slices)."""
+    for M, N, K in [(300, 260, 4112), (64, 96, 640), (40, 33 * 8, 16 * 9)]:
+        print(f"gemm_i8 split_k={split} config {cfg} M={M} N={N} K={K}", flush=True)
+        A = rand_i8((M, K), 41)
+        B = rand_i8((N, K), 42)
+        C = ops.gemm_i8(A.to(dev), B.to(dev), b_layout="nk", config=_split(cfg, split))
+        assert np.array_equal(C.cpu().numpy(), orc.gemm_i8(A.numpy(), B.numpy(), b_nk=True))
+
+
+def test_gemm_i8_split_k_accumulate_dequant_and_layout(dev):
+    M, N, K = 200, 264, 2048
+    A = rand_i8((M, K), 51)
+    B = rand_i8((N, K), 52)
+    acc = orc.gemm_i8(A.numpy(), B.numpy(), b_nk=True)
+    cfg = _split(S.gemm_configs(hxm.I8)[0], 8)
+    print(f"gemm_i8 split_k accumulate/dequant/kn {cfg}", flush=True)
+    # accumulate into a strided int32 view: C += A.B
+    base = torch.randint(-1000, 1000, (M, N + 8), dtype=torch.int32)
+    Cd = base.clone().to(dev)
+    ops.gemm_i8(A.to(dev), B.to(dev), Cd[:, :N], b_layout="nk", accumulate=True, config=cfg)
+    got = Cd.cpu().numpy()
+    assert np.array_equal(got[:, :N], base.numpy()[:, :N] + acc)
+    assert np.array_equal(got[:, N:], base.numpy()[:, N:])
+    # dequant epilogue, same spelling as the unsplit kernel
+    g = torch.Generator().manual_seed(53)
+    rs = (torch.rand(M, generator=g) * 0.019 + 0.001).float()
+    cs = (torch.rand(N, generator=g) * 0.019 + 0.001).float()
+    D = ops.gemm_i8_dequant(A.to(dev), B.to(dev), rs.to(dev), cs.to(dev), b_layout="nk",
+                            config=cfg)
+    assert np.array_equal(bits(D), orc.dequant_f16(acc, rs.numpy(), cs.numpy()))
+    # B as a plain [K, N] operand (packed per call into the other workspace slot)
+    Bkn = B.t().contiguous()
+    C = ops.gemm_i8(A.to(dev), Bkn.to(dev), b_layout="kn", config=cfg)
+    assert np.array_equal(C.cpu().numpy(), acc)
+
+
+def test_split_k_is_int8_only(dev):
+    A = torch.zeros(64, 64, dtype=torch.float16, device=dev)
+    B = torch.zeros(64, 64, dtype=torch.float16, device=dev)
+    cfg = _split(S.gemm_configs(hxm.F16)[0], 2)
+    with pytest.raises(hxm.HxmError):
+        ops.matmul(A, B, b_layout="nk", config=cfg)

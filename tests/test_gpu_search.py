@@ -104,6 +104,7 @@ def test_cost_model_floor_holds_and_prune_keeps_the_measured_winner(dev):
         t = tuple(c["tiles"][:3])
         cfg = next(x for x in S.gemm_configs(I8) if (x.bm, x.bn, x.bk) == t
                    and x.stages == c["stages"])
+        cfg.split_k = c["split_k"]
         measured[cfg.as_tuple()] = (cfg, c["q50"])
     assert len(measured) >= 3
     preds = {}

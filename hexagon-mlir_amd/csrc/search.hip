@@ -660,14 +660,15 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
     hxm_gemm_config c = kernel_config(i, op);
     if (hxm_gpu_tile_verdict(&c, op, 0) != HXM_REASON_OK) continue;
     sp.cands.push_back(c);
-    // int8 tiles that leave CUs idle also run with K split over enough
-    // workgroup rows to cover every CU (up to 16, at least one stage each).
+    // int8 tiles that leave half the CUs idle also run with K split over
+    // 2, 4, 8 and 16 workgroup rows (at most two workgroups per CU, at least
+    // one stage per slice).  The best split is shape-dependent (measured,
+    // 256x256 tile: 512x512x16384 best at 16, 1024x1024x4096 at 4).
     const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
     const int cus = device_cus();
     if (op == HXM_I8 && cus > 0 && tiles * 2 <= cus) {
-      int32_t s = 2;
-      while (s < 16 && tiles * s < cus) s *= 2;
-      if ((K + c.bk - 1) / c.bk >= s) {
+      for (int32_t s = 2; s <= 16 && tiles * s <= 2 * cus && (K + c.bk - 1) / c.bk >= s;
+           s *= 2) {
         hxm_gemm_config sc = c;
         sc.split_k = s;
         sp.cands.push_back(sc);

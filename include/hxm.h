@@ -74,7 +74,8 @@ typedef struct hxm_gemm_config {
   int32_t bm, bn, bk;       /* workgroup tile; bk = K elements per LDS stage */
   int32_t waves_m, waves_n; /* wave grid inside the workgroup */
   int32_t stages;           /* LDS stages (2 = double buffer; prefetch depth stages-1) */
-  int32_t split_k;          /* workgroups along K (1 = none) */
+  int32_t split_k;          /* workgroup rows along K (0/1 = none; int8: 2, 4, 8 or 16,
+                               int32 partial planes summed exactly) */
 } hxm_gemm_config;
 
 /* ---- status / library ------------------------------------------------- */

@@ -313,6 +313,11 @@ hxm_status run_gemm(int32_t op, int32_t ab_dtype, int epi, const void* A,
     const int S = static_cast<int>((K * eb + kslice - 1) / kslice);
     if (S > 1) {
       const int64_t plane = M * N;
+      if (S * plane * 4 > kSplitKPlaneBytesMax)
+        return fail(HXM_UNSUPPORTED_SHAPE,
+                    "workspace-budget: split_k=%d needs %lld bytes of int32 partial planes, "
+                    "above the %lld-byte limit",
+                    S, (long long)(S * plane * 4), (long long)kSplitKPlaneBytesMax);
       void* ws = nullptr;
       if ((st = stream_workspace(stream, static_cast<size_t>(S * plane * 4), &ws, kWsSplitK)) !=
           HXM_OK)

@@ -60,6 +60,9 @@ hxm_status require_device(int* device_out);
 // operand packs and the tuner's reference output; slot 1 the split-K
 // partial planes, so the two never overwrite or reallocate each other.
 constexpr int kWsMain = 0, kWsSplitK = 1;
+// Largest split-K partial-plane buffer (S * M * N int32) a call may ask for;
+// the buffer stays allocated until hxm_release_cache().
+constexpr int64_t kSplitKPlaneBytesMax = int64_t(256) << 20;
 hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out, int slot = kWsMain);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

@@ -2,8 +2,9 @@
 // admission and the per-stream workspace (the library-owned counterpart of
 // the reference's VTCM pool, bin/runtime/include/HexagonCAPI.h:26-57 --
 // allocated once, kept for the process until released).
+#include <map>
 #include <mutex>
-#include <unordered_map>
+#include <tuple>
 #include <vector>
 
 #include "hxm_internal.h"
@@ -18,9 +19,11 @@ struct Workspace {
   size_t bytes = 0;
 };
 std::mutex g_ws_mu;
-// key: ((device << 48) ^ stream pointer) | slot (stream objects are at least
-// 8-byte aligned, so the slot bit does not collide)
-std::unordered_map<uint64_t, Workspace> g_ws;
+// One buffer per (device, stream handle, slot).  The handle is compared as a
+// value: the null stream (0) and the special handles such as
+// hipStreamLegacy (1) are keys like any other.
+typedef std::tuple<int, uintptr_t, int> WsKey;
+std::map<WsKey, Workspace> g_ws;
 
 std::mutex g_dev_mu;
 std::vector<int8_t> g_dev_ok;  // -1 unknown, 0 not gfx950, 1 ok
@@ -80,9 +83,9 @@ hxm_status require_device(int* device_out) {
 hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out, int slot) {
   int dev = 0;
   HXM_HIP_TRY(hipGetDevice(&dev));
-  const uint64_t key = ((static_cast<uint64_t>(dev) << 48) ^
-                        reinterpret_cast<uint64_t>(stream)) |
-                       static_cast<uint64_t>(slot & 1);
+  if (slot != kWsMain && slot != kWsSplitK)
+    return fail(HXM_INVALID_ARG, "invalid-argument: workspace slot %d", slot);
+  const WsKey key(dev, reinterpret_cast<uintptr_t>(stream), slot);
   std::lock_guard<std::mutex> lk(g_ws_mu);
   Workspace& w = g_ws[key];
   if (w.bytes < bytes) {
@@ -147,7 +150,7 @@ hxm_status hxm_release_cache(void) {
   if (st != HXM_OK) return st;
   std::lock_guard<std::mutex> lk(hxm::g_ws_mu);
   for (auto it = hxm::g_ws.begin(); it != hxm::g_ws.end();) {
-    if ((it->first >> 48) == static_cast<uint64_t>(dev)) {
+    if (std::get<0>(it->first) == dev) {
       if (it->second.ptr) HXM_HIP_TRY(hipFree(it->second.ptr));
       it = hxm::g_ws.erase(it);
     } else {

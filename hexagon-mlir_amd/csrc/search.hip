@@ -64,6 +64,43 @@ static int64_t next_pow2(int64_t v) {
 }
 static bool is_fin(double v) { return std::isfinite(v); }
 
+// hxm_canary_status codes.
+enum { kCanaryOk = 0, kCanaryMissing = 1, kCanaryUnmeasured = 2, kCanaryDrift = 3,
+       kCanaryReference = 4 };
+
+// The gated walk over arms 0..n-1 in index order from the incumbent
+// `start`: a challenger takes the crown only when its median is lower than
+// the incumbent's by more than the gate of the noisier of the two.  Arms
+// with no finite median are passed over.  arm(i) yields arm i's
+// hxm_arm_quantiles.  Returns the survivor, -1 when `start` is not a
+// measured arm.
+template <typename ArmFn>
+int32_t gated_walk(int32_t n, int32_t start, ArmFn arm, int32_t* outcome, int32_t* faced,
+                   double* delta_out, double* gate_out) {
+  for (int32_t i = 0; i < n; ++i) {
+    if (outcome) outcome[i] = -1;
+    if (faced) faced[i] = -1;
+    if (delta_out) delta_out[i] = NAN;
+    if (gate_out) gate_out[i] = NAN;
+  }
+  if (start < 0 || start >= n || !is_fin(arm(start).q50)) return -1;
+  auto cv = [](const hxm_arm_quantiles& a) { return hxm_quantile_spread_cv(a.q20, a.q50, a.q80); };
+  int32_t inc = start;
+  for (int32_t i = 0; i < n; ++i) {
+    const hxm_arm_quantiles ch = arm(i);
+    if (i == start || !is_fin(ch.q50)) continue;
+    const hxm_arm_quantiles cur = arm(inc);
+    const double gate = hxm_champion_gate(std::max(cv(ch), cv(cur)));
+    const double delta = (cur.q50 - ch.q50) / cur.q50;
+    if (faced) faced[i] = inc;
+    if (delta_out) delta_out[i] = delta;
+    if (gate_out) gate_out[i] = gate;
+    if (outcome) outcome[i] = delta > gate ? 1 : 0;
+    if (delta > gate) inc = i;
+  }
+  return inc;
+}
+
 // ---- the tuned-winner cache -------------------------------------------
 namespace {
 typedef std::tuple<int32_t, int64_t, int64_t, int64_t> TuneKey;
@@ -122,6 +159,14 @@ int device_cus() {
 bool same_config(const hxm_gemm_config& a, const hxm_gemm_config& b) {
   return a.bm == b.bm && a.bn == b.bn && a.bk == b.bk && a.waves_m == b.waves_m &&
          a.waves_n == b.waves_n && a.stages == b.stages && a.split_k == b.split_k;
+}
+
+// Same kernel and the same K split (0 and 1 both mean "no split").
+bool same_launch(const hxm_gemm_config& a, const hxm_gemm_config& b) {
+  hxm_gemm_config x = a, y = b;
+  x.split_k = x.split_k > 1 ? x.split_k : 1;
+  y.split_k = y.split_k > 1 ? y.split_k : 1;
+  return same_config(x, y);
 }
 
 // True when this build compiled `c` for `op`.
@@ -244,17 +289,12 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
     auto it = g_canary_ref.find(op);
     if (it != g_canary_ref.end()) cref = it->second;
   }
-  double cdelta = NAN, cgate = NAN;
-  const int32_t cstatus = hxm_canary_status(1, c20, c50, c80, cref, &cdelta, &cgate);
-  const bool round_valid = cstatus == 0 || cstatus == 4;
 
-  // Control output is the verify reference.
+  // The control (what an untuned call runs, split_k included) is the verify
+  // reference: its output is what every other candidate must reproduce.
   int32_t ctl_idx = -1;
-  for (size_t i = 0; i < cands.size(); ++i)
-    if (cands[i].bm == control.bm && cands[i].bn == control.bn &&
-        cands[i].bk == control.bk && cands[i].stages == control.stages &&
-        cands[i].waves_m == control.waves_m && cands[i].waves_n == control.waves_n)
-      ctl_idx = static_cast<int32_t>(i);
+  for (size_t i = 0; i < cands.size() && ctl_idx < 0; ++i)
+    if (same_launch(cands[i], control)) ctl_idx = static_cast<int32_t>(i);
   bool have_ref = false;
   if (ctl_idx >= 0 && word_rows &&
       sp.run(cands[ctl_idx], M, N, K) == HXM_OK) {
@@ -286,14 +326,19 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
 
-  int32_t start = (ctl_idx >= 0 && is_fin(q50[ctl_idx])) ? ctl_idx : -1;
-  if (start < 0)
-    for (int i = 0; i < n && start < 0; ++i)
-      if (is_fin(q50[i])) start = i;
-  std::vector<int32_t> outcome(n);
+  // The round's verdict.  Should the control fail to run, the walk starts at
+  // the first measured config instead (no control arm: nothing is proven).
+  std::vector<hxm_arm_quantiles> arms(n);
+  for (int i = 0; i < n; ++i) arms[i] = hxm_arm_quantiles{q20[i], q50[i], q80[i]};
+  const hxm_arm_quantiles canary_q{c20, c50, c80};
+  const int32_t ctl_arm = (ctl_idx >= 0 && is_fin(q50[ctl_idx])) ? ctl_idx : -1;
+  hxm_round_verdict verdict{};
+  std::vector<int32_t> outcome(n), faced(n);
   std::vector<double> delta(n), gate(n);
-  const int32_t champ = hxm_champion_walk(q20.data(), q50.data(), q80.data(), n, start,
-                                          outcome.data(), delta.data(), gate.data());
+  const int32_t champ =
+      hxm_judge_round(arms.data(), n, ctl_arm, &canary_q, cref, &verdict, outcome.data(),
+                      faced.data(), delta.data(), gate.data());
+  const bool round_valid = verdict.valid != 0;
   hxm_gemm_config win = champ >= 0 ? cands[champ] : control;
   {
     std::lock_guard<std::mutex> lk(g_tune_mu);
@@ -308,6 +353,10 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
   if (report && report_cap > 0) {
     static const char* kCanary[] = {"ok", "missing", "unmeasured", "drift",
                                     "reference-established"};
+    static const char* kStart[] = {"control", "nominal", "control-unmeasured",
+                                   "control-absent", "empty"};
+    static const char* kProof[] = {"proven", "within-gate", "control-held", "no-control",
+                                   "void"};
     auto num = [](double v) {
       char b[64];
       if (!is_fin(v)) return std::string("null");
@@ -319,9 +368,11 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
                     std::to_string(K) + "],\"reps\":" + std::to_string(reps) +
                     ",\"unit\":\"us\",\"round_verdict\":\"" +
                     (round_valid ? "valid" : "invalid-canary") +
-                    "\",\"canary\":{\"status\":\"" + kCanary[cstatus] +
-                    "\",\"q50\":" + num(c50) + ",\"reference_q50\":" + num(cref) +
-                    ",\"delta_pct\":" + num(100.0 * cdelta) + "},\"control\":" +
+                    "\",\"start\":\"" + kStart[verdict.start] + "\",\"proof\":\"" +
+                    kProof[verdict.proof] + "\",\"canary\":{\"status\":\"" +
+                    kCanary[verdict.canary] + "\",\"q50\":" + num(c50) +
+                    ",\"reference_q50\":" + num(cref) + ",\"delta_pct\":" +
+                    num(100.0 * verdict.canary_delta) + "},\"control\":" +
                     (ctl_idx >= 0 ? std::to_string(ctl_idx) : "null") +
                     ",\"champion\":" + (champ >= 0 ? std::to_string(champ) : "null") +
                     ",\"configs\":[";
@@ -335,7 +386,8 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
            num(q80[i]) + ",\"verified\":" + (verified[i] ? "true" : "false") +
            ",\"outcome\":\"" +
            (outcome[i] == 1 ? "takeover" : outcome[i] == 0 ? "kept" : "-") +
-           "\",\"delta_pct\":" + num(100.0 * delta[i]) + ",\"gate_pct\":" +
+           "\",\"faced\":" + (faced[i] >= 0 ? std::to_string(faced[i]) : "null") +
+           ",\"delta_pct\":" + num(100.0 * delta[i]) + ",\"gate_pct\":" +
            num(100.0 * gate[i]) + "}";
     }
     r += "]}";
@@ -471,26 +523,9 @@ int32_t hxm_calibration_iters(double perf_us, double target_us, int32_t lo, int3
 int32_t hxm_champion_walk(const double* q20, const double* q50, const double* q80,
                           int32_t n, int32_t start, int32_t* outcome,
                           double* delta_out, double* gate_out) {
-  for (int i = 0; i < n; ++i) {
-    if (outcome) outcome[i] = -1;
-    if (delta_out) delta_out[i] = NAN;
-    if (gate_out) gate_out[i] = NAN;
-  }
-  if (start < 0 || start >= n || !is_fin(q50[start])) return -1;
-  int inc = start;
-  for (int i = 0; i < n; ++i) {
-    if (i == start || !is_fin(q50[i])) continue;
-    const double cv = std::max(hxm_quantile_spread_cv(q20[i], q50[i], q80[i]),
-                               hxm_quantile_spread_cv(q20[inc], q50[inc], q80[inc]));
-    const double gate = hxm_champion_gate(cv);
-    const double delta = (q50[inc] - q50[i]) / q50[inc];
-    if (delta_out) delta_out[i] = delta;
-    if (gate_out) gate_out[i] = gate;
-    const bool take = delta > gate;
-    if (outcome) outcome[i] = take ? 1 : 0;
-    if (take) inc = i;
-  }
-  return inc;
+  return hxm::gated_walk(
+      n, start, [&](int i) { return hxm_arm_quantiles{q20[i], q50[i], q80[i]}; }, outcome,
+      nullptr, delta_out, gate_out);
 }
 
 /* canary_verdict's status (hmx_search.py:1292-1367): 0 ok, 1 missing,
@@ -499,14 +534,76 @@ int32_t hxm_canary_status(int32_t present, double q20, double q50, double q80,
                           double reference_q50, double* delta_out, double* gate_out) {
   if (delta_out) *delta_out = NAN;
   if (gate_out) *gate_out = NAN;
-  if (!present) return 1;
-  if (!is_fin(q50)) return 2;
-  if (!is_fin(reference_q50) || reference_q50 <= 0.0) return 4;
+  if (!present) return kCanaryMissing;
+  if (!is_fin(q50)) return kCanaryUnmeasured;
+  if (!is_fin(reference_q50) || reference_q50 <= 0.0) return kCanaryReference;
   const double gate = hxm_champion_gate(hxm_quantile_spread_cv(q20, q50, q80));
   const double delta = (q50 - reference_q50) / reference_q50;
   if (delta_out) *delta_out = delta;
   if (gate_out) *gate_out = gate;
-  return std::fabs(delta) > gate ? 3 : 0;
+  return std::fabs(delta) > gate ? kCanaryDrift : kCanaryOk;
+}
+
+int32_t hxm_judge_round(const hxm_arm_quantiles* arms, int32_t n, int32_t control,
+                        const hxm_arm_quantiles* canary, double canary_reference_q50,
+                        hxm_round_verdict* out, int32_t* outcome, int32_t* faced,
+                        double* delta, double* gate) {
+  if (n < 0 || (n > 0 && !arms)) return -2;
+  hxm_round_verdict v{};
+  v.canary_cv = v.canary_delta = v.canary_gate = NAN;
+  v.control_cv = v.control_delta = v.control_gate = NAN;
+
+  // The canary decides whether the round may be read at all.
+  if (canary) {
+    v.canary = hxm_canary_status(1, canary->q20, canary->q50, canary->q80, canary_reference_q50,
+                                 &v.canary_delta, &v.canary_gate);
+    v.canary_cv = hxm_quantile_spread_cv(canary->q20, canary->q50, canary->q80);
+  } else {
+    v.canary = kCanaryMissing;
+  }
+  v.valid = v.canary == kCanaryOk || v.canary == kCanaryReference;
+
+  int32_t first = -1;
+  for (int32_t i = 0; i < n; ++i)
+    if (is_fin(arms[i].q50)) {
+      ++v.measured;
+      if (first < 0) first = i;
+    }
+
+  // The incumbent the walk starts from.
+  int32_t start = -1;
+  if (control >= 0 && control < n) {
+    v.start = is_fin(arms[control].q50) ? HXM_START_CONTROL : HXM_START_CONTROL_UNMEASURED;
+    if (v.start == HXM_START_CONTROL) start = control;
+  } else if (control != -1) {
+    v.start = HXM_START_CONTROL_ABSENT;
+  } else {
+    v.start = first >= 0 ? HXM_START_NOMINAL : HXM_START_EMPTY;
+    start = first;
+  }
+  auto arm = [&](int i) { return arms[i]; };
+  v.champion = gated_walk(n, start, arm, outcome, faced, delta, gate);
+  if (outcome)
+    for (int32_t i = 0; i < n; ++i) v.takeovers += outcome[i] == 1;
+
+  // Champion against the control arm, judged with the noisier arm's gate.
+  if (v.start == HXM_START_CONTROL && v.champion >= 0) {
+    const hxm_arm_quantiles c = arms[control], w = arms[v.champion];
+    v.control_cv = std::max(hxm_quantile_spread_cv(c.q20, c.q50, c.q80),
+                            hxm_quantile_spread_cv(w.q20, w.q50, w.q80));
+    v.control_gate = hxm_champion_gate(v.control_cv);
+    v.control_delta = (c.q50 - w.q50) / c.q50;
+  }
+  if (!v.valid)
+    v.proof = HXM_PROOF_VOID;
+  else if (v.start != HXM_START_CONTROL || v.champion < 0)
+    v.proof = HXM_PROOF_NO_CONTROL;
+  else if (v.champion == control)
+    v.proof = HXM_PROOF_CONTROL_HELD;
+  else
+    v.proof = v.control_delta > v.control_gate ? HXM_PROOF_PROVEN : HXM_PROOF_WITHIN_GATE;
+  if (out) *out = v;
+  return v.champion;
 }
 
 int32_t hxm_tune_cache_lookup(int32_t op, int64_t M, int64_t N, int64_t K,
@@ -667,7 +764,8 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
     const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
     const int cus = device_cus();
     if (op == HXM_I8 && cus > 0 && tiles * 2 <= cus) {
-      for (int32_t s = 2; s <= 16 && tiles * s <= 2 * cus && (K + c.bk - 1) / c.bk >= s;
+      for (int32_t s = 2; s <= 16 && tiles * s <= 2 * cus && (K + c.bk - 1) / c.bk >= s &&
+                          s * M * N * 4 <= kSplitKPlaneBytesMax;
            s *= 2) {
         hxm_gemm_config sc = c;
         sc.split_k = s;

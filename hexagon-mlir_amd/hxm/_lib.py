@@ -67,6 +67,22 @@ class TilePredictionC(ctypes.Structure):
                 ("heat", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
+class ArmQuantiles(ctypes.Structure):
+    """hxm_arm_quantiles: one measured arm of a search round."""
+    _fields_ = [("q20", ctypes.c_double), ("q50", ctypes.c_double), ("q80", ctypes.c_double)]
+
+
+class RoundVerdict(ctypes.Structure):
+    """hxm_round_verdict: a search round judged as a whole (codes only)."""
+    _fields_ = [("canary", ctypes.c_int32), ("valid", ctypes.c_int32),
+                ("start", ctypes.c_int32), ("champion", ctypes.c_int32),
+                ("proof", ctypes.c_int32), ("measured", ctypes.c_int32),
+                ("takeovers", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("canary_cv", ctypes.c_double), ("canary_delta", ctypes.c_double),
+                ("canary_gate", ctypes.c_double), ("control_cv", ctypes.c_double),
+                ("control_delta", ctypes.c_double), ("control_gate", ctypes.c_double)]
+
+
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -121,6 +137,10 @@ SIGNATURES = {
                                  ctypes.POINTER(_f64), ctypes.POINTER(_f64)]),
     "hxm_canary_status": (_i32, [_i32, _f64, _f64, _f64, _f64, ctypes.POINTER(_f64),
                                  ctypes.POINTER(_f64)]),
+    "hxm_judge_round": (_i32, [ctypes.POINTER(ArmQuantiles), _i32, _i32,
+                               ctypes.POINTER(ArmQuantiles), _f64, ctypes.POINTER(RoundVerdict),
+                               ctypes.POINTER(_i32), ctypes.POINTER(_i32), ctypes.POINTER(_f64),
+                               ctypes.POINTER(_f64)]),
     "hxm_tune_gemm": (_st, [_i32, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _cfgp,
                             ctypes.c_char_p, _i64, _p]),
     "hxm_tune_cache_clear": (None, []),

@@ -16,7 +16,7 @@ import ctypes
 import math
 from typing import Any, Mapping, NamedTuple, Optional, Sequence
 
-from ._lib import GemmConfig, lib
+from ._lib import ArmQuantiles, GemmConfig, RoundVerdict, lib
 
 # Constants (hmx_search.py:172-205, :1184-1214).
 TILE_EDGE = 32
@@ -155,189 +155,123 @@ def _record_q50(record) -> Optional[float]:
     return float(value) if _is_finite(value) else None
 
 
+def _arm(record) -> ArmQuantiles:
+    """A measurement record (``q20_pcyc`` / ``q50_pcyc`` / ``q80_pcyc``) as the
+    C arm; missing or non-finite quantiles become NaN."""
+    get = record.get if isinstance(record, Mapping) else (lambda _k: None)
+    return ArmQuantiles(_f(get("q20_pcyc")), _f(get("q50_pcyc")), _f(get("q80_pcyc")))
+
+
+#: hxm_judge_round's codes (include/hxm.h), by value.
+START_CODES = ("control", "nominal", "control-unmeasured", "control-absent", "empty")
+PROOF_CODES = ("proven", "within-gate", "control-held", "no-control", "void")
+GATE_FORM = "max(3xCV, 15%)"
+
+
 def canary_verdict(metrics, reference=None) -> dict:
-    """hmx_search.canary_verdict (hmx_search.py:1292-1367)."""
-    record = dict(status=CANARY_OK, healthy=True, q50_pcyc=None, cv=0.0,
-                  reference_q50_pcyc=None, delta_pct=None, gate_pct=None, reason="")
+    """The canary's status for one round (hmx_search.canary_verdict,
+    hmx_search.py:1292-1367; decided by hxm_canary_status).  ``metrics`` is
+    the canary's measurement record or None; ``reference`` the previous
+    round's canary record (or its median)."""
     present = metrics is not None
-    q50 = _record_q50(metrics) if present else None
-    q20 = metrics.get("q20_pcyc") if isinstance(metrics, Mapping) else None
-    q80 = metrics.get("q80_pcyc") if isinstance(metrics, Mapping) else None
+    arm = _arm(metrics)
     ref = _record_q50(reference)
-    delta = ctypes.c_double()
-    gate = ctypes.c_double()
-    code = lib.hxm_canary_status(int(present), _f(q20), _f(q50), _f(q80), _f(ref),
+    delta, gate = ctypes.c_double(), ctypes.c_double()
+    code = lib.hxm_canary_status(int(present), arm.q20, arm.q50, arm.q80, _f(ref),
                                  ctypes.byref(delta), ctypes.byref(gate))
     status = _CANARY_STATUS[code]
-    if present and isinstance(metrics, Mapping):
-        record["cv"] = quantile_spread_cv(q20, metrics.get("q50_pcyc"), q80)
-    record["q50_pcyc"] = _finite_or_none(q50)
-    if status == CANARY_MISSING:
-        record.update(status=status, healthy=False,
-                      reason=("no canary measurement rode with this round: without its "
-                              "sentinel the round cannot tell a broken device from slow "
-                              "configs, so it publishes no verdict"))
-        return record
-    if status == CANARY_UNMEASURED:
-        record.update(status=status, healthy=False,
-                      reason=("the canary config failed or printed no cycles: a "
-                              "known-healthy config that cannot run indicts the device "
-                              "or the launch path, not the config"))
-        return record
-    record["reference_q50_pcyc"] = _finite_or_none(ref)
-    if status == CANARY_REFERENCE:
-        record.update(status=status,
-                      reason=("no healthy reference existed, so this run establishes it; "
-                              "the round is valid and the next round can judge against "
-                              "this median"))
-        return record
-    record["delta_pct"] = _finite_or_none(100.0 * delta.value)
-    record["gate_pct"] = _finite_or_none(100.0 * gate.value)
-    if status == CANARY_DRIFT:
-        record.update(status=status, healthy=False,
-                      reason=(f"the canary moved {100.0 * delta.value:+.1f}% from its "
-                              f"reference, more than the {100.0 * gate.value:.1f}% gate: "
-                              "same config, same build, same iteration count, so the "
-                              "device state moved and every other number in this round "
-                              "was taken under it"))
-        return record
-    record["reason"] = (f"the canary stayed within {100.0 * abs(delta.value):.1f}% of its "
-                        f"reference (gate {100.0 * gate.value:.1f}%)")
-    return record
+    return dict(status=status, healthy=status in (CANARY_OK, CANARY_REFERENCE),
+                q50_pcyc=_finite_or_none(arm.q50),
+                cv=quantile_spread_cv(arm.q20, arm.q50, arm.q80) if present else 0.0,
+                reference_q50_pcyc=_finite_or_none(ref) if present else None,
+                delta_pct=_finite_or_none(100.0 * delta.value),
+                gate_pct=_finite_or_none(100.0 * gate.value))
+
+
+def _matches(control, label: str, tiles: tuple) -> bool:
+    if control is None:
+        return False
+    if isinstance(control, str):
+        return control == label
+    return tuple(control) == tiles
 
 
 def judge_champion_round(measurements, *, control=None, canary=None, canary_reference=None,
                          iters=None) -> dict:
-    """hmx_search.judge_champion_round (hmx_search.py:1370-1571).
+    """The verdict of one search round (the decision of
+    hmx_search.judge_champion_round, hmx_search.py:1370-1571).
 
-    The walk itself is hxm_champion_walk; this builds the same report."""
-    canary_record = canary_verdict(canary, canary_reference)
-    round_valid = bool(canary_record["healthy"])
-    rows = []
-    for entry in measurements:
-        row = dict(entry)
-        row["tiles_tuple"] = tuple(row.get("tiles") or ())
-        rows.append(row)
-    label_of = lambda r: str(r.get("cfg", ""))  # noqa: E731
-    cv_of = lambda r: quantile_spread_cv(r.get("q20_pcyc"), r.get("q50_pcyc"),  # noqa: E731
-                                         r.get("q80_pcyc"))
-    measured = [r for r in rows if _record_q50(r) is not None]
-    unmeasured = [label_of(r) for r in rows if _record_q50(r) is None]
+    ``measurements``: records with ``cfg`` (label), ``tiles`` and the
+    ``q20_pcyc`` / ``q50_pcyc`` / ``q80_pcyc`` quantiles (a non-finite median
+    means the config never ran).  ``control`` names the control arm by label
+    or tiles.  The decision is hxm_judge_round's: the arms are handed over
+    sorted by (tiles, label), which is the walk order.  ``start`` and
+    ``proof`` carry its codes (START_CODES / PROOF_CODES)."""
+    arms = sorted(({"label": str(m.get("cfg", "")), "tiles": tuple(m.get("tiles") or ()),
+                    "rec": m} for m in measurements), key=lambda a: (a["tiles"], a["label"]))
+    n = len(arms)
+    hits = [i for i, a in enumerate(arms) if _matches(control, a["label"], a["tiles"])]
+    if control is None:
+        ctl = -1
+    elif not hits:
+        ctl = -2
+    else:  # a measured match if there is one
+        ctl = next((i for i in hits if _record_q50(arms[i]["rec"]) is not None), hits[0])
 
-    def as_control(row):
-        if control is None:
-            return False
-        if str(control) == label_of(row):
-            return True
-        tiles = tuple(control) if not isinstance(control, str) else None
-        return tiles is not None and tiles == row["tiles_tuple"]
+    c_arms = (ArmQuantiles * max(1, n))(*[_arm(a["rec"]) for a in arms])
+    canary_arm = _arm(canary) if canary is not None else None
+    ref = _record_q50(canary_reference)
+    v = RoundVerdict()
+    outcome, faced = (ctypes.c_int32 * max(1, n))(), (ctypes.c_int32 * max(1, n))()
+    delta, gate = (ctypes.c_double * max(1, n))(), (ctypes.c_double * max(1, n))()
+    lib.hxm_judge_round(c_arms, n, ctl, ctypes.byref(canary_arm) if canary_arm else None,
+                        _f(ref), ctypes.byref(v), outcome, faced, delta, gate)
 
-    control_rows = [r for r in measured if as_control(r)]
-    control_row = control_rows[0] if control_rows else None
-    control_any = [r for r in rows if as_control(r)]
-    ordered = sorted(measured, key=lambda r: (r["tiles_tuple"], label_of(r)))
+    def q50(i):
+        return _finite_or_none(c_arms[i].q50)
 
-    walk_note = ""
-    start = -1
-    if control_row is not None:
-        start = next(i for i, r in enumerate(ordered) if r is control_row)
-        walk_note = ("the incumbent starts at the manual control tile: the winner is judged "
-                     "against it, so it defends the crown first")
-    elif control_any:
-        walk_note = ("the manual control tile was nominated but never measured (it scored "
-                     "inf), so there is no arm to judge a win against")
-    elif control is not None:
-        walk_note = ("the nominated control arm is not among this round's measurements, so "
-                     "there is no arm to judge a win against")
-    elif ordered:
-        start = 0
-        walk_note = ("no control arm was nominated: the incumbent starts at the first "
-                     "enumerated candidate, so the walk is deterministic but the starting "
-                     "point is nominal")
+    def cv(i):
+        return quantile_spread_cv(c_arms[i].q20, c_arms[i].q50, c_arms[i].q80)
 
-    n = len(ordered)
-    arr = lambda key: (ctypes.c_double * max(1, n))(*[_f(r.get(key)) for r in ordered])  # noqa
-    outcome = (ctypes.c_int32 * max(1, n))()
-    delta = (ctypes.c_double * max(1, n))()
-    gate = (ctypes.c_double * max(1, n))()
-    champ = -1
-    comparisons, changes = [], []
-    if start >= 0:
-        champ = lib.hxm_champion_walk(arr("q20_pcyc"), arr("q50_pcyc"), arr("q80_pcyc"), n,
-                                      start, outcome, delta, gate)
-        # Replay the visit order to name the incumbent each challenger faced.
-        inc = start
-        step = 0
-        for i in range(n):
-            if i == start or outcome[i] < 0:
-                continue
-            ch, ic = ordered[i], ordered[inc]
-            rec = dict(step=step, challenger=label_of(ch), incumbent=label_of(ic),
-                       challenger_q50_pcyc=_finite_or_none(_record_q50(ch)),
-                       incumbent_q50_pcyc=_finite_or_none(_record_q50(ic)),
-                       delta_pct=_finite_or_none(100.0 * delta[i]),
-                       cv=_finite_or_none(max(cv_of(ch), cv_of(ic))),
-                       gate_pct=_finite_or_none(100.0 * gate[i]),
-                       gate_form="max(3xCV, 15%)",
-                       outcome="takeover" if outcome[i] == 1 else "kept")
-            comparisons.append(rec)
-            if outcome[i] == 1:
-                changes.append(dict(rec))
-                inc = i
-            step += 1
-    champion_row = ordered[champ] if champ >= 0 else None
+    comparisons = []
+    for i in range(n):
+        if outcome[i] < 0:
+            continue
+        j = faced[i]
+        comparisons.append(dict(
+            step=len(comparisons), challenger=arms[i]["label"], incumbent=arms[j]["label"],
+            challenger_q50_pcyc=q50(i), incumbent_q50_pcyc=q50(j),
+            delta_pct=_finite_or_none(100.0 * delta[i]), cv=_finite_or_none(max(cv(i), cv(j))),
+            gate_pct=_finite_or_none(100.0 * gate[i]), gate_form=GATE_FORM,
+            outcome="takeover" if outcome[i] == 1 else "kept"))
 
-    beats_control = None
-    if control_row is not None and champion_row is not None:
-        cv = max(cv_of(control_row), cv_of(champion_row))
-        g = champion_gate(cv)
-        if champion_row is control_row:
-            beats_control = dict(delta_pct=0.0, cv=_finite_or_none(cv),
-                                 gate_pct=_finite_or_none(100.0 * g),
-                                 gate_form="max(3xCV, 15%)", significant=False,
-                                 note=("the manual control tile kept the crown: no candidate "
-                                       "beat it by the gate"))
-        else:
-            cq, wq = _record_q50(control_row), _record_q50(champion_row)
-            d = (cq - wq) / cq
-            beats_control = dict(
-                delta_pct=_finite_or_none(100.0 * d), cv=_finite_or_none(cv),
-                gate_pct=_finite_or_none(100.0 * g), gate_form="max(3xCV, 15%)",
-                significant=bool(round_valid and d > g),
-                note=("the champion beat the manual control tile by "
-                      f"{100.0 * d:.1f}%, " + ("more than" if d > g else "not more than")
-                      + f" the {100.0 * g:.1f}% gate"))
-    significant = bool(round_valid and beats_control is not None
-                       and beats_control["significant"])
-    if not round_valid:
-        note = ("the round is void (" + canary_record["status"] + "): "
-                + canary_record["reason"] + ". The champion below is the walk's survivor, "
-                "not a verdict.")
-    elif beats_control is None:
-        note = ("no control arm produced a measurement, so there is nothing to prove a win "
-                "against: the champion is the walk's survivor (NOT-PROVEN, which is not the "
-                "same as 'no effect')")
-    elif beats_control["significant"]:
-        note = f"the champion beat the manual control tile by more than the gate at iters={iters}"
-    else:
-        note = (f"the champion did not beat the manual control tile by more than the gate at "
-                f"iters={iters}: NOT-PROVEN, which is not the same as 'no effect'")
+    champ = v.champion if v.champion >= 0 else None
+    has_control = START_CODES[v.start] == "control"
+    proof = PROOF_CODES[v.proof]
+    versus = None
+    if has_control and champ is not None:
+        versus = dict(delta_pct=_finite_or_none(100.0 * v.control_delta),
+                      cv=_finite_or_none(v.control_cv),
+                      gate_pct=_finite_or_none(100.0 * v.control_gate), gate_form=GATE_FORM,
+                      significant=proof == "proven")
     return dict(
         kind="hmx-search-champion",
-        round_verdict=ROUND_VALID if round_valid else ROUND_INVALID_CANARY,
+        round_verdict=ROUND_VALID if v.valid else ROUND_INVALID_CANARY,
         iters=iters,
-        gate=dict(form="max(3xCV, 15%)", cv_factor=CHAMPION_CV_FACTOR,
+        gate=dict(form=GATE_FORM, cv_factor=CHAMPION_CV_FACTOR,
                   margin_floor=CHAMPION_MARGIN_FLOOR),
-        canary=canary_record, walk_note=walk_note, measured_configs=len(measured),
-        champion=label_of(champion_row) if champion_row is not None else None,
-        champion_tiles=list(champion_row["tiles_tuple"]) if champion_row is not None else None,
-        champion_q50_pcyc=(_finite_or_none(_record_q50(champion_row))
-                           if champion_row is not None else None),
-        control=label_of(control_row) if control_row is not None else None,
-        control_tiles=list(control_row["tiles_tuple"]) if control_row is not None else None,
-        beats_control=beats_control, champion_significant=significant,
-        significance_note=note, changes=changes, comparisons=comparisons,
-        unmeasured=unmeasured, cvs={label_of(r): _finite_or_none(cv_of(r)) for r in rows},
+        canary=canary_verdict(canary, canary_reference),
+        start=START_CODES[v.start], proof=proof, measured_configs=int(v.measured),
+        champion=arms[champ]["label"] if champ is not None else None,
+        champion_tiles=list(arms[champ]["tiles"]) if champ is not None else None,
+        champion_q50_pcyc=q50(champ) if champ is not None else None,
+        control=arms[ctl]["label"] if has_control else None,
+        control_tiles=list(arms[ctl]["tiles"]) if has_control else None,
+        beats_control=versus, champion_significant=proof == "proven",
+        changes=[dict(c) for c in comparisons if c["outcome"] == "takeover"],
+        comparisons=comparisons,
+        unmeasured=[a["label"] for i, a in enumerate(arms) if q50(i) is None],
+        cvs={a["label"]: _finite_or_none(cv(i)) for i, a in enumerate(arms)},
     )
 
 
@@ -539,12 +473,22 @@ def manifest_abstains(record: Optional[Mapping[str, Any]]) -> Optional[str]:
     return None
 
 
+#: hxm_cost_prune's kept codes (include/hxm.h), by value.
+KEPT_CODES = ("dropped", "band", "control", "abstains", "unvouched", "not-current",
+              "nothing-priced")
+
+
 def cost_prune(candidates, shape, *, control_tile=None, margin: float = PRUNE_MARGIN,
                envelope: tuple = COST_ENVELOPE, predictions: Optional[Mapping] = None,
                manifest_records: Optional[Mapping] = None, model=None, dtype: int = 4,
                out_dtype: Optional[int] = None):
-    """cost_prune (hmx_search.py:916-1027): returns ``(kept, dropped, notes)``;
-    ``kept`` keeps the caller's order, ``dropped`` holds (candidate, reason)."""
+    """The conservative prune (hmx_search.cost_prune, hmx_search.py:916-1027;
+    decided by hxm_cost_prune).  Returns ``(kept, dropped, notes)``: ``kept``
+    in the caller's order, ``dropped`` as (candidate, record) pairs, and
+    ``notes`` as event records: ``{"event": "champion", ...}`` (or
+    ``"nothing-priced"``) first, one ``{"event": "kept", "why": ...}`` per
+    candidate kept for a reason other than lying inside the band, and a
+    closing ``{"event": "summary", ...}``."""
     from ._lib import TilePredictionC
     m, n, k = shape
     candidates = list(candidates)
@@ -553,60 +497,52 @@ def cost_prune(candidates, shape, *, control_tile=None, margin: float = PRUNE_MA
                                                       out_dtype=out_dtype, model=model)
                        for c in candidates}
     count = len(candidates)
+    tiles = [tiles_of(c) for c in candidates]
     preds = (TilePredictionC * max(1, count))()
     cfgs = (GemmConfig * max(1, count))()
     vouched = (ctypes.c_int32 * max(1, count))()
-    control_tiles = tiles_of(control_tile) if control_tile is not None else None
-    control = -1
-    for i, cand in enumerate(candidates):
-        t = tiles_of(cand)
+    for i, t in enumerate(tiles):
         p = predictions[t]
         preds[i].lb_us, preds[i].ub_us, preds[i].p50_us = _f(p.lb), _f(p.ub), _f(p.p50)
         preds[i].abstain = _ABSTAIN_CODE.get(p.abstain, _ABSTAIN_CODE[ABSTAIN_NO_CELL])
-        preds[i].tier = 1 if not any(tr != TIER_CURRENT for tr in p.lb_tiers) else 0
+        preds[i].tier = 1 if all(tr == TIER_CURRENT for tr in p.lb_tiers) else 0
         cfgs[i] = GemmConfig(*(list(t) + [0] * 7)[:7])
         if manifest_records is not None:
-            vouched[i] = 1 if manifest_abstains(manifest_records.get(t)) is None else 0
-        if control < 0 and control_tiles is not None and t == control_tiles:
-            control = i
+            vouched[i] = manifest_abstains(manifest_records.get(t)) is None
+    wanted = tiles_of(control_tile) if control_tile is not None else None
+    control = tiles.index(wanted) if wanted in tiles else -1
     lo, hi = envelope
-    kept_code = (ctypes.c_int32 * max(1, count))()
+    codes = (ctypes.c_int32 * max(1, count))()
     threshold = ctypes.c_double(0.0)
     champ = lib.hxm_cost_prune(preds, cfgs, count, control,
                                vouched if manifest_records is not None else None,
-                               float(margin), float(lo), float(hi), kept_code,
+                               float(margin), float(lo), float(hi), codes,
                                ctypes.byref(threshold))
     if champ == -2:
         raise ValueError("cost_prune: invalid margin or envelope")
     if champ < 0:
-        return list(candidates), [], [
-            "cost_prune: no priced candidate -- nothing compared, nothing dropped"]
-    ch_t = tiles_of(candidates[champ])
-    ch = predictions[ch_t]
-    thr = threshold.value
+        return candidates, [], [{"event": "nothing-priced", "candidates": count},
+                                {"event": "summary", "kept": count, "dropped": 0}]
+    best = predictions[tiles[champ]]
+    notes = [{"event": "champion", "tiles": tiles[champ], "p50": best.p50, "lb": best.lb,
+              "ub": best.ub, "threshold": threshold.value}]
     kept, dropped = [], []
-    notes = [f"cost_prune: champion {ch_t} p50={ch.p50:.3f} lb={ch.lb:.3f} ub={ch.ub:.3f}; "
-             f"drop when lb(B) > {thr:.3f} * ub(A)"]
     for i, cand in enumerate(candidates):
-        t = tiles_of(cand)
-        p = predictions[t]
-        code = kept_code[i]
-        if code == 0:
-            dropped.append((cand, dict(tiles=list(t), lb=p.lb, ub=p.ub,
-                                       champion_tiles=list(ch_t), champion_ub=ch.ub,
-                                       ratio=p.lb / ch.ub, threshold=thr, margin=margin,
-                                       envelope=list(envelope), table_rev=p.table_rev)))
+        p, why = predictions[tiles[i]], KEPT_CODES[codes[i]]
+        if why == "dropped":
+            dropped.append((cand, dict(tiles=list(tiles[i]), lb=p.lb, ub=p.ub,
+                                       champion_tiles=list(tiles[champ]), champion_ub=best.ub,
+                                       ratio=p.lb / best.ub, threshold=threshold.value,
+                                       margin=margin, envelope=list(envelope),
+                                       table_rev=p.table_rev)))
             continue
         kept.append(cand)
-        if code == 2:
-            notes.append(f"cost_prune: {t} kept (control tile is the arm the winner is "
-                         "judged against)")
-        elif code == 3:
-            notes.append(f"cost_prune: {t} kept (abstain {p.abstain})")
-        elif code == 4:
-            notes.append(f"cost_prune: {t} kept (abstain {ABSTAIN_MANIFEST})")
-        elif code == 5:
-            notes.append(f"cost_prune: {t} kept (lower bound rests on {p.lb_tiers} prices: "
-                         "only a current-device model may drive a drop)")
-    notes.append(f"cost_prune: kept {len(kept)}, dropped {len(dropped)}")
+        if why != "band":
+            note = {"event": "kept", "tiles": tiles[i], "why": why}
+            if why == "abstains":
+                note["abstain"] = p.abstain
+            elif why == "not-current":
+                note["lb_tiers"] = tuple(p.lb_tiers)
+            notes.append(note)
+    notes.append({"event": "summary", "kept": len(kept), "dropped": len(dropped)})
     return kept, dropped, notes

@@ -14,7 +14,8 @@
  *     (qcom_hexagon_backend/include/hexagon/Dialect/Hmx/Transforms/
  *      HmxManifest.h:81-100): "unsupported-dtype", "min-rows",
  *     "tile-alignment", "lds-budget" (the VTCM budget's counterpart), plus
- *     "invalid-argument".  There is no silent fallback: a refused call
+ *     "invalid-argument" and "workspace-budget" (a library-owned scratch
+ *     buffer would exceed its stated limit).  There is no silent fallback: a refused call
  *     computes nothing.
  *   - numerics: fp16/bf16 products accumulate in fp32 and are rounded once
  *     to the output dtype; int8 products accumulate exactly in int32.
@@ -75,7 +76,11 @@ typedef struct hxm_gemm_config {
   int32_t waves_m, waves_n; /* wave grid inside the workgroup */
   int32_t stages;           /* LDS stages (2 = double buffer; prefetch depth stages-1) */
   int32_t split_k;          /* workgroup rows along K (0/1 = none; int8: 2, 4, 8 or 16,
-                               int32 partial planes summed exactly) */
+                               int32 partial planes summed exactly).  The planes,
+                               S * M * N * 4 bytes, live in a library-owned
+                               per-stream buffer kept until hxm_release_cache();
+                               above 256 MiB the call is refused
+                               ("workspace-budget") */
 } hxm_gemm_config;
 
 /* ---- status / library ------------------------------------------------- */
@@ -405,6 +410,57 @@ int32_t hxm_champion_walk(const double* q20, const double* q50,
 int32_t hxm_canary_status(int32_t present, double q20, double q50, double q80,
                           double reference_q50, double* delta_out,
                           double* gate_out);
+
+/* One search round judged as a whole (the decision of
+ * hmx_search.judge_champion_round, hmx_search.py:1370-1571, as codes; the
+ * measured tuner and the Python mirror both call it).  Arms are given in
+ * walk order (the caller sorts them by their config); an arm whose q50 is
+ * not finite was never measured. */
+typedef struct hxm_arm_quantiles {
+  double q20, q50, q80;
+} hxm_arm_quantiles;
+
+/* Where the walk began. */
+enum {
+  HXM_START_CONTROL = 0,            /* at the measured control arm */
+  HXM_START_NOMINAL = 1,            /* no control named: the first measured arm */
+  HXM_START_CONTROL_UNMEASURED = 2, /* the control arm scored inf: no walk */
+  HXM_START_CONTROL_ABSENT = 3,     /* the named control is not an arm: no walk */
+  HXM_START_EMPTY = 4               /* nothing was measured */
+};
+/* What the round proves about its champion against the control arm. */
+enum {
+  HXM_PROOF_PROVEN = 0,       /* beat the control by more than the gate */
+  HXM_PROOF_WITHIN_GATE = 1,  /* won the walk, not by the gate against the control */
+  HXM_PROOF_CONTROL_HELD = 2, /* the control kept the crown */
+  HXM_PROOF_NO_CONTROL = 3,   /* no measured control arm to prove against */
+  HXM_PROOF_VOID = 4          /* the canary voided the round */
+};
+
+typedef struct hxm_round_verdict {
+  int32_t canary;    /* hxm_canary_status code */
+  int32_t valid;     /* 1 when the canary is ok or reference-established */
+  int32_t start;     /* HXM_START_* */
+  int32_t champion;  /* arm index of the walk's survivor, -1 for none */
+  int32_t proof;     /* HXM_PROOF_* */
+  int32_t measured;  /* arms with a finite q50 */
+  int32_t takeovers; /* crown changes during the walk */
+  int32_t reserved;
+  double canary_cv, canary_delta, canary_gate;    /* NaN where not judged */
+  double control_cv, control_delta, control_gate; /* champion vs control; NaN without one */
+} hxm_round_verdict;
+
+/* control: arm index of the control, -1 when none is named, any other
+ * negative value when one is named but is not among the arms.  canary: the
+ * canary's quantiles, NULL when no canary ran.  Per arm (each array may be
+ * NULL): outcome -1 not compared, 0 the incumbent kept the crown,
+ * 1 takeover; faced = the incumbent's index it was compared with (-1);
+ * delta/gate as in hxm_champion_walk.  Returns the champion's index (-1 for
+ * none), or -2 for invalid arguments (n < 0, or arms NULL with n > 0). */
+int32_t hxm_judge_round(const hxm_arm_quantiles* arms, int32_t n, int32_t control,
+                        const hxm_arm_quantiles* canary, double canary_reference_q50,
+                        hxm_round_verdict* out, int32_t* outcome, int32_t* faced,
+                        double* delta, double* gate);
 
 /* Measured tile search for one GEMM shape on the caller's operands (the
  * reference's autotune sweep + hexagon_bench + judge_champion_round,

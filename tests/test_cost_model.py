@@ -48,7 +48,8 @@ def test_prune_arithmetic_and_refusals_match_the_reference_contract():
     assert reason["ratio"] == 2000.0
     assert abs(reason["threshold"] - 2.0535714285714286) < 1e-9
     assert reason["table_rev"] == "test"
-    assert any("champion" in n for n in notes)
+    assert notes[0]["event"] == "champion" and notes[0]["tiles"] == control
+    assert notes[-1] == {"event": "summary", "kept": 2, "dropped": 1}
 
     # the control tile is immune even when it is the expensive one
     preds[control] = _fake(control, 900.0, 900.0)
@@ -90,7 +91,7 @@ def test_prune_arithmetic_and_refusals_match_the_reference_contract():
     none = {t: _fake(t, 1.0, 1.0, abstain=S.ABSTAIN_TAIL) for t in cands}
     kept, dropped, notes = S.cost_prune(cands, shape, predictions=none)
     assert dropped == [] and kept == cands
-    assert any("no priced candidate" in n for n in notes)
+    assert notes[0]["event"] == "nothing-priced"
 
     # the same partition whatever the input order; kept keeps the caller's order
     a = S.cost_prune(cands, shape, control_tile=control, predictions=preds)
@@ -106,7 +107,7 @@ def test_prune_champion_tie_breaks_on_the_config_not_the_order():
     preds = {a: _fake(a, 5.0, 5.0), b: _fake(b, 5.0, 5.0), far: _fake(far, 100.0, 100.0)}
     for order in ([a, b, far], [far, b, a]):
         kept, dropped, notes = S.cost_prune(order, (1024, 1024, 1024), predictions=preds)
-        assert notes[0].startswith("cost_prune: champion (32, 32, 32)")
+        assert notes[0]["event"] == "champion" and notes[0]["tiles"] == (32, 32, 32)
         assert [c for c, _ in dropped] == [far]
 
 

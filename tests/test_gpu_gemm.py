@@ -278,9 +278,10 @@ def _split(cfg, s):
 def test_gemm_i8_split_k_bit_exact(dev, cfg, split):
     """K split over workgroup rows: int32 partial planes summed in plane order
     are exact, so every split equals the oracle bit for bit -- with K not a
-    multiple of the slice (a short last slice) and with fewer stages than
-    splits (fewer, non-empty slices)."""
-    for M, N, K in [(300, 260, 4112), (64, 96, 640), (40, 33 * 8, 16 * 9)]:
+    multiple of the slice (a short last slice), with fewer stages than
+    splits (fewer, non-empty slices) and with N = 33 (plane rows of 132
+    bytes: the partial planes take the element-wise store path)."""
+    for M, N, K in [(300, 260, 4112), (64, 96, 640), (40, 33 * 8, 16 * 9), (72, 33, 1024)]:
         print(f"gemm_i8 split_k={split} config {cfg} M={M} N={N} K={K}", flush=True)
         A = rand_i8((M, K), 41)
         B = rand_i8((N, K), 42)
@@ -312,6 +313,32 @@ def test_gemm_i8_split_k_accumulate_dequant_and_layout(dev):
     # B as a plain [K, N] operand (packed per call into the other workspace slot)
     Bkn = B.t().contiguous()
     C = ops.gemm_i8(A.to(dev), Bkn.to(dev), b_layout="kn", config=cfg)
+    assert np.array_equal(C.cpu().numpy(), acc)
+
+
+class _RawStream:
+    """A HIP stream handle given by value (ops reads .cuda_stream)."""
+
+    def __init__(self, handle):
+        self.cuda_stream = handle
+
+
+@pytest.mark.parametrize("handle", [1, 2], ids=["hipStreamLegacy", "hipStreamPerThread"])
+def test_split_k_kn_layout_on_special_stream_handles(dev, handle):
+    """The per-stream workspace keeps the per-call B pack and the split-K
+    partial planes apart on every stream handle, including the small integer
+    handles HIP reserves (hipStreamLegacy = 1, hipStreamPerThread = 2)."""
+    M, N, K = 200, 264, 2048
+    A = rand_i8((M, K), 61)
+    B = rand_i8((N, K), 62)
+    acc = orc.gemm_i8(A.numpy(), B.numpy(), b_nk=True)
+    cfg = _split(S.gemm_configs(hxm.I8)[0], 8)
+    print(f"gemm_i8 split_k=8 kn layout on stream handle {handle}", flush=True)
+    Bkn = B.t().contiguous().to(dev)
+    Ad = A.to(dev)
+    torch.cuda.synchronize()
+    C = ops.gemm_i8(Ad, Bkn, b_layout="kn", config=cfg, stream=_RawStream(handle))
+    torch.cuda.synchronize()
     assert np.array_equal(C.cpu().numpy(), acc)
 
 

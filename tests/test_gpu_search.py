@@ -33,6 +33,13 @@ def test_tune_gemm_picks_a_verified_winner(dev, dtype, M, N, K):
     assert measured and all(c["verified"] for c in measured)
     win = rep["configs"][rep["champion"]]
     assert win["tiles"][:2] == [best.bm, best.bn]
+    # the control arm is what an untuned call runs: the default tile, unsplit
+    ctl = rep["configs"][rep["control"]]
+    assert ctl["split_k"] == 1
+    if dtype == torch.int8:
+        assert ctl["tiles"][:2] == [64, 64]
+    assert rep["start"] == "control" and rep["proof"] in (
+        "proven", "control-held", "within-gate", "void")
     # later calls with no config use the cached winner and stay correct
     if dtype == torch.int8:
         C = ops.gemm_i8(Ad, Bd, b_layout="nk").cpu().numpy()
@@ -82,15 +89,18 @@ def test_tune_cache_save_load_round_trip(dev, tmp_path):
     hxm.lib.hxm_tune_cache_clear()
 
 
-def test_cost_model_floor_holds_and_prune_keeps_the_measured_winner(dev):
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (512, 512, 16384)])
+def test_cost_model_floor_holds_and_prune_keeps_the_measured_winner(dev, M, N, K):
     """predict_tile_pcyc / cost_prune (hmx_search.py:778-1027) priced by this
     device: every measured config time is at or above its modeled lower bound,
-    and the conservative prune never drops the config measured fastest."""
+    and the conservative prune never drops the config measured fastest.  The
+    under-filled 512x512x16384 shape brings in the K-split candidates, so the
+    split terms of the model (S workgroup rows, K/S per slice, the partial
+    planes and the second launch) are held against measured times too."""
     from hxm import search as S
     from hxm._lib import I8, I32
     model = S.device_model()
     assert model.tier == 1 and model.cus > 0 and model.sclk_mhz_peak > 0
-    M = N = K = 4096
     g = torch.Generator().manual_seed(11)
     A = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
     B = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
@@ -107,6 +117,8 @@ def test_cost_model_floor_holds_and_prune_keeps_the_measured_winner(dev):
         cfg.split_k = c["split_k"]
         measured[cfg.as_tuple()] = (cfg, c["q50"])
     assert len(measured) >= 3
+    if M == 512:
+        assert any(key[6] > 1 for key in measured), "no K-split candidate was measured"
     preds = {}
     for key, (cfg, q50) in measured.items():
         p = S.predict_tile_time(M, N, K, cfg, dtype=I8, out_dtype=I32, model=model)

@@ -115,6 +115,7 @@ def test_gate_and_tie_goes_to_incumbent():
     rep = S.judge_champion_round(rows, control="ctrl", canary=_canary())
     assert rep["champion"] == "ctrl" and rep["changes"] == []
     assert rep["comparisons"][0]["outcome"] == "kept"
+    assert rep["start"] == "control" and rep["proof"] == "control-held"
 
 
 def test_challenger_takes_crown_only_past_gate():
@@ -132,6 +133,7 @@ def test_challenger_takes_crown_only_past_gate():
     assert rep["beats_control"]["significant"] is True
     assert abs(rep["beats_control"]["delta_pct"] - 30.0) < 1e-9
     assert rep["champion_significant"] is True and rep["iters"] == 300
+    assert rep["proof"] == "proven"
     noisy = [_row("ctrl", (32, 32, 32), 1000.0, spread=50.0),
              _row("A", (64, 32, 32), 700.0, spread=35.0)]
     rep = S.judge_champion_round(noisy, control="ctrl", canary=_canary())
@@ -143,11 +145,15 @@ def test_no_control_arm_is_named_not_proven():
     rows = [_row("x", (32, 32, 32), 900.0), _row("y", (64, 32, 32), 500.0)]
     rep = S.judge_champion_round(rows, canary=_canary())
     assert rep["champion"] == "y" and rep["beats_control"] is None
-    assert rep["champion_significant"] is False and "NOT-PROVEN" in rep["significance_note"]
+    assert rep["start"] == "nominal" and rep["proof"] == "no-control"
+    assert rep["champion_significant"] is False
     dead = rows + [_row("ctrl", (128, 128, 128), INF)]
     rep = S.judge_champion_round(dead, control=(128, 128, 128), canary=_canary())
     assert rep["control"] is None and rep["beats_control"] is None
-    assert "never measured" in rep["walk_note"]
+    assert rep["start"] == "control-unmeasured" and rep["champion"] is None
+    assert rep["proof"] == "no-control"
+    rep = S.judge_champion_round(rows, control="nobody", canary=_canary())
+    assert rep["start"] == "control-absent" and rep["champion"] is None
 
 
 def test_unmeasured_config_is_per_config_fact():
@@ -175,12 +181,13 @@ def test_canary_voids_round():
         assert rep["round_verdict"] == S.ROUND_INVALID_CANARY
         assert rep["champion"] == "A" and rep["champion_significant"] is False
         assert rep["beats_control"]["significant"] is False
-        assert "void" in rep["significance_note"]
+        assert rep["proof"] == "void" and rep["start"] == "control"
     ref = _canary(5000.0)
     rep = S.judge_champion_round(rows, control="ctrl", canary=_canary(8000.0),
                                  canary_reference=ref)
-    assert rep["canary"]["status"] == S.CANARY_DRIFT
-    assert "device state moved" in rep["canary"]["reason"]
+    assert rep["canary"]["status"] == S.CANARY_DRIFT and not rep["canary"]["healthy"]
+    assert abs(rep["canary"]["delta_pct"] - 60.0) < 1e-9
+    assert rep["round_verdict"] == S.ROUND_INVALID_CANARY and rep["proof"] == "void"
     assert S.canary_verdict(_canary(3000.0), ref)["status"] == S.CANARY_DRIFT
     steady = S.canary_verdict(_canary(5400.0), ref)
     assert steady["status"] == S.CANARY_OK and abs(steady["delta_pct"] - 8.0) < 1e-9

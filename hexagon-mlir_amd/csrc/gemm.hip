@@ -260,13 +260,15 @@ hxm_status pick_kernel(int32_t op, int32_t ab_dtype, int64_t M, int64_t N,
 
 }  // namespace
 
-// Shared by the entry points and the tuner.
-hxm_status run_gemm(int32_t op, int32_t ab_dtype, int epi, const void* A,
-                    int64_t lda, const void* B, int64_t ldb, int32_t b_layout,
-                    void* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
-                    int32_t out_dtype, int32_t accumulate, const float* rs,
-                    const float* cs, const hxm_gemm_config* cfg,
-                    hipStream_t stream) {
+// Shared by the entry points and the tuner.  planes / planes_cap: where a
+// K split keeps its int32 partial planes; nullptr takes the stream's
+// library-owned workspace (grown on demand).
+static hxm_status run_gemm_with(int32_t op, int32_t ab_dtype, int epi, const void* A,
+                                int64_t lda, const void* B, int64_t ldb, int32_t b_layout,
+                                void* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                int32_t out_dtype, int32_t accumulate, const float* rs,
+                                const float* cs, const hxm_gemm_config* cfg,
+                                hipStream_t stream, void* planes, size_t planes_cap) {
   const int64_t eb = dtype_bytes(ab_dtype);
   const KernelEntry* e = nullptr;
   int split = 1;
@@ -318,9 +320,15 @@ hxm_status run_gemm(int32_t op, int32_t ab_dtype, int epi, const void* A,
                     "workspace-budget: split_k=%d needs %lld bytes of int32 partial planes, "
                     "above the %lld-byte limit",
                     S, (long long)(S * plane * 4), (long long)kSplitKPlaneBytesMax);
-      void* ws = nullptr;
-      if ((st = stream_workspace(stream, static_cast<size_t>(S * plane * 4), &ws, kWsSplitK)) !=
-          HXM_OK)
+      void* ws = planes;
+      if (planes && static_cast<size_t>(S * plane * 4) > planes_cap)
+        return fail(HXM_UNSUPPORTED_SHAPE,
+                    "workspace-budget: split_k=%d needs %lld bytes of int32 partial planes, "
+                    "above the %zu-byte static scratch",
+                    S, (long long)(S * plane * 4), planes_cap);
+      if (!planes &&
+          (st = stream_workspace(stream, static_cast<size_t>(S * plane * 4), &ws, kWsSplitK)) !=
+              HXM_OK)
         return st;
       GemmArgs p = g;
       p.C = ws;
@@ -345,6 +353,46 @@ hxm_status run_gemm(int32_t op, int32_t ab_dtype, int epi, const void* A,
   if ((st = launch_gemm(*e, ab_dtype, epi, g, stream)) != HXM_OK) return st;
   return ok();
 }
+
+hxm_status run_gemm(int32_t op, int32_t ab_dtype, int epi, const void* A,
+                    int64_t lda, const void* B, int64_t ldb, int32_t b_layout,
+                    void* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                    int32_t out_dtype, int32_t accumulate, const float* rs,
+                    const float* cs, const hxm_gemm_config* cfg,
+                    hipStream_t stream) {
+  return run_gemm_with(op, ab_dtype, epi, A, lda, B, ldb, b_layout, C, ldc, M, N, K,
+                       out_dtype, accumulate, rs, cs, cfg, stream, nullptr, 0);
+}
+
+// ---- the allocation-free int8 GEMM ----
+// Its K-split partial planes live in this file-scope device array, one copy
+// per device for the life of the process.  In host code `scratch` names a
+// host-side stand-in, not device memory: its device address is looked up once
+// per device (hipGetSymbolAddress with that device current) and only that
+// address is handed to kernels.
+constexpr size_t kNoAllocScratchBytes = static_cast<size_t>(HXM_NOALLOC_SCRATCH_BYTES);
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // device address of `scratch`, per device
+
+// The current device's copy of `scratch` (looked up on the first call on it).
+hxm_status scratch_address(void** out) {
+  int dev = 0;
+  HXM_HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (static_cast<int>(g_scratch_ptr.size()) <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    HXM_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(HXM_HIP_ERROR, "hip-error: no device address for the static scratch");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return HXM_OK;
+}
+}  // namespace
 
 // ---- W8A16 GEMM (f16 x int8 [N, K]) ----
 
@@ -546,6 +594,22 @@ hxm_status hxm_gemm_i8(const int8_t* A, int64_t lda, const int8_t* B,
   return run_gemm(HXM_I8, HXM_I8, kEpiI32, A, lda, B, ldb, b_layout, C, ldc, M,
                   N, K, HXM_I32, accumulate, nullptr, nullptr, cfg,
                   as_stream(stream));
+}
+
+hxm_status hxm_gemm_i8_noalloc(const int8_t* A, int64_t lda, const int8_t* B_nk,
+                               int64_t ldb, int32_t* C, int64_t ldc, int64_t M, int64_t N,
+                               int64_t K, int32_t accumulate, const hxm_gemm_config* cfg,
+                               void* stream) {
+  hxm_status st = validate_common("gemm_i8_noalloc", A, lda, B_nk, ldb, HXM_B_NK, C, ldc, M,
+                                  N, K, 1);
+  if (st != HXM_OK) return st;
+  if ((st = require_device(nullptr)) != HXM_OK) return st;
+  if (K == 0 && accumulate) return ok();
+  void* planes = nullptr;
+  if ((st = scratch_address(&planes)) != HXM_OK) return st;
+  return run_gemm_with(HXM_I8, HXM_I8, kEpiI32, A, lda, B_nk, ldb, HXM_B_NK, C, ldc, M, N, K,
+                       HXM_I32, accumulate, nullptr, nullptr, cfg, as_stream(stream), planes,
+                       kNoAllocScratchBytes);
 }
 
 hxm_status hxm_gemm_i8_dequant(const int8_t* A, int64_t lda, const int8_t* B,

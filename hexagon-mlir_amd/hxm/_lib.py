@@ -102,6 +102,8 @@ SIGNATURES = {
     "hxm_matmul": (_st, [_p, _i64, _p, _i64, _i32, _p, _i64, _i64, _i64, _i64, _i32, _i32,
                          _i32, _cfgp, _p]),
     "hxm_gemm_i8": (_st, [_p, _i64, _p, _i64, _i32, _p, _i64, _i64, _i64, _i64, _i32, _cfgp, _p]),
+    "hxm_gemm_i8_noalloc": (_st, [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _cfgp,
+                                  _p]),
     "hxm_gemm_i8_dequant": (_st, [_p, _i64, _p, _i64, _i32, _p, _p, _p, _i64, _i64, _i64,
                                   _i64, _cfgp, _p]),
     "hxm_prepack_weight": (_st, [_p, _i64, _p, _i64, _i64, _i64, _i32, _p]),

@@ -147,6 +147,23 @@ hxm_status hxm_gemm_i8(const int8_t* A, int64_t lda, const int8_t* B,
                        int64_t M, int64_t N, int64_t K, int32_t accumulate,
                        const hxm_gemm_config* cfg, void* stream);
 
+/* hxm_gemm_i8 that allocates no device memory.  It has no counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and result as hxm_gemm_i8 with B as the resident [N,K] image
+ * (b_layout HXM_B_NK; the per-call pack of a [K,N] B would need a
+ * workspace).  A K split (cfg->split_k, or a tuned winner that has one)
+ * keeps its S*M*N int32 partial planes in a library-static device array of
+ * HXM_NOALLOC_SCRATCH_BYTES per device, which each device holds until the
+ * process ends; a split needing more is refused ("workspace-budget").
+ * Every call on a device shares that array: calls that overlap on one device
+ * (on different streams) race; calls on one stream are ordered. */
+#define HXM_NOALLOC_SCRATCH_BYTES (64ll << 20)
+hxm_status hxm_gemm_i8_noalloc(const int8_t* A, int64_t lda, const int8_t* B_nk,
+                               int64_t ldb, int32_t* C, int64_t ldc, int64_t M,
+                               int64_t N, int64_t K, int32_t accumulate,
+                               const hxm_gemm_config* cfg, void* stream);
+
 /* int8 GEMM with the fused dequant epilogue (the GPU counterpart of the
  * fused read-out convert, HMXAPI.c:36-44, with per-channel scales):
  *   C_f16[i,j] = rne_f16( ((float)acc_i32[i,j] * row_scale[i]) * col_scale[j] )

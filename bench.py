@@ -20,8 +20,15 @@ residual x + FFN(x) added in the down GEMM's epilogue), a plain
 and for context the vendor library (hipBLASLt via torch._int_mm /
 torch.matmul) on the 4096^3 shapes next to this library's f16 4096^3 matmul.
 
-cpu_baseline: the C restatement in oracle/ (OpenMP over the host cores)
-timed on a bounded row sample of the same GEMM.
+Timing: every timed launch sits between its own pair of HIP events; rates
+divide the algorithmic work by the median launch time (q20 / q80 and the mean
+are reported beside it).  HBM-bound results are also given as a fraction of
+this library's streaming probes over the same bytes (hxm_probe_copy for the
+row ops, hxm_probe_read for the GEMV): the measured practical ceiling.
+
+cpu_baseline: the C restatement in oracle/ built with -march=native on this
+host (OpenMP over the host cores) timed on a bounded row sample of the same
+GEMM; the CPU model is recorded.
 
 Warmup: the GPU's shader clock ramps up over the first ~60 ms of sustained
 load (the headline kernel goes from ~66 to ~56 us per launch over its first
@@ -66,22 +73,44 @@ class Ctx:
         self.stream = torch.cuda.current_stream().cuda_stream
 
     def time_ms(self, fn, steps, warmup, rotate=1):
-        """Average per-launch time over `steps` launches: HIP events recorded
-        on torch's current stream, the stream every launch here is issued on."""
+        """Times `steps` launches after `warmup` untimed ones.  Each launch sits
+        between its own pair of HIP events recorded on torch's current stream
+        (the stream every launch here is issued on); the loop is bracketed by
+        device synchronisations.  Returns a Timing in milliseconds."""
         torch = self.torch
         for i in range(warmup):
             fn(i % rotate)
         torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
         t0 = time.perf_counter()
-        e0.record()
         for i in range(steps):
+            ev[i][0].record()
             fn(i % rotate)
-        e1.record()
+            ev[i][1].record()
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) * 1e3 / steps
-        return e0.elapsed_time(e1) / steps, wall
+        per = [a.elapsed_time(b) for a, b in ev]
+        span = ev[0][0].elapsed_time(ev[-1][1]) / steps
+        return Timing(per, span, wall)
+
+
+class Timing:
+    """Per-launch event times (ms): median / q20 / q80 with numpy's linear
+    interpolation (the rule of hxm_quantile), their mean, the bracketed loop's
+    time per launch (launch gaps included) and the host wall time per
+    launch.  `median` is what every rate below divides by."""
+
+    def __init__(self, per, span, wall):
+        import numpy as np
+        self.per = per
+        self.median, self.q20, self.q80 = (float(np.quantile(per, q)) for q in (0.5, 0.2, 0.8))
+        self.mean = float(np.mean(per))
+        self.span, self.wall = span, wall
+
+    def us(self):
+        return {"us": self.median * 1e3, "q20_us": self.q20 * 1e3, "q80_us": self.q80 * 1e3,
+                "mean_us": self.mean * 1e3}
 
 
 def int8_operands(c):
@@ -114,11 +143,11 @@ def run_int8(c, A, Bp, rs, cs, out_i32=False):
         def step(_):
             hxm.check(L.hxm_gemm_i8_dequant(a, K, b, K, hxm.B_NK, r, s, o, N, M, N, K, None,
                                             st), "hxm_gemm_i8_dequant")
-    ms, wall = c.time_ms(step, c.args.steps, c.args.warmup)
+    t = c.time_ms(step, c.args.steps, c.args.warmup)
     c.last_step = step
     ops_per = 2.0 * M * N * K
-    return {"us": ms * 1e3, "wall_us": wall * 1e3, "TOPS": ops_per / (ms * 1e-3) / 1e12,
-            "ops_per_launch": ops_per}
+    return {**t.us(), "loop_us_per_launch": t.span * 1e3, "wall_us": t.wall * 1e3,
+            "TOPS": ops_per / (t.median * 1e-3) / 1e12, "ops_per_launch": ops_per}
 
 
 def run_f16(c):
@@ -131,8 +160,8 @@ def run_f16(c):
     def step(_):
         hxm.check(L.hxm_matmul(pa, 256, pb, 256, hxm.B_NK, pc, 256, 256, 256, 256, hxm.F16,
                                hxm.F16, 0, None, st), "hxm_matmul")
-    ms, _ = c.time_ms(step, c.args.steps, c.args.warmup)
-    return {"f16_matmul_256": {"us": ms * 1e3, "TFLOPS": 2 * 256 ** 3 / (ms * 1e-3) / 1e12,
+    t = c.time_ms(step, c.args.steps, c.args.warmup)
+    return {"f16_matmul_256": {**t.us(), "TFLOPS": 2 * 256 ** 3 / (t.median * 1e-3) / 1e12,
                                "note": "launch-bound; roofline fraction not meaningful"}}
 
 
@@ -155,11 +184,26 @@ def run_gemv(c):
         def step(i, M=M, px=px, py=py):
             hxm.check(L.hxm_gemv_w8a16(px, K, wp[i], K, hxm.W_PACKED, sp[i], py, N, M, N, K,
                                        st), "hxm_gemv_w8a16")
-        ms, _ = c.time_ms(step, 240, 24, rotate=R)
+        t = c.time_ms(step, 240, 24, rotate=R)
         nbytes = N * K + N * 2 + M * K * 2 + M * N * 2
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        out[f"w8a16_gemv_M{M}"] = {"us": ms * 1e3, "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
+        gbs = nbytes / (t.median * 1e-3) / 1e9
+        out[f"w8a16_gemv_M{M}"] = {**t.us(), "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
                                    "bytes": nbytes}
+    # The practical ceiling: this library's streaming read of the same weight
+    # bytes, over the same rotation of images.
+    sink = torch.empty(8192, dtype=torch.int32, device=c.dev)  # HXM_PROBE_SINK_WORDS
+
+    def read(i):
+        hxm.check(L.hxm_probe_read(wp[i], N * K, sink.data_ptr(), c.stream), "hxm_probe_read")
+    t = c.time_ms(read, 240, 24, rotate=R)
+    gbs = N * K / (t.median * 1e-3) / 1e9
+    out["hbm_ceiling_read_45MB"] = {**t.us(), "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
+                                    "bytes": N * K,
+                                    "what": "hxm_probe_read of one packed weight image "
+                                            "(N*K bytes), 12 images rotated"}
+    for M in (1, 4, 16):
+        rec = out[f"w8a16_gemv_M{M}"]
+        rec["ceiling_frac"] = rec["GB/s"] / gbs
     return out
 
 
@@ -187,15 +231,24 @@ def run_rows(c):
         hxm.check(L.hxm_layernorm_rows(xp[i], cols, gp, bp, yp[i], cols, mean.data_ptr(),
                                        rstd.data_ptr(), rows, cols, 1e-5, hxm.F16, st),
                   "hxm_layernorm_rows")
+    def copy(i):  # the ceiling: this library's streaming copy of the same bytes
+        hxm.check(L.hxm_probe_copy(xp[i], yp[i], rows * cols * 2, st), "hxm_probe_copy")
     out = {}
+    t = c.time_ms(copy, 200, 20, rotate=R)
+    ceil_gbs = 2 * rows * cols * 2 / (t.median * 1e-3) / 1e9
+    out["hbm_ceiling_copy_64MiB"] = {**t.us(), "GB/s": ceil_gbs,
+                                     "hbm_frac": ceil_gbs / PEAK_HBM_GBS,
+                                     "bytes": 2 * rows * cols * 2,
+                                     "what": "hxm_probe_copy of one 64 MiB row set (read + "
+                                             "write), 4 sets rotated"}
     for name, fn, nbytes in (("softmax_f16_8192x4096", softmax, 2 * rows * cols * 2),
                              ("rmsnorm_f16_8192x4096", rms, 2 * rows * cols * 2 + cols * 2),
                              ("layernorm_f16_8192x4096", layernorm,
                               2 * rows * cols * 2 + 2 * cols * 2 + 2 * rows * 4)):
-        ms, _ = c.time_ms(fn, 200, 20, rotate=R)
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        out[name] = {"us": ms * 1e3, "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
-                     "bytes": nbytes}
+        t = c.time_ms(fn, 200, 20, rotate=R)
+        gbs = nbytes / (t.median * 1e-3) / 1e9
+        out[name] = {**t.us(), "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
+                     "ceiling_frac": gbs / ceil_gbs, "bytes": nbytes}
     return out
 
 
@@ -253,17 +306,18 @@ def run_ffn(c):
     def block_residual(i):
         norm(i), gateup(i), down_residual(i)
     steps, warm = 50, 5
-    t_blk, _ = c.time_ms(block, steps, warm)
-    t_norm, _ = c.time_ms(norm, steps, warm)
-    t_gu, _ = c.time_ms(gateup, steps, warm)
-    t_d, _ = c.time_ms(down, steps, warm)
-    t_dr, _ = c.time_ms(down_residual, steps, warm)
-    t_blkr, _ = c.time_ms(block_residual, steps, warm)
+    tb = c.time_ms(block, steps, warm)
+    t_blk = tb.median
+    t_norm = c.time_ms(norm, steps, warm).median
+    t_gu = c.time_ms(gateup, steps, warm).median
+    t_d = c.time_ms(down, steps, warm).median
+    t_dr = c.time_ms(down_residual, steps, warm).median
+    t_blkr = c.time_ms(block_residual, steps, warm).median
     f_gu, f_d = 2.0 * T * H * (2 * I), 2.0 * T * I * H
     flops = f_gu + f_d
     tf = flops / (t_blk * 1e-3) / 1e12
     return {"swiglu_ffn_2048x4096x11008": {
-        "us": t_blk * 1e3, "TFLOPS": tf, "mfma_frac": tf / PEAK_F16_TFLOPS,
+        **tb.us(), "TFLOPS": tf, "mfma_frac": tf / PEAK_F16_TFLOPS,
         "gemm_flops": flops,
         "stages_us": {"rmsnorm": t_norm * 1e3, "gate_up_swiglu": t_gu * 1e3, "down": t_d * 1e3,
                       "down_with_residual": t_dr * 1e3},
@@ -290,11 +344,11 @@ def run_ragged(c):
     def step(_):
         hxm.check(L.hxm_gemm_i8_dequant(a, K, b, K, hxm.B_NK, r, s, o, 4096, M, N, K, None, st),
                   "hxm_gemm_i8_dequant")
-    ms, _ = c.time_ms(step, 200, 200)
+    t = c.time_ms(step, 200, 200)
     ops_per = 2.0 * M * N * K
     return {"int8_gemm_dequant_ragged_4000_ldc4096": {
-        "us": ms * 1e3, "TOPS": ops_per / (ms * 1e-3) / 1e12,
-        "mfma_frac": ops_per / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS}}
+        **t.us(), "TOPS": ops_per / (t.median * 1e-3) / 1e12,
+        "mfma_frac": ops_per / (t.median * 1e-3) / 1e12 / PEAK_INT8_TOPS}}
 
 
 def run_vendor(c):
@@ -310,10 +364,10 @@ def run_vendor(c):
     Bnk = Bh.t().contiguous()                       # resident [N, K] image of B
     Ch = torch.empty(n, n, dtype=torch.float16, device=c.dev)
     out = {}
-    ms, _ = c.time_ms(lambda i: torch._int_mm(A, Bt), 100, 10)
+    ms = c.time_ms(lambda i: torch._int_mm(A, Bt), 100, 10).median
     out["vendor_int_mm_4096"] = {"us": ms * 1e3, "TOPS": 2 * n ** 3 / (ms * 1e-3) / 1e12,
                                  "what": "torch._int_mm (hipBLASLt), int8 -> int32, B column-major"}
-    ms, _ = c.time_ms(lambda i: torch.matmul(Ah, Bnk.t()), 100, 10)
+    ms = c.time_ms(lambda i: torch.matmul(Ah, Bnk.t()), 100, 10).median
     out["vendor_f16_matmul_4096"] = {"us": ms * 1e3, "TFLOPS": 2 * n ** 3 / (ms * 1e-3) / 1e12,
                                      "what": "torch.matmul (hipBLASLt), f16, B = [N,K] transposed view"}
     pa, pb, pc, st = Ah.data_ptr(), Bnk.data_ptr(), Ch.data_ptr(), c.stream
@@ -321,7 +375,7 @@ def run_vendor(c):
     def f16(_):
         hxm.check(L.hxm_matmul(pa, n, pb, n, hxm.B_NK, pc, n, n, n, n, hxm.F16, hxm.F16, 0,
                                None, st), "hxm_matmul")
-    ms, _ = c.time_ms(f16, 100, 10)
+    ms = c.time_ms(f16, 100, 10).median
     out["f16_matmul_4096"] = {"us": ms * 1e3, "TFLOPS": 2 * n ** 3 / (ms * 1e-3) / 1e12,
                               "mfma_frac": 2 * n ** 3 / (ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS}
     return out
@@ -333,7 +387,7 @@ def run_copy(c):
     torch = c.torch
     src = torch.empty(1 << 28, dtype=torch.uint8, device=c.dev).fill_(1)
     dst = torch.empty_like(src)
-    ms, _ = c.time_ms(lambda i: dst.copy_(src), c.args.steps, c.args.warmup)
+    ms = c.time_ms(lambda i: dst.copy_(src), c.args.steps, c.args.warmup).median
     return {"copy_256MiB": {"us": ms * 1e3, "bytes_read": 1 << 28, "bytes_written": 1 << 28,
                             "GB/s": 2 * (1 << 28) / (ms * 1e-3) / 1e9}}
 
@@ -352,28 +406,45 @@ def measured_traffic():
     return None
 
 
+def cpu_model():
+    """The host CPU's model name (what lscpu reports as "Model name")."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(A, Bp, seconds):
+    """The C restatement (oracle/oracle.c) of the same int8 GEMM on the host
+    cores, built here with -march=native (gcc -O3 -fopenmp); the checker's
+    portable x86-64-v3 build is the fallback when no compiler is present."""
     from oracle import oracle as orc
+    native, why = orc.native_lib()
+    march = "native" if native is not None else f"x86-64-v3 (native build failed: {why})"
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     threads = max(1, min(threads, os.cpu_count() or 1))
     Ah, Bh = A.cpu().numpy(), Bp.cpu().numpy()
     M, K = Ah.shape
     N = Bh.shape[0]
     t0 = time.perf_counter()
-    orc.gemm_i8(Ah[:8], Bh, b_nk=True, threads=threads)
+    orc.gemm_i8(Ah[:8], Bh, b_nk=True, threads=threads, using=native)
     probe = max(time.perf_counter() - t0, 1e-6)
     rows = int(min(M, max(8, 8 * seconds / probe / 3)))
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
-        orc.gemm_i8(Ah[:rows], Bh, b_nk=True, threads=threads)
+        orc.gemm_i8(Ah[:rows], Bh, b_nk=True, threads=threads, using=native)
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
     return {"value": 2.0 * rows * N * K / t / 1e12, "unit": "TOPS", "cores": threads,
-            "kind": "port",
+            "kind": "port", "cpu_model": cpu_model(), "host_threads": os.cpu_count(),
+            "march": march,
             "sample": f"int8 GEMM rows 0..{rows - 1} of A[{M},{K}] x resident B[{N},{K}] -> "
-                      f"int32 (C restatement oracle/oracle.c, gcc -O3 OpenMP, {threads} "
-                      f"threads), median of 3 runs of {t:.3f} s"}
+                      f"int32 (C restatement oracle/oracle.c, gcc -O3 -march={march.split()[0]} "
+                      f"OpenMP, {threads} threads), median of 3 runs of {t:.3f} s"}
 
 
 def sclk_under_load(c, fn, seconds=1.0):
@@ -474,7 +545,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": head["us"] / 1e3,
+        "ms_per_step": head["us"] / 1e3,  # the median launch (work / median)
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -488,7 +559,11 @@ def main() -> int:
                      "traffic": measured_traffic(),
                      "traffic_source": "profiles/int8_gemm_4096_dequant.md",
                      "kernel": "gemm_kernel<int8_t,...,kEpiDequant>",
-                     "work_per_launch": head["ops_per_launch"], "avg_launch_us": head["us"],
+                     "work_per_launch": head["ops_per_launch"],
+                     "q20_us": head["q20_us"], "q50_us": head["us"], "q80_us": head["q80_us"],
+                     "avg_launch_us": head["mean_us"],
+                     "loop_us_per_launch": head["loop_us_per_launch"],
+                     "achieved_basis": "work / median per-launch event time",
                      "sclk_under_load": clk,
                      "frac_at_measured_sclk": (tops / (PEAK_INT8_TOPS * clk["median_mhz"] / 2400.0)
                                                if clk else None)},

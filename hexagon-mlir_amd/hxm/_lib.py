@@ -125,6 +125,8 @@ SIGNATURES = {
     "hxm_rmsnorm_rows": (_st, [_p, _i64, _p, _p, _i64, _i64, _i64, _f32, _i32, _p]),
     "hxm_layernorm_rows": (_st, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i64, _i64, _f32, _i32,
                                  _p]),
+    "hxm_probe_copy": (_st, [_p, _p, _i64, _p]),
+    "hxm_probe_read": (_st, [_p, _i64, _p, _p]),
     "hxm_reason_string": (ctypes.c_char_p, [_i32]),
     "hxm_tile_ladder": (_i32, [_i64, ctypes.POINTER(_i64), _i32]),
     "hxm_hmx_tile_verdict": (_i32, [_i64, _i64, _i64, _i64]),

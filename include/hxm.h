@@ -357,6 +357,19 @@ hxm_status hxm_layernorm_rows(const void* x, int64_t ldx, const void* gamma,
                               int64_t cols, float eps, int32_t dtype,
                               void* stream);
 
+/* ---- HBM probes (measurement helpers; no counterpart in the reference) ----
+ * The practical ceiling of the HBM-bound kernels above, measured with the
+ * same access pattern (16-byte nontemporal accesses, four in flight per
+ * lane).  bytes: a multiple of 16; buffers 16-byte aligned. */
+#define HXM_PROBE_SINK_WORDS 8192
+
+/* dst[0, bytes) = src[0, bytes); the buffers must not overlap. */
+hxm_status hxm_probe_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
+/* Reads src[0, bytes) and folds it; sink (at least HXM_PROBE_SINK_WORDS
+ * uint32 of device memory) receives a word only for one rare fold value. */
+hxm_status hxm_probe_read(const void* src, int64_t bytes, uint32_t* sink, void* stream);
+
 /* ---- tile search (backend/hmx_search.py) -------------------------------- */
 
 /* Reason codes shared by the two verdict functions below. */

@@ -98,16 +98,33 @@ def build() -> str:
     return _LIB_PATH
 
 
+def _load(path):
+    l = ctypes.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(l, name)
+        fn.restype = res
+        fn.argtypes = args
+    return l
+
+
+def native_lib():
+    """The same C source built for the host it runs on (-march=native), for
+    bench.py's CPU baseline only.  Returns (library, None), or (None, reason)
+    when it cannot be built here."""
+    try:
+        subprocess.run(["make", "-s", "-B", "-C", _HERE, "native"], check=True, capture_output=True,
+                       timeout=120)
+        return _load(os.path.join(_HERE, "_build", "liboracle_native.so")), None
+    except (OSError, subprocess.SubprocessError) as e:
+        return None, f"{type(e).__name__}: {e}"
+
+
 def lib():
     global _lib
     if _lib is None:
         if not os.path.exists(_LIB_PATH):
             build()
-        l = ctypes.CDLL(_LIB_PATH)
-        for name, (res, args) in _SIGS.items():
-            fn = getattr(l, name)
-            fn.restype = res
-            fn.argtypes = args
+        l = _load(_LIB_PATH)
         _lib = l
     return _lib
 
@@ -163,8 +180,9 @@ def to_f32(bits: np.ndarray, dtype) -> np.ndarray:
 
 def gemm_i8(A: np.ndarray, B: np.ndarray, *, b_nk: bool = False,
             C: np.ndarray | None = None, accumulate: bool = False,
-            threads: int = 0) -> np.ndarray:
-    """int32 C = [C +] A[M,K] . B ([K,N], or [N,K] when b_nk)."""
+            threads: int = 0, using=None) -> np.ndarray:
+    """int32 C = [C +] A[M,K] . B ([K,N], or [N,K] when b_nk).  ``using``: a
+    library from native_lib() instead of the checker build."""
     A = np.ascontiguousarray(A, dtype=np.int8)
     B = np.ascontiguousarray(B, dtype=np.int8)
     M, K = A.shape
@@ -174,8 +192,8 @@ def gemm_i8(A: np.ndarray, B: np.ndarray, *, b_nk: bool = False,
         C = np.zeros((M, N), dtype=np.int32)
     else:
         C = np.ascontiguousarray(C, dtype=np.int32).copy()
-    lib().hxo_gemm_i8(_ptr(A), K, _ptr(B), B.shape[1], int(b_nk), _ptr(C), N,
-                      M, N, K, int(accumulate), threads)
+    (using or lib()).hxo_gemm_i8(_ptr(A), K, _ptr(B), B.shape[1], int(b_nk), _ptr(C), N,
+                                 M, N, K, int(accumulate), threads)
     return C
 
 

@@ -46,38 +46,87 @@ def _gpu_present():
     return torch.cuda.is_available()
 
 
-def test_refusals_happen_before_launch():
+class _Fake:
+    """Stand-in device addresses for a machine with no GPU: every call below
+    must be refused on the host, so none of them is ever dereferenced."""
+
+    def __call__(self, nbytes):
+        return 16
+
+
+class _Real:
+    """Real device buffers of the declared sizes, for a machine with a GPU:
+    should a refusal ever regress into a launch, it stays inside them."""
+
+    def __init__(self):
+        import torch
+        self.torch, self.keep = torch, []
+
+    def __call__(self, nbytes):
+        t = self.torch.zeros(max(int(nbytes), 16), dtype=self.torch.uint8, device="cuda:0")
+        self.keep.append(t)
+        return t.data_ptr()
+
+
+def _check_refusals(buf):
     L = hxm.lib
     # int8 GEMM with K not a multiple of 16 bytes -> tile-alignment
-    st = L.hxm_gemm_i8(16, 24, 16, 24, hxm.B_NK, 16, 8, 8, 8, 24, 0, None, None)
+    st = L.hxm_gemm_i8(buf(8 * 24), 24, buf(8 * 24), 24, hxm.B_NK, buf(8 * 8 * 4), 8, 8, 8, 24,
+                       0, None, None)
     assert st == _lib.HXM_UNSUPPORTED_SHAPE
     assert hxm.last_error().startswith("tile-alignment")
     # negative extent -> invalid argument
-    st = L.hxm_gemm_i8(16, 32, 16, 32, hxm.B_NK, 16, 8, -1, 8, 32, 0, None, None)
+    st = L.hxm_gemm_i8(buf(256), 32, buf(256), 32, hxm.B_NK, buf(256), 8, -1, 8, 32, 0, None,
+                       None)
     assert st == _lib.HXM_INVALID_ARG
-    # fp32 operands are not an MFMA matmul dtype -> unsupported-dtype
-    st = L.hxm_matmul(16, 32, 16, 32, hxm.B_KN, 16, 32, 4, 4, 32, hxm.F32, hxm.F32, 0, None,
-                      None)
+    # int8 A/B with a float C is not an admitted matmul -> unsupported-dtype
+    st = L.hxm_matmul(buf(4 * 32), 32, buf(32 * 4), 4, hxm.B_KN, buf(64), 4, 4, 4, 32, hxm.I8,
+                      hxm.F16, 0, None, None)
     assert st == _lib.HXM_UNSUPPORTED_DTYPE
     assert hxm.last_error().startswith("unsupported-dtype")
     # leading dimension smaller than the row
-    st = L.hxm_softmax_rows(16, 4, 16, 8, 2, 8, hxm.F16, None)
+    st = L.hxm_softmax_rows(buf(64), 4, buf(64), 8, 2, 8, hxm.F16, None)
     assert st == _lib.HXM_INVALID_ARG
     # int8 softmax is refused
-    st = L.hxm_softmax_rows(16, 8, 16, 8, 2, 8, hxm.I8, None)
+    st = L.hxm_softmax_rows(buf(16), 8, buf(16), 8, 2, 8, hxm.I8, None)
     assert st == _lib.HXM_UNSUPPORTED_DTYPE
     # gemv: K not a multiple of 16
-    st = L.hxm_gemv_w8a16(16, 24, 16, 24, hxm.W_NK, 16, 16, 8, 1, 8, 24, None)
+    st = L.hxm_gemv_w8a16(buf(48), 24, buf(8 * 24), 24, hxm.W_NK, buf(16), buf(16), 8, 1, 8, 24,
+                          None)
     assert st == _lib.HXM_UNSUPPORTED_SHAPE
     # an unknown B layout
-    st = L.hxm_gemm_i8(16, 32, 16, 32, 7, 16, 8, 8, 8, 32, 0, None, None)
+    st = L.hxm_gemm_i8(buf(256), 32, buf(256), 32, 7, buf(256), 8, 8, 8, 32, 0, None, None)
     assert st == _lib.HXM_INVALID_ARG
-    # rows 16 MiB apart: 256 rows of a tile would span 4 GiB of 32-bit offsets
+    # HBM probes: a length that is not a multiple of 16, overlapping buffers
+    src = buf(64)
+    assert L.hxm_probe_copy(src, buf(64), 24, None) == _lib.HXM_INVALID_ARG
+    assert L.hxm_probe_copy(src, src + 16, 32, None) == _lib.HXM_INVALID_ARG
+    assert "overlap" in hxm.last_error()
+    assert L.hxm_probe_read(src, 32, None, None) == _lib.HXM_INVALID_ARG
+
+
+def _span_refusals():
+    """Rows 16 MiB apart: 256 rows of a tile would span 4 GiB of 32-bit
+    offsets (checked with stand-in addresses only: the refusal precedes any
+    use of them, and these sizes are not worth allocating)."""
+    L = hxm.lib
     st = L.hxm_gemm_i8(16, 1 << 24, 16, 32, hxm.B_NK, 16, 8, 8, 8, 32, 0, None, None)
     assert st == _lib.HXM_UNSUPPORTED_SHAPE
     assert hxm.last_error().startswith("tile-alignment") and "2 GiB" in hxm.last_error()
     st = L.hxm_gemm_w8a16(16, 32, 16, 1 << 24, 16, 16, 8, 8, 8, 32, None, None)
     assert st == _lib.HXM_UNSUPPORTED_SHAPE and "2 GiB" in hxm.last_error()
+
+
+@pytest.mark.skipif("_gpu_present()", reason="stand-in addresses are for machines without a GPU; "
+                    "test_refusals_with_device_buffers covers a GPU box")
+def test_refusals_happen_before_launch():
+    _check_refusals(_Fake())
+    _span_refusals()
+
+
+@pytest.mark.gpu
+def test_refusals_with_device_buffers():
+    _check_refusals(_Real())
 
 
 @pytest.mark.skipif("_gpu_present()")

@@ -20,9 +20,10 @@ residual x + FFN(x) added in the down GEMM's epilogue), a plain
 and for context the vendor library (hipBLASLt via torch._int_mm /
 torch.matmul) on the 4096^3 shapes next to this library's f16 4096^3 matmul.
 
-Timing: every timed launch sits between its own pair of HIP events; rates
-divide the algorithmic work by the median launch time (q20 / q80 and the mean
-are reported beside it).  HBM-bound results are also given as a fraction of
+Timing: rates divide the algorithmic work by the time per launch over the
+timed region (back-to-back launches between one pair of HIP events); further
+reps of the same launches, each between its own event pair, give the q20 /
+q50 / q80 spread reported beside it.  HBM-bound results are also given as a fraction of
 this library's streaming probes over the same bytes (hxm_probe_copy for the
 row ops, hxm_probe_read for the GEMV): the measured practical ceiling.
 
@@ -72,45 +73,52 @@ class Ctx:
         self.dev = torch.device("cuda:0")
         self.stream = torch.cuda.current_stream().cuda_stream
 
-    def time_ms(self, fn, steps, warmup, rotate=1):
-        """Times `steps` launches after `warmup` untimed ones.  Each launch sits
-        between its own pair of HIP events recorded on torch's current stream
-        (the stream every launch here is issued on); the loop is bracketed by
-        device synchronisations.  Returns a Timing in milliseconds."""
+    def time_ms(self, fn, steps, warmup, rotate=1, reps=10):
+        """Times `steps` launches after `warmup` untimed ones.
+
+        The timed region: the launches back to back on torch's current stream
+        (the stream every launch here is issued on) between one pair of HIP
+        events, bracketed by device synchronisations; its time per launch is
+        what every rate below divides by.  The spread: `reps` more reps of the
+        same `steps` back-to-back launches, each between its own event pair;
+        q20 / q50 / q80 are taken over the timed region and those reps (an
+        event pair around every single launch would put a gap between
+        launches, and the GPU's clock reacts to such gaps).  Returns a Timing
+        in milliseconds per launch."""
         torch = self.torch
         for i in range(warmup):
             fn(i % rotate)
         torch.cuda.synchronize()
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(steps)]
+
+        def rep():
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(steps):
+                fn(i % rotate)
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / steps
         t0 = time.perf_counter()
-        for i in range(steps):
-            ev[i][0].record()
-            fn(i % rotate)
-            ev[i][1].record()
-        torch.cuda.synchronize()
+        span = rep()
         wall = (time.perf_counter() - t0) * 1e3 / steps
-        per = [a.elapsed_time(b) for a, b in ev]
-        span = ev[0][0].elapsed_time(ev[-1][1]) / steps
-        return Timing(per, span, wall)
+        return Timing([span] + [rep() for _ in range(reps)], span, wall)
 
 
 class Timing:
-    """Per-launch event times (ms): median / q20 / q80 with numpy's linear
-    interpolation (the rule of hxm_quantile), their mean, the bracketed loop's
-    time per launch (launch gaps included) and the host wall time per
-    launch.  `median` is what every rate below divides by."""
+    """One workload's times in ms per launch: `span`, the timed region (the
+    rate's basis), and q20 / q50 / q80 over it and the extra reps (numpy's
+    linear interpolation, the rule of hxm_quantile)."""
 
-    def __init__(self, per, span, wall):
+    def __init__(self, per_rep, span, wall):
         import numpy as np
-        self.per = per
-        self.median, self.q20, self.q80 = (float(np.quantile(per, q)) for q in (0.5, 0.2, 0.8))
-        self.mean = float(np.mean(per))
+        self.per_rep = per_rep
+        self.median, self.q20, self.q80 = (float(np.quantile(per_rep, q)) for q in (0.5, 0.2, 0.8))
         self.span, self.wall = span, wall
 
     def us(self):
-        return {"us": self.median * 1e3, "q20_us": self.q20 * 1e3, "q80_us": self.q80 * 1e3,
-                "mean_us": self.mean * 1e3}
+        return {"us": self.span * 1e3, "q20_us": self.q20 * 1e3, "q50_us": self.median * 1e3,
+                "q80_us": self.q80 * 1e3, "reps": len(self.per_rep)}
 
 
 def int8_operands(c):
@@ -146,8 +154,8 @@ def run_int8(c, A, Bp, rs, cs, out_i32=False):
     t = c.time_ms(step, c.args.steps, c.args.warmup)
     c.last_step = step
     ops_per = 2.0 * M * N * K
-    return {**t.us(), "loop_us_per_launch": t.span * 1e3, "wall_us": t.wall * 1e3,
-            "TOPS": ops_per / (t.median * 1e-3) / 1e12, "ops_per_launch": ops_per}
+    return {**t.us(), "wall_us": t.wall * 1e3,
+            "TOPS": ops_per / (t.span * 1e-3) / 1e12, "ops_per_launch": ops_per}
 
 
 def run_f16(c):
@@ -161,7 +169,7 @@ def run_f16(c):
         hxm.check(L.hxm_matmul(pa, 256, pb, 256, hxm.B_NK, pc, 256, 256, 256, 256, hxm.F16,
                                hxm.F16, 0, None, st), "hxm_matmul")
     t = c.time_ms(step, c.args.steps, c.args.warmup)
-    return {"f16_matmul_256": {**t.us(), "TFLOPS": 2 * 256 ** 3 / (t.median * 1e-3) / 1e12,
+    return {"f16_matmul_256": {**t.us(), "TFLOPS": 2 * 256 ** 3 / (t.span * 1e-3) / 1e12,
                                "note": "launch-bound; roofline fraction not meaningful"}}
 
 
@@ -186,7 +194,7 @@ def run_gemv(c):
                                        st), "hxm_gemv_w8a16")
         t = c.time_ms(step, 240, 24, rotate=R)
         nbytes = N * K + N * 2 + M * K * 2 + M * N * 2
-        gbs = nbytes / (t.median * 1e-3) / 1e9
+        gbs = nbytes / (t.span * 1e-3) / 1e9
         out[f"w8a16_gemv_M{M}"] = {**t.us(), "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
                                    "bytes": nbytes}
     # The practical ceiling: this library's streaming read of the same weight
@@ -196,7 +204,7 @@ def run_gemv(c):
     def read(i):
         hxm.check(L.hxm_probe_read(wp[i], N * K, sink.data_ptr(), c.stream), "hxm_probe_read")
     t = c.time_ms(read, 240, 24, rotate=R)
-    gbs = N * K / (t.median * 1e-3) / 1e9
+    gbs = N * K / (t.span * 1e-3) / 1e9
     out["hbm_ceiling_read_45MB"] = {**t.us(), "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
                                     "bytes": N * K,
                                     "what": "hxm_probe_read of one packed weight image "
@@ -235,7 +243,7 @@ def run_rows(c):
         hxm.check(L.hxm_probe_copy(xp[i], yp[i], rows * cols * 2, st), "hxm_probe_copy")
     out = {}
     t = c.time_ms(copy, 200, 20, rotate=R)
-    ceil_gbs = 2 * rows * cols * 2 / (t.median * 1e-3) / 1e9
+    ceil_gbs = 2 * rows * cols * 2 / (t.span * 1e-3) / 1e9
     out["hbm_ceiling_copy_64MiB"] = {**t.us(), "GB/s": ceil_gbs,
                                      "hbm_frac": ceil_gbs / PEAK_HBM_GBS,
                                      "bytes": 2 * rows * cols * 2,
@@ -246,7 +254,7 @@ def run_rows(c):
                              ("layernorm_f16_8192x4096", layernorm,
                               2 * rows * cols * 2 + 2 * cols * 2 + 2 * rows * 4)):
         t = c.time_ms(fn, 200, 20, rotate=R)
-        gbs = nbytes / (t.median * 1e-3) / 1e9
+        gbs = nbytes / (t.span * 1e-3) / 1e9
         out[name] = {**t.us(), "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
                      "ceiling_frac": gbs / ceil_gbs, "bytes": nbytes}
     return out
@@ -306,13 +314,13 @@ def run_ffn(c):
     def block_residual(i):
         norm(i), gateup(i), down_residual(i)
     steps, warm = 50, 5
-    tb = c.time_ms(block, steps, warm)
-    t_blk = tb.median
-    t_norm = c.time_ms(norm, steps, warm).median
-    t_gu = c.time_ms(gateup, steps, warm).median
-    t_d = c.time_ms(down, steps, warm).median
-    t_dr = c.time_ms(down_residual, steps, warm).median
-    t_blkr = c.time_ms(block_residual, steps, warm).median
+    tb = c.time_ms(block, steps, warm, reps=5)
+    t_blk = tb.span
+    t_norm = c.time_ms(norm, steps, warm, reps=0).span
+    t_gu = c.time_ms(gateup, steps, warm, reps=0).span
+    t_d = c.time_ms(down, steps, warm, reps=0).span
+    t_dr = c.time_ms(down_residual, steps, warm, reps=0).span
+    t_blkr = c.time_ms(block_residual, steps, warm, reps=0).span
     f_gu, f_d = 2.0 * T * H * (2 * I), 2.0 * T * I * H
     flops = f_gu + f_d
     tf = flops / (t_blk * 1e-3) / 1e12
@@ -347,8 +355,8 @@ def run_ragged(c):
     t = c.time_ms(step, 200, 200)
     ops_per = 2.0 * M * N * K
     return {"int8_gemm_dequant_ragged_4000_ldc4096": {
-        **t.us(), "TOPS": ops_per / (t.median * 1e-3) / 1e12,
-        "mfma_frac": ops_per / (t.median * 1e-3) / 1e12 / PEAK_INT8_TOPS}}
+        **t.us(), "TOPS": ops_per / (t.span * 1e-3) / 1e12,
+        "mfma_frac": ops_per / (t.span * 1e-3) / 1e12 / PEAK_INT8_TOPS}}
 
 
 def run_vendor(c):
@@ -364,10 +372,10 @@ def run_vendor(c):
     Bnk = Bh.t().contiguous()                       # resident [N, K] image of B
     Ch = torch.empty(n, n, dtype=torch.float16, device=c.dev)
     out = {}
-    ms = c.time_ms(lambda i: torch._int_mm(A, Bt), 100, 10).median
+    ms = c.time_ms(lambda i: torch._int_mm(A, Bt), 100, 10).span
     out["vendor_int_mm_4096"] = {"us": ms * 1e3, "TOPS": 2 * n ** 3 / (ms * 1e-3) / 1e12,
                                  "what": "torch._int_mm (hipBLASLt), int8 -> int32, B column-major"}
-    ms = c.time_ms(lambda i: torch.matmul(Ah, Bnk.t()), 100, 10).median
+    ms = c.time_ms(lambda i: torch.matmul(Ah, Bnk.t()), 100, 10).span
     out["vendor_f16_matmul_4096"] = {"us": ms * 1e3, "TFLOPS": 2 * n ** 3 / (ms * 1e-3) / 1e12,
                                      "what": "torch.matmul (hipBLASLt), f16, B = [N,K] transposed view"}
     pa, pb, pc, st = Ah.data_ptr(), Bnk.data_ptr(), Ch.data_ptr(), c.stream
@@ -375,7 +383,7 @@ def run_vendor(c):
     def f16(_):
         hxm.check(L.hxm_matmul(pa, n, pb, n, hxm.B_NK, pc, n, n, n, n, hxm.F16, hxm.F16, 0,
                                None, st), "hxm_matmul")
-    ms = c.time_ms(f16, 100, 10).median
+    ms = c.time_ms(f16, 100, 10).span
     out["f16_matmul_4096"] = {"us": ms * 1e3, "TFLOPS": 2 * n ** 3 / (ms * 1e-3) / 1e12,
                               "mfma_frac": 2 * n ** 3 / (ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS}
     return out
@@ -387,7 +395,7 @@ def run_copy(c):
     torch = c.torch
     src = torch.empty(1 << 28, dtype=torch.uint8, device=c.dev).fill_(1)
     dst = torch.empty_like(src)
-    ms = c.time_ms(lambda i: dst.copy_(src), c.args.steps, c.args.warmup).median
+    ms = c.time_ms(lambda i: dst.copy_(src), c.args.steps, c.args.warmup).span
     return {"copy_256MiB": {"us": ms * 1e3, "bytes_read": 1 << 28, "bytes_written": 1 << 28,
                             "GB/s": 2 * (1 << 28) / (ms * 1e-3) / 1e9}}
 
@@ -407,14 +415,21 @@ def measured_traffic():
 
 
 def cpu_model():
-    """The host CPU's model name (what lscpu reports as "Model name")."""
+    """The host CPU's model name (what lscpu reports as "Model name") and the
+    vector extensions it exposes that the int8 loop can use."""
+    name, isa = None, []
     try:
         for line in open("/proc/cpuinfo"):
-            if line.lower().startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key = line.split(":", 1)[0].strip().lower()
+            if key == "model name" and name is None:
+                name = line.split(":", 1)[1].strip()
+            elif key == "flags" and not isa:
+                flags = set(line.split(":", 1)[1].split())
+                isa = [f for f in ("avx2", "avx512f", "avx512bw", "avx512_vnni", "avx_vnni")
+                       if f in flags]
     except OSError:
         pass
-    return None
+    return name, isa
 
 
 def cpu_baseline(A, Bp, seconds):
@@ -434,17 +449,18 @@ def cpu_baseline(A, Bp, seconds):
     probe = max(time.perf_counter() - t0, 1e-6)
     rows = int(min(M, max(8, 8 * seconds / probe / 3)))
     times = []
-    for _ in range(3):
+    for _ in range(5):
         t0 = time.perf_counter()
         orc.gemm_i8(Ah[:rows], Bh, b_nk=True, threads=threads, using=native)
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
+    model, isa = cpu_model()
     return {"value": 2.0 * rows * N * K / t / 1e12, "unit": "TOPS", "cores": threads,
-            "kind": "port", "cpu_model": cpu_model(), "host_threads": os.cpu_count(),
+            "kind": "port", "cpu_model": model, "cpu_isa": isa, "host_threads": os.cpu_count(),
             "march": march,
             "sample": f"int8 GEMM rows 0..{rows - 1} of A[{M},{K}] x resident B[{N},{K}] -> "
                       f"int32 (C restatement oracle/oracle.c, gcc -O3 -march={march.split()[0]} "
-                      f"OpenMP, {threads} threads), median of 3 runs of {t:.3f} s"}
+                      f"OpenMP, {threads} threads), median of 5 runs of {t:.3f} s"}
 
 
 def sclk_under_load(c, fn, seconds=1.0):
@@ -545,7 +561,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": head["us"] / 1e3,  # the median launch (work / median)
+        "ms_per_step": head["us"] / 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -560,10 +576,13 @@ def main() -> int:
                      "traffic_source": "profiles/int8_gemm_4096_dequant.md",
                      "kernel": "gemm_kernel<int8_t,...,kEpiDequant>",
                      "work_per_launch": head["ops_per_launch"],
-                     "q20_us": head["q20_us"], "q50_us": head["us"], "q80_us": head["q80_us"],
-                     "avg_launch_us": head["mean_us"],
-                     "loop_us_per_launch": head["loop_us_per_launch"],
-                     "achieved_basis": "work / median per-launch event time",
+                     "avg_launch_us": head["us"],
+                     "q20_us": head["q20_us"], "q50_us": head["q50_us"],
+                     "q80_us": head["q80_us"], "reps": head["reps"],
+                     "achieved_basis": "work / time per launch over the timed region (one "
+                                       "event pair around the back-to-back launches); q20 / "
+                                       "q50 / q80 over it and further reps of the same "
+                                       "launches",
                      "sclk_under_load": clk,
                      "frac_at_measured_sclk": (tops / (PEAK_INT8_TOPS * clk["median_mhz"] / 2400.0)
                                                if clk else None)},

@@ -1,6 +1,6 @@
 // HBM probes: a streaming copy and a streaming read with the same access
 // pattern as the HBM-bound kernels of this library (16-byte nontemporal
-// accesses, several in flight per lane).  They measure the practical
+// accesses, eight in flight per lane).  They measure the practical
 // ceiling those kernels are compared against; they have no counterpart in
 // the reference.
 #include "device_util.h"
@@ -11,50 +11,64 @@ namespace hxm {
 namespace {
 
 constexpr int kProbeThreads = 256;
-constexpr int kProbeUnroll = 4;  // 16-byte vectors in flight per lane
+constexpr int kProbeUnroll = 8;  // 16-byte vectors in flight per lane
+constexpr int64_t kProbeChunk = int64_t(kProbeThreads) * kProbeUnroll;  // vectors per pass
 
-// Lane `t` of `threads` handles vectors t, t + threads, ... ; each pass
-// issues kProbeUnroll loads before any store.
+// Workgroup w owns chunks w, w + groups, ... of kProbeChunk vectors; inside a
+// chunk lane t takes vectors t, t + 256, ... (every load instruction of the
+// workgroup covers 4 KiB contiguous), all kProbeUnroll loads issued before
+// any store -- the access pattern of the row kernels, one row per wave.
 __global__ __launch_bounds__(kProbeThreads) void stream_copy_kernel(
     const v4u32_t* __restrict__ src, v4u32_t* __restrict__ dst, int64_t n16) {
-  const int64_t threads = static_cast<int64_t>(gridDim.x) * kProbeThreads;
-  int64_t i = static_cast<int64_t>(blockIdx.x) * kProbeThreads + threadIdx.x;
-  for (; i + (kProbeUnroll - 1) * threads < n16; i += kProbeUnroll * threads) {
-    v4u32_t v[kProbeUnroll];
+  for (int64_t c = static_cast<int64_t>(blockIdx.x) * kProbeChunk; c < n16;
+       c += static_cast<int64_t>(gridDim.x) * kProbeChunk) {
+    const int64_t i = c + threadIdx.x;
+    if (c + kProbeChunk <= n16) {
+      v4u32_t v[kProbeUnroll];
 #pragma unroll
-    for (int u = 0; u < kProbeUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * threads);
+      for (int u = 0; u < kProbeUnroll; ++u)
+        v[u] = __builtin_nontemporal_load(src + i + u * kProbeThreads);
 #pragma unroll
-    for (int u = 0; u < kProbeUnroll; ++u) __builtin_nontemporal_store(v[u], dst + i + u * threads);
+      for (int u = 0; u < kProbeUnroll; ++u)
+        __builtin_nontemporal_store(v[u], dst + i + u * kProbeThreads);
+    } else {
+      for (int u = 0; u < kProbeUnroll; ++u)
+        if (i + u * kProbeThreads < n16)
+          __builtin_nontemporal_store(__builtin_nontemporal_load(src + i + u * kProbeThreads),
+                                      dst + i + u * kProbeThreads);
+    }
   }
-  for (; i < n16; i += threads) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
-// Folds every loaded word into one value per lane; the value is stored only
-// when it equals `never`, which the compiler cannot rule out, so the loads
-// stay and almost nothing is written.
+// The same walk, reading only: every loaded word is folded into one value
+// per lane, which is stored only when it equals `never` -- a value the
+// compiler cannot rule out, so the loads stay, and almost nothing is written.
 __global__ __launch_bounds__(kProbeThreads) void stream_read_kernel(
     const v4u32_t* __restrict__ src, int64_t n16, uint32_t never, uint32_t* __restrict__ sink) {
-  const int64_t threads = static_cast<int64_t>(gridDim.x) * kProbeThreads;
-  int64_t i = static_cast<int64_t>(blockIdx.x) * kProbeThreads + threadIdx.x;
   uint32_t acc = 0;
-  for (; i + (kProbeUnroll - 1) * threads < n16; i += kProbeUnroll * threads) {
+  for (int64_t c = static_cast<int64_t>(blockIdx.x) * kProbeChunk; c < n16;
+       c += static_cast<int64_t>(gridDim.x) * kProbeChunk) {
+    const int64_t i = c + threadIdx.x;
     v4u32_t v[kProbeUnroll];
+    if (c + kProbeChunk <= n16) {
 #pragma unroll
-    for (int u = 0; u < kProbeUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * threads);
+      for (int u = 0; u < kProbeUnroll; ++u)
+        v[u] = __builtin_nontemporal_load(src + i + u * kProbeThreads);
+    } else {
+      for (int u = 0; u < kProbeUnroll; ++u)
+        v[u] = i + u * kProbeThreads < n16 ? __builtin_nontemporal_load(src + i + u * kProbeThreads)
+                                           : v4u32_t{};
+    }
 #pragma unroll
     for (int u = 0; u < kProbeUnroll; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
-  }
-  for (; i < n16; i += threads) {
-    const v4u32_t v = __builtin_nontemporal_load(src + i);
-    acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
   }
   if (acc == never) sink[blockIdx.x] = acc;
 }
 
-// One pass of kProbeUnroll vectors per lane, capped at HXM_PROBE_SINK_WORDS
-// workgroups (32 per CU); larger buffers loop.
+// One chunk per workgroup, at most HXM_PROBE_SINK_WORDS workgroups (32 per
+// CU); larger buffers loop.
 int64_t probe_groups(int64_t n16) {
-  const int64_t want = (n16 + kProbeThreads * kProbeUnroll - 1) / (kProbeThreads * kProbeUnroll);
+  const int64_t want = (n16 + kProbeChunk - 1) / kProbeChunk;
   return want < 1 ? 1 : want > HXM_PROBE_SINK_WORDS ? HXM_PROBE_SINK_WORDS : want;
 }
 

@@ -359,7 +359,7 @@ hxm_status hxm_layernorm_rows(const void* x, int64_t ldx, const void* gamma,
 
 /* ---- HBM probes (measurement helpers; no counterpart in the reference) ----
  * The practical ceiling of the HBM-bound kernels above, measured with the
- * same access pattern (16-byte nontemporal accesses, four in flight per
+ * same access pattern (16-byte nontemporal accesses, eight in flight per
  * lane).  bytes: a multiple of 16; buffers 16-byte aligned. */
 #define HXM_PROBE_SINK_WORDS 8192
 

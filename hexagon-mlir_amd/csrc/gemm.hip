@@ -3,6 +3,7 @@
 // weight pack and the extern "C" entry points.  The kernels themselves are
 // in gemm_kernel.h, instantiated by gemm_i8.hip, gemm_f16.hip and
 // gemm_w8.hip.
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -32,6 +33,57 @@ __global__ __launch_bounds__(256) void transpose_kernel(const E* __restrict__ sr
   for (int r = ty; r < 32; r += 8) {
     const int64_t n = n0 + r, k = k0 + tx;
     if (n < N && k < K) dst[n * ldd + k] = tile[tx][r];
+  }
+}
+
+// f32 operands of a matmul enter the fp16 MFMA through these packs (the
+// reference's hmx_pack_act_f32 / hmx_pack_weight_f32, HMXAPI.h:107-137,
+// which quantise in the pack; its host prepack spells the conversion as
+// x + 0.0f -- -0 becomes +0 -- then IEEE round to nearest even,
+// hmx_weight_prepack.py:196-207).  The images are fp16 with rows of kp
+// elements, kp = K rounded up to 8 (16-byte rows for the LDS-DMA); the
+// padding columns hold +0, which adds nothing to any sum.
+__device__ __forceinline__ _Float16 f32_operand_to_f16(float x) {
+  return static_cast<_Float16>(x + 0.0f);
+}
+
+// Row-major [rows, cols] f32 (row stride ld) -> [rows, kp] f16.  Each unit
+// is 8 output elements (one 16-byte store).
+__global__ __launch_bounds__(256) void pack_f32_rows_kernel(const float* __restrict__ src,
+                                                            int64_t ld, _Float16* __restrict__ dst,
+                                                            int64_t rows, int64_t cols,
+                                                            int64_t kp) {
+  const int64_t units = rows * (kp / 8);
+  for (int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; u < units;
+       u += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t r = u / (kp / 8), c0 = (u % (kp / 8)) * 8;
+    v8f16 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      h[e] = c0 + e < cols ? f32_operand_to_f16(src[r * ld + c0 + e]) : static_cast<_Float16>(0.0f);
+    *reinterpret_cast<v8f16*>(dst + r * kp + c0) = h;
+  }
+}
+
+// [K, N] f32 (row stride ld) -> the [N, kp] f16 image, 32 x 32 tiles through
+// LDS; image columns k in [K, kp) are +0.
+__global__ __launch_bounds__(256) void pack_f32_kn_kernel(const float* __restrict__ src,
+                                                          int64_t ld, _Float16* __restrict__ dst,
+                                                          int64_t K, int64_t N, int64_t kp) {
+  __shared__ float tile[32][33];
+  const int64_t k0 = static_cast<int64_t>(blockIdx.y) * 32;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+#pragma unroll
+  for (int r = ty; r < 32; r += 8) {
+    const int64_t k = k0 + r, n = n0 + tx;
+    tile[r][tx] = k < K && n < N ? src[k * ld + n] : 0.0f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = ty; r < 32; r += 8) {
+    const int64_t n = n0 + r, k = k0 + tx;
+    if (n < N && k < kp) dst[n * kp + k] = f32_operand_to_f16(tile[tx][r]);
   }
 }
 
@@ -239,25 +291,119 @@ hxm_status resolve_b(const void* B, int64_t ldb, int32_t b_layout, int64_t K,
   return HXM_OK;
 }
 
-hxm_status pick_kernel(int32_t op, int32_t ab_dtype, int64_t M, int64_t N,
-                       int64_t K, const hxm_gemm_config* cfg,
-                       const KernelEntry** out, int* split_out) {
+// LDS of one compiled kernel (its stage buffers and scale block, as
+// gemm_kernel declares them).
+int64_t kernel_lds_bytes(const KernelEntry& e, bool b_int8, bool dequant) {
+  const int64_t bkb = e.cfg.bk;  // A bytes per stage row
+  const int64_t sb = e.cfg.bm * bkb + e.cfg.bn * (b_int8 ? bkb / 2 : bkb);
+  const int64_t qr = dequant ? (e.cfg.bm + 63) / 64 : 0;
+  const int64_t qc = (dequant || b_int8) ? (e.cfg.bn + 63) / 64 : 0;
+  const int st = e.cfg.stages;
+  return 2 * sb + (st > 2 ? sb : 1024) + (st > 3 ? sb : 1024) +
+         ((qr + qc) > 0 ? (qr + qc) * 64 * 4 : 16);
+}
+
+// Why a caller's config has no compiled kernel: the first rule of the
+// legality lattice it breaks (wildcard fields filled the way the compiled
+// configs fill them), else "no-kernel".
+int32_t explain_config(hxm_gemm_config c, int64_t a_bytes, int64_t b_bytes) {
+  if (!c.bk) c.bk = static_cast<int32_t>(128 / a_bytes);
+  if (!c.waves_m) c.waves_m = 2;
+  if (!c.waves_n) c.waves_n = 2;
+  if (!c.stages) c.stages = 2;
+  const int32_t r = gpu_lattice(c, a_bytes, b_bytes, 0);
+  return r == HXM_REASON_OK ? HXM_REASON_NO_KERNEL : r;
+}
+
+// Records a refusal in *p and as the thread's reason.
+hxm_status refuse(hxm_plan* p, hxm_status st, int32_t reason, const char* detail) {
+  p->plan = HXM_PLAN_REFUSED;
+  p->reason = reason;
+  return fail(st, "%s: %s", hxm_reason_string(reason), detail);
+}
+
+}  // namespace
+
+thread_local hxm_plan g_last_plan{};
+thread_local bool g_has_last_plan = false;
+
+// Chooses and explains the kernel of one matmul-family call (the manifest's
+// plan/reason record): the caller's config, else the tuned winner for
+// (op, M, N, K), else the shape's default; the K split it launches, its LDS,
+// the library workspace it needs and its grid.  `table` is the kernel table
+// dtype (HXM_I8 / HXM_F16 / HXM_BF16), `op` the tuning-cache key and the
+// plan's op, `epi` the epilogue, `extra_ws` workspace the caller adds (the
+// f32 operand images).  The plan is also kept as this thread's last plan.
+hxm_status plan_gemm(int32_t op, int32_t table, int epi, int32_t b_layout, int64_t M,
+                     int64_t N, int64_t K, const hxm_gemm_config* cfg, int64_t extra_ws,
+                     hxm_plan* p, const KernelEntry** entry) {
+  *p = hxm_plan{};
+  p->op = op;
+  p->m = M, p->n = N, p->k = K;
+  p->plan = HXM_PLAN_REFUSED;
+  p->k_slices = 1;
+  g_last_plan = *p;
+  g_has_last_plan = true;
+  const int64_t eb = dtype_bytes(table);
+  char why[192];
   hxm_gemm_config c;
   if (cfg && cfg->bm) {
     c = *cfg;
-  } else if (!lookup_tuned(op, M, N, K, &c)) {
-    c = default_config(M, N, ab_dtype);
+    p->source = HXM_SOURCE_CALLER;
+  } else if (lookup_tuned(op == HXM_F32 ? HXM_F16 : op, M, N, K, &c)) {
+    p->source = HXM_SOURCE_TUNED;
+  } else {
+    c = default_config(M, N, table);
+    p->source = HXM_SOURCE_DEFAULT;
   }
-  const KernelEntry* e = find_kernel(c, ab_dtype);
-  if (!e)
-    return fail(HXM_UNSUPPORTED_SHAPE,
-                "no-kernel: no compiled GEMM for bm=%d bn=%d bk=%d waves=%dx%d split_k=%d",
-                c.bm, c.bn, c.bk, c.waves_m, c.waves_n, c.split_k);
-  *out = e;
-  *split_out = c.split_k > 1 ? c.split_k : 1;
-  return HXM_OK;
+  p->config = c;
+  hxm_status st = HXM_OK;
+  const KernelEntry* e = find_kernel(c, table);
+  if (!e) {
+    snprintf(why, sizeof(why), "no compiled GEMM for bm=%d bn=%d bk=%d waves=%dx%d stages=%d",
+             c.bm, c.bn, c.bk, c.waves_m, c.waves_n, c.stages);
+    st = refuse(p, HXM_UNSUPPORTED_SHAPE, explain_config(c, eb, eb), why);
+  } else if (c.split_k > 1 && table != HXM_I8) {
+    st = refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_NO_KERNEL,
+                "split-K is compiled for int8 only");
+  }
+  if (st == HXM_OK) {
+    const int32_t split = c.split_k > 1 ? c.split_k : 1;
+    p->config = kernel_config(static_cast<int>(e - kKernels), table);
+    p->config.split_k = split;
+    p->threads = e->threads;
+    p->tiles = ((M + e->cfg.bm - 1) / e->cfg.bm) * ((N + e->cfg.bn - 1) / e->cfg.bn);
+    p->lds_bytes = kernel_lds_bytes(*e, false, epi == kEpiDequant);
+    p->workspace_bytes = extra_ws + (b_layout == HXM_B_KN && K > 0 ? N * K * eb : 0);
+    if (split > 1 && K > 0) {
+      // K in S slices of whole stages (the last may be short).
+      const int64_t bkb = e->cfg.bk;
+      const int64_t per = ((K * eb + bkb - 1) / bkb + split - 1) / split;
+      p->k_slices = static_cast<int32_t>((K * eb + per * bkb - 1) / (per * bkb));
+      if (p->k_slices > 1) p->workspace_bytes += p->k_slices * M * N * 4;
+    }
+    if (p->k_slices > 1 && p->k_slices * M * N * 4 > kSplitKPlaneBytesMax) {
+      snprintf(why, sizeof(why),
+               "split_k=%d needs %lld bytes of int32 partial planes, above the %lld-byte limit",
+               p->k_slices, (long long)(p->k_slices * M * N * 4),
+               (long long)kSplitKPlaneBytesMax);
+      st = refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_WORKSPACE_BUDGET, why);
+    } else if (!grid_fits(p->tiles, e->threads, p->k_slices)) {
+      snprintf(why, sizeof(why), "%lld x %d workgroups of %d threads exceed the launch limit",
+               (long long)p->tiles, p->k_slices, e->threads);
+      st = refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_TILE_ALIGNMENT, why);
+    } else {
+      const bool full = M % 32 == 0 && N % 32 == 0 && K % 32 == 0;
+      p->plan = full ? HXM_PLAN_MFMA_FULL : HXM_PLAN_MFMA_TAIL;
+      p->reason = full ? HXM_REASON_SELECTED_ALIGNED : HXM_REASON_SELECTED_TAIL;
+    }
+  }
+  g_last_plan = *p;
+  if (entry) *entry = st == HXM_OK ? e : nullptr;
+  return st;
 }
 
+namespace {
 }  // namespace
 
 // Shared by the entry points and the tuner.  planes / planes_cap: where a
@@ -268,14 +414,14 @@ static hxm_status run_gemm_with(int32_t op, int32_t ab_dtype, int epi, const voi
                                 void* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
                                 int32_t out_dtype, int32_t accumulate, const float* rs,
                                 const float* cs, const hxm_gemm_config* cfg,
-                                hipStream_t stream, void* planes, size_t planes_cap) {
+                                hipStream_t stream, void* planes, size_t planes_cap,
+                                int64_t extra_ws = 0) {
   const int64_t eb = dtype_bytes(ab_dtype);
   const KernelEntry* e = nullptr;
-  int split = 1;
-  hxm_status st = pick_kernel(op, ab_dtype, M, N, K, cfg, &e, &split);
+  hxm_plan plan;
+  hxm_status st = plan_gemm(op, ab_dtype, epi, b_layout, M, N, K, cfg, extra_ws, &plan, &e);
   if (st != HXM_OK) return st;
-  if (split > 1 && ab_dtype != HXM_I8)
-    return fail(HXM_UNSUPPORTED_SHAPE, "no-kernel: split-K is compiled for int8 only");
+  const int split = plan.config.split_k;
   if ((st = require_device(nullptr)) != HXM_OK) return st;
   if (M == 0 || N == 0) return ok();
   const uint8_t* bk = nullptr;
@@ -306,26 +452,24 @@ static hxm_status run_gemm_with(int32_t op, int32_t ab_dtype, int epi, const voi
     g.vec_store = (reinterpret_cast<uintptr_t>(C) % (4 * ob) == 0) && ((ldc * ob) % (4 * ob) == 0);
     g.vec8_store = (reinterpret_cast<uintptr_t>(C) % 16 == 0) && ((ldc * ob) % 16 == 0);
   }
-  if (split > 1 && K > 0) {
-    // K in S slices of whole stages; workgroup row z writes int32 plane z of
-    // a library-owned [S, M, N] buffer, then one pass sums the planes.
+  if (plan.k_slices > 1) {
+    // K in S slices of whole stages (the plan's split); workgroup row z
+    // writes int32 plane z of an [S, M, N] buffer, then one pass sums the
+    // planes.
     const int64_t bkb = e->cfg.bk;  // stage bytes
-    const int64_t per = ((K * eb + bkb - 1) / bkb + split - 1) / split;
-    const int64_t kslice = per * bkb;
-    const int S = static_cast<int>((K * eb + kslice - 1) / kslice);
-    if (S > 1) {
+    const int64_t kslice = ((K * eb + bkb - 1) / bkb + split - 1) / split * bkb;
+    const int S = plan.k_slices;
+    {
       const int64_t plane = M * N;
-      if (S * plane * 4 > kSplitKPlaneBytesMax)
-        return fail(HXM_UNSUPPORTED_SHAPE,
-                    "workspace-budget: split_k=%d needs %lld bytes of int32 partial planes, "
-                    "above the %lld-byte limit",
-                    S, (long long)(S * plane * 4), (long long)kSplitKPlaneBytesMax);
       void* ws = planes;
-      if (planes && static_cast<size_t>(S * plane * 4) > planes_cap)
+      if (planes && static_cast<size_t>(S * plane * 4) > planes_cap) {
+        g_last_plan.plan = HXM_PLAN_REFUSED;
+        g_last_plan.reason = HXM_REASON_WORKSPACE_BUDGET;
         return fail(HXM_UNSUPPORTED_SHAPE,
                     "workspace-budget: split_k=%d needs %lld bytes of int32 partial planes, "
                     "above the %zu-byte static scratch",
                     S, (long long)(S * plane * 4), planes_cap);
+      }
       if (!planes &&
           (st = stream_workspace(stream, static_cast<size_t>(S * plane * 4), &ws, kWsSplitK)) !=
               HXM_OK)
@@ -450,25 +594,67 @@ __global__ __launch_bounds__(256) void swiglu_pack_kernel(
     out_scale[r] = ch < I ? (up ? su : sg)[ch] : 0.0f;
 }
 
+// plan_gemm for the W8A16 GEMMs (f16 A, int8 [N, K] B): N is the B rows
+// (the SwiGLU image's), n_out the output columns.
+hxm_status plan_gemm_w8(int32_t op, bool sw, int64_t M, int64_t N, int64_t n_out, int64_t K,
+                        const hxm_gemm_config* cfg, hxm_plan* p, const KernelEntry** entry) {
+  *p = hxm_plan{};
+  p->op = op;
+  p->m = M, p->n = n_out, p->k = K;
+  p->plan = HXM_PLAN_REFUSED;
+  p->k_slices = 1;
+  char why[192];
+  hxm_gemm_config c;
+  if (cfg && cfg->bm) {
+    c = *cfg;
+    p->source = HXM_SOURCE_CALLER;
+  } else if (lookup_tuned(op, M, sw ? n_out : N, K, &c)) {
+    p->source = HXM_SOURCE_TUNED;
+  } else {
+    c = default_w8_config(M, N, sw);
+    p->source = HXM_SOURCE_DEFAULT;
+  }
+  p->config = c;
+  hxm_status st = HXM_OK;
+  const KernelEntry* e = find_w8_kernel(c, sw);
+  if (!e) {
+    const bool plain = find_w8_kernel(c, false) != nullptr;
+    snprintf(why, sizeof(why), "no compiled W8A16 GEMM%s for bm=%d bn=%d bk=%d waves=%dx%d",
+             sw ? " with the SwiGLU epilogue (its wave tile is 128 wide)" : "", c.bm, c.bn,
+             c.bk, c.waves_m, c.waves_n);
+    st = refuse(p, HXM_UNSUPPORTED_SHAPE,
+                plain ? HXM_REASON_NO_KERNEL : explain_config(c, 2, 1), why);
+  } else {
+    p->config = w8_kernel_config(static_cast<int>(e - kW8Kernels));
+    p->threads = e->threads;
+    p->tiles = ((M + e->cfg.bm - 1) / e->cfg.bm) * ((N + e->cfg.bn - 1) / e->cfg.bn);
+    p->lds_bytes = kernel_lds_bytes(*e, true, false);
+    if (!grid_fits(p->tiles, e->threads)) {
+      snprintf(why, sizeof(why), "%lld workgroups of %d threads exceed the launch limit",
+               (long long)p->tiles, e->threads);
+      st = refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_TILE_ALIGNMENT, why);
+    } else {
+      const bool full = M % 32 == 0 && n_out % 32 == 0 && K % 32 == 0;
+      p->plan = full ? HXM_PLAN_MFMA_FULL : HXM_PLAN_MFMA_TAIL;
+      p->reason = full ? HXM_REASON_SELECTED_ALIGNED : HXM_REASON_SELECTED_TAIL;
+    }
+  }
+  g_last_plan = *p;
+  g_has_last_plan = true;
+  if (entry) *entry = st == HXM_OK ? e : nullptr;
+  return st;
+}
+
 hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const int8_t* W,
                        int64_t ldw, const float* scale, void* C, int64_t ldc, int64_t M,
                        int64_t N, int64_t K, int64_t n_out, const hxm_gemm_config* cfg,
                        hipStream_t stream, const void* residual = nullptr, int64_t ldr = 0) {
   const bool sw = epi == kEpiSwiglu;
-  hxm_gemm_config c;
-  if (cfg && cfg->bm) {
-    c = *cfg;
-  } else if (!lookup_tuned(op, M, sw ? n_out : N, K, &c)) {
-    c = default_w8_config(M, N, sw);
-  }
-  const KernelEntry* e = find_w8_kernel(c, sw);
-  if (!e)
-    return fail(HXM_UNSUPPORTED_SHAPE,
-                "no-kernel: no compiled W8A16 GEMM%s for bm=%d bn=%d bk=%d waves=%dx%d",
-                sw ? " (SwiGLU: wave tile must be 128 wide)" : "", c.bm, c.bn, c.bk,
-                c.waves_m, c.waves_n);
-  hxm_status st = require_device(nullptr);
+  const KernelEntry* e = nullptr;
+  hxm_plan plan;
+  hxm_status st = plan_gemm_w8(op, sw, M, N, n_out, K, cfg, &plan, &e);
   if (st != HXM_OK) return st;
+  if ((st = require_device(nullptr)) != HXM_OK) return st;
   if (M == 0 || N == 0) return ok();
   GemmArgs g;
   g.A = static_cast<const uint8_t*>(x);
@@ -491,11 +677,9 @@ hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const in
   g.res_vec8 = residual && (reinterpret_cast<uintptr_t>(residual) % 16 == 0) && ((ldr * 2) % 16 == 0);
   g.vec_store = (reinterpret_cast<uintptr_t>(C) % 8 == 0) && ((ldc * 2) % 8 == 0);
   g.vec8_store = (reinterpret_cast<uintptr_t>(C) % 16 == 0) && ((ldc * 2) % 16 == 0);
-  const int64_t tiles = ((M + e->cfg.bm - 1) / e->cfg.bm) * ((N + e->cfg.bn - 1) / e->cfg.bn);
-  if ((st = check_grid("w8a16 gemm", tiles, e->threads)) != HXM_OK) return st;
   const int wi = static_cast<int>(e - kW8Kernels);
   hipLaunchKernelGGL(part_fn(kW8Parts, wi, sw ? 1 : epi == kEpiW8Res ? 2 : 0),
-                     dim3(static_cast<unsigned>(tiles)),
+                     dim3(static_cast<unsigned>(plan.tiles)),
                      dim3(e->threads), 0, stream, g);
   if ((st = check_launch("w8a16 gemm kernel")) != HXM_OK) return st;
   return ok();
@@ -533,27 +717,121 @@ using namespace hxm;
 
 extern "C" {
 
+hxm_status hxm_plan_matmul(int64_t M, int64_t N, int64_t K, int32_t a_dtype,
+                           int32_t b_dtype, int32_t c_dtype, int32_t b_layout,
+                           const hxm_gemm_config* cfg, hxm_plan* out) {
+  hxm_plan local;
+  hxm_plan* p = out ? out : &local;
+  *p = hxm_plan{};
+  p->op = a_dtype;
+  p->m = M, p->n = N, p->k = K;
+  p->plan = HXM_PLAN_REFUSED;
+  const bool i8 = a_dtype == HXM_I8 && b_dtype == HXM_I8 &&
+                  (c_dtype == HXM_I32 || c_dtype == HXM_F16);
+  const bool fl = (a_dtype == HXM_F16 || a_dtype == HXM_BF16 || a_dtype == HXM_F32) &&
+                  b_dtype == a_dtype &&
+                  (c_dtype == HXM_F16 || c_dtype == HXM_BF16 || c_dtype == HXM_F32);
+  char why[160];
+  if (!i8 && !fl) {
+    snprintf(why, sizeof(why), "a=%d b=%d c=%d", a_dtype, b_dtype, c_dtype);
+    return refuse(p, HXM_UNSUPPORTED_DTYPE, HXM_REASON_UNSUPPORTED_DTYPE, why);
+  }
+  if (M <= 0 || N <= 0 || K <= 0 || (b_layout != HXM_B_KN && b_layout != HXM_B_NK))
+    return refuse(p, HXM_INVALID_ARG, HXM_REASON_INVALID_ARGUMENT,
+                  "extents must be positive and b_layout HXM_B_KN or HXM_B_NK");
+  const int32_t table = a_dtype == HXM_F32 ? HXM_F16 : a_dtype;
+  const int64_t eb = dtype_bytes(table);
+  const int64_t kk = a_dtype == HXM_F32 ? (K + 7) / 8 * 8 : K;  // f32: the padded image
+  if ((kk * eb) % 16) {
+    snprintf(why, sizeof(why), "K*elem_bytes=%lld is not a multiple of 16", (long long)(K * eb));
+    return refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_TILE_ALIGNMENT, why);
+  }
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || kk * eb > INT32_MAX / 2 ||
+      !tile_rows_addressable(kk * eb, kk * eb))
+    return refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_TILE_ALIGNMENT,
+                  "extents beyond the 32-bit offsets of the kernels");
+  const int epi = a_dtype == HXM_I8 ? (c_dtype == HXM_F16 ? kEpiDequant : kEpiI32) : kEpiFloat;
+  const int64_t extra = a_dtype == HXM_F32 ? (M * kk * 2 + 255) / 256 * 256 + N * kk * 2 : 0;
+  // A query is not a call: the thread's last-call plan stays as it was.
+  const hxm_plan saved = g_last_plan;
+  const bool had = g_has_last_plan;
+  const hxm_status st = plan_gemm(a_dtype, table, epi, a_dtype == HXM_F32 ? HXM_B_NK : b_layout,
+                                  M, N, kk, cfg, extra, p, nullptr);
+  g_last_plan = saved;
+  g_has_last_plan = had;
+  p->k = K;
+  if (st == HXM_OK) ok();
+  return st;
+}
+
+int32_t hxm_last_plan(hxm_plan* out) {
+  if (!g_has_last_plan) return 0;
+  if (out) *out = g_last_plan;
+  return 1;
+}
+
 hxm_status hxm_query_contraction(int64_t M, int64_t N, int64_t K,
                                  int32_t a_dtype, int32_t b_dtype,
                                  int32_t c_dtype, int32_t* plan_out) {
-  if (plan_out) *plan_out = -1;
-  const bool i8 = a_dtype == HXM_I8 && b_dtype == HXM_I8 &&
-                  (c_dtype == HXM_I32 || c_dtype == HXM_F16);
-  const bool fl = (a_dtype == HXM_F16 || a_dtype == HXM_BF16) && b_dtype == a_dtype &&
-                  (c_dtype == HXM_F16 || c_dtype == HXM_BF16 || c_dtype == HXM_F32);
-  if (!i8 && !fl)
-    return fail(HXM_UNSUPPORTED_DTYPE, "unsupported-dtype: a=%d b=%d c=%d",
-                a_dtype, b_dtype, c_dtype);
-  if (M <= 0 || N <= 0 || K <= 0)
-    return fail(HXM_INVALID_ARG, "invalid-argument: extents must be positive");
-  const int64_t eb = dtype_bytes(a_dtype);
-  if ((K * eb) % 16)
+  hxm_plan p;
+  const hxm_status st = hxm_plan_matmul(M, N, K, a_dtype, b_dtype, c_dtype, HXM_B_NK, nullptr, &p);
+  if (plan_out) *plan_out = st == HXM_OK ? p.plan : -1;
+  return st;
+}
+
+static hxm_status matmul_f32(const float* A, int64_t lda, const float* B, int64_t ldb,
+                             int32_t b_layout, void* C, int64_t ldc, int64_t M, int64_t N,
+                             int64_t K, int32_t c_dtype, int32_t accumulate,
+                             const hxm_gemm_config* cfg, hipStream_t stream) {
+  if (M < 0 || N < 0 || K < 0)
+    return fail(HXM_INVALID_ARG, "invalid-argument: matmul negative extent");
+  if (b_layout != HXM_B_KN && b_layout != HXM_B_NK)
+    return fail(HXM_INVALID_ARG, "invalid-argument: matmul b_layout=%d", b_layout);
+  if (M > 0 && N > 0 && (!C || (K > 0 && (!A || !B))))
+    return fail(HXM_INVALID_ARG, "invalid-argument: matmul null operand");
+  if (lda < K || ldc < N || (b_layout == HXM_B_NK ? ldb < K : ldb < N))
+    return fail(HXM_INVALID_ARG, "invalid-argument: matmul leading dimension too small");
+  if ((K > 0 && ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3)))
+    return fail(HXM_INVALID_ARG, "invalid-argument: matmul f32 operands must be 4-byte aligned");
+  const int64_t kp = (K + 7) / 8 * 8;
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || kp * 2 > INT32_MAX / 2)
+    return fail(HXM_UNSUPPORTED_SHAPE, "tile-alignment: matmul extent beyond 2^30");
+  if (kp > 0 && !tile_rows_addressable(kp * 2, kp * 2))
     return fail(HXM_UNSUPPORTED_SHAPE,
-                "tile-alignment: K*elem_bytes=%lld is not a multiple of 16",
-                (long long)(K * eb));
-  const bool full = M % 32 == 0 && N % 32 == 0 && K % 32 == 0;
-  if (plan_out) *plan_out = full ? 0 : 1;
-  return ok();
+                "tile-alignment: matmul needs %lld rows of the fp16 operand images within 2 GiB",
+                (long long)kTileRowsMax);
+  hxm_status st = HXM_OK;
+  const int64_t a_bytes = (M * kp * 2 + 255) / 256 * 256, img_bytes = a_bytes + N * kp * 2;
+  hxm_plan plan;
+  if ((st = plan_gemm(HXM_F32, HXM_F16, kEpiFloat, HXM_B_NK, M, N, kp, cfg, img_bytes, &plan,
+                      nullptr)) != HXM_OK)
+    return st;
+  if ((st = require_device(nullptr)) != HXM_OK) return st;
+  if (M == 0 || N == 0 || (K == 0 && accumulate)) return ok();
+  void* ws = nullptr;
+  _Float16 *ai = nullptr, *bi = nullptr;
+  if (K > 0) {
+    if ((st = stream_workspace(stream, static_cast<size_t>(img_bytes), &ws)) != HXM_OK) return st;
+    ai = static_cast<_Float16*>(ws);
+    bi = reinterpret_cast<_Float16*>(static_cast<char*>(ws) + a_bytes);
+    auto blocks = [](int64_t units) {
+      return static_cast<unsigned>(std::min<int64_t>((units + 255) / 256, 65536));
+    };
+    pack_f32_rows_kernel<<<blocks(M * (kp / 8)), 256, 0, stream>>>(A, lda, ai, M, K, kp);
+    if ((st = check_launch("f32 operand pack")) != HXM_OK) return st;
+    if (b_layout == HXM_B_NK) {
+      pack_f32_rows_kernel<<<blocks(N * (kp / 8)), 256, 0, stream>>>(B, ldb, bi, N, K, kp);
+    } else {
+      if ((st = check_grid("f32 weight pack", (N + 31) / 32, 256, (kp + 31) / 32)) != HXM_OK)
+        return st;
+      const dim3 grid(static_cast<unsigned>((N + 31) / 32), static_cast<unsigned>((kp + 31) / 32));
+      pack_f32_kn_kernel<<<grid, 256, 0, stream>>>(B, ldb, bi, K, N, kp);
+    }
+    if ((st = check_launch("f32 operand pack")) != HXM_OK) return st;
+  }
+  return run_gemm_with(HXM_F32, HXM_F16, kEpiFloat, ai, kp, bi, kp, HXM_B_NK, C, ldc, M, N, kp,
+                       c_dtype, accumulate, nullptr, nullptr, cfg, stream, nullptr, 0,
+                       img_bytes);
 }
 
 hxm_status hxm_matmul(const void* A, int64_t lda, const void* B, int64_t ldb,
@@ -561,12 +839,15 @@ hxm_status hxm_matmul(const void* A, int64_t lda, const void* B, int64_t ldb,
                       int64_t N, int64_t K, int32_t ab_dtype, int32_t c_dtype,
                       int32_t accumulate, const hxm_gemm_config* cfg,
                       void* stream) {
-  if (ab_dtype != HXM_F16 && ab_dtype != HXM_BF16)
+  if (ab_dtype != HXM_F16 && ab_dtype != HXM_BF16 && ab_dtype != HXM_F32)
     return fail(HXM_UNSUPPORTED_DTYPE, "unsupported-dtype: matmul A/B dtype %d",
                 ab_dtype);
   if (c_dtype != HXM_F16 && c_dtype != HXM_BF16 && c_dtype != HXM_F32)
     return fail(HXM_UNSUPPORTED_DTYPE, "unsupported-dtype: matmul C dtype %d",
                 c_dtype);
+  if (ab_dtype == HXM_F32)
+    return matmul_f32(static_cast<const float*>(A), lda, static_cast<const float*>(B), ldb,
+                      b_layout, C, ldc, M, N, K, c_dtype, accumulate, cfg, as_stream(stream));
   hxm_status st = validate_common("matmul", A, lda, B, ldb, b_layout, C, ldc, M,
                                   N, K, 2);
   if (st != HXM_OK) return st;

@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void pack_w8a16_kernel(const int8_t* __restric
 // load lands.  PACKED reads the resident image (1 KiB contiguous per wave
 // instruction); otherwise W is the plain [N, K] matrix (16 rows x 64 bytes
 // per instruction).
-template <int KW, int SPW, bool PACKED, int MR, int CB>
+template <int KW, int SPW, bool PACKED, int MR, int CB, bool LATE_SCALES>
 __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
   constexpr int kChunkSlabs = KW * SPW;
   constexpr int kChunkK = kChunkSlabs * 64;
@@ -95,14 +95,19 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
   const int r16 = lane & 15;                    // W row (channel) for A; x row for B
   const int kq = lane >> 4;                     // 16-byte quarter of the 64-wide slab
   const int slabs = (g.K + 63) / 64;
-  // The per-channel scales wave 0 applies at the end, loaded (and converted,
-  // so every wave first waits for this one small load) before the weight
-  // stream: no dependent memory round trip sits in the kernel's tail.
-  // Measured at N=11008, K=4096: this ordering beats both the scale load in
-  // the tail and an unconverted prefetch that lets the weight loads issue
-  // at once (M=4: 10.1-10.7 us against 11.2 and 12.3-12.7 us).
+  // The per-channel scales wave 0 applies at the end.  No dependent memory
+  // round trip may sit in the kernel's tail, so they are loaded early, in one
+  // of two places.  LATE_SCALES (M <= 4): right after wave 0's weight loads
+  // of the first K chunk; loads complete in order, so by the time wave 0 has
+  // its weights the scales are there too, and nothing waits for them before
+  // the weight stream starts.  Otherwise: before the weight stream, converted
+  // at once (wave 0 waits one small round trip before issuing its weight
+  // loads).  Measured at N=11008, K=4096 (one box, 5 runs each): M=1 9.38 us
+  // late against 9.67 early, M=4 9.93 against 10.08, M=16 11.83 against
+  // 11.55; a load in the tail was slower still (M=4: 11.2 us).
   float sc[CB][4];
-  if (wave == 0) {
+  _Float16 sc_raw[CB][4];
+  if (!LATE_SCALES && wave == 0) {
 #pragma unroll
     for (int b = 0; b < CB; ++b)
 #pragma unroll
@@ -162,6 +167,15 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
         }
       }
     }
+    if (LATE_SCALES && c0 == 0 && wave == 0) {
+#pragma unroll
+      for (int b = 0; b < CB; ++b)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int no = n0 + 16 * b + 4 * kq + v;
+          sc_raw[b][v] = g.scale[no < g.N ? no : g.N - 1];
+        }
+    }
     // The previous chunk's LDS reads are done; then x goes to LDS.  These
     // barriers wait for LDS operations only, never for the weight loads.
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -199,6 +213,12 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
   for (int b = 0; b < CB; ++b) part[wave][b][lane] = acc[b];
   __syncthreads();
   if (wave != 0) return;
+  if (LATE_SCALES) {
+#pragma unroll
+    for (int b = 0; b < CB; ++b)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sc[b][v] = static_cast<float>(sc_raw[b][v]);
+  }
   // D[row = channel 4*(l/16)+v][col = m l%16]
   const int mo = m_base + (lane & 15);
   if (mo >= g.M) return;
@@ -291,16 +311,16 @@ hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W, int64_t l
   // Small M: a 4096-wide K chunk (x rows fit LDS), so at K <= 4096 each wave
   // issues all its weight loads at once and makes one memory round trip.
   if (M <= 1) {
-    if (pk) gemv_w8a16_kernel<8, 8, true, 1, 1><<<grid(1), 512, 0, s>>>(g);
-    else gemv_w8a16_kernel<8, 8, false, 1, 1><<<grid(1), 512, 0, s>>>(g);
+    if (pk) gemv_w8a16_kernel<8, 8, true, 1, 1, true><<<grid(1), 512, 0, s>>>(g);
+    else gemv_w8a16_kernel<8, 8, false, 1, 1, true><<<grid(1), 512, 0, s>>>(g);
   } else if (M <= 4) {
-    if (pk) gemv_w8a16_kernel<8, 8, true, 4, 1><<<grid(1), 512, 0, s>>>(g);
-    else gemv_w8a16_kernel<8, 8, false, 4, 1><<<grid(1), 512, 0, s>>>(g);
+    if (pk) gemv_w8a16_kernel<8, 8, true, 4, 1, true><<<grid(1), 512, 0, s>>>(g);
+    else gemv_w8a16_kernel<8, 8, false, 4, 1, true><<<grid(1), 512, 0, s>>>(g);
   } else {
     // 16 x rows: three channel groups per workgroup share each staged x
     // chunk (measured: 13.1 vs 14.7 us at N=11008, K=4096).
-    if (pk) gemv_w8a16_kernel<8, 4, true, 16, 3><<<grid(3), 512, 0, s>>>(g);
-    else gemv_w8a16_kernel<8, 4, false, 16, 3><<<grid(3), 512, 0, s>>>(g);
+    if (pk) gemv_w8a16_kernel<8, 4, true, 16, 3, false><<<grid(3), 512, 0, s>>>(g);
+    else gemv_w8a16_kernel<8, 4, false, 16, 3, false><<<grid(3), 512, 0, s>>>(g);
   }
   return check_launch("gemv_w8a16");
 }

@@ -67,6 +67,13 @@ hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out, int sl
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// The legality lattice of a GEMM config (search.hip): front-end block
+// limit, min-rows, MFMA edge and wave grid, LDS budget (0 = 160 KiB) for
+// a_bytes / b_bytes per element of A and B; HXM_REASON_OK or the first rule
+// it breaks.  Whether the config was compiled is not part of it.
+int32_t gpu_lattice(const hxm_gemm_config& c, int64_t a_bytes, int64_t b_bytes,
+                    int64_t lds_budget);
+
 // Frees the resident weight images of device `dev` (resident.hip).
 hxm_status release_images(int dev);
 

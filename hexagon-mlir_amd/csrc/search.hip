@@ -101,6 +101,29 @@ int32_t gated_walk(int32_t n, int32_t start, ArmFn arm, int32_t* outcome, int32_
   return inc;
 }
 
+// The legality lattice of a GPU GEMM config in the reference's order
+// (hmx_search.tile_verdict, hmx_search.py:269-292): front-end block limit ->
+// min-rows -> the 32-wide MFMA edge (and the wave grid) -> LDS budget, for
+// a_bytes / b_bytes bytes per element of A and B (the W8A16 kernels hold B
+// as int8).  Whether a kernel was compiled for the config is the caller's
+// last step.
+int32_t gpu_lattice(const hxm_gemm_config& c, int64_t a_bytes, int64_t b_bytes,
+                    int64_t lds_budget) {
+  const int64_t bm = c.bm, bn = c.bn, bk = c.bk;
+  if (!is_pow2(bm) || !is_pow2(bn) || !is_pow2(bk)) return HXM_REASON_FRONTEND_BLOCK_LIMIT;
+  if (bm * bk > kFrontendMaxBlockNumel || bk * bn > kFrontendMaxBlockNumel ||
+      bm * bn > kFrontendMaxBlockNumel)
+    return HXM_REASON_FRONTEND_BLOCK_LIMIT;
+  if (bm <= kMinRows) return HXM_REASON_MIN_ROWS;
+  if (bm % kTileEdge || bn % kTileEdge || bk % kTileEdge || c.waves_m <= 0 ||
+      c.waves_n <= 0 || bm % (kTileEdge * c.waves_m) || bn % (kTileEdge * c.waves_n))
+    return HXM_REASON_TILE_ALIGNMENT;
+  if (lds_budget <= 0) lds_budget = kDefaultLdsBudget;
+  const int64_t stages = c.stages > 0 ? c.stages : 2;
+  if (stages * (bm * a_bytes + bn * b_bytes) * bk > lds_budget) return HXM_REASON_LDS_BUDGET;
+  return HXM_REASON_OK;
+}
+
 // ---- the tuned-winner cache -------------------------------------------
 namespace {
 typedef std::tuple<int32_t, int64_t, int64_t, int64_t> TuneKey;
@@ -418,6 +441,10 @@ const char* hxm_reason_string(int32_t reason) {
     case HXM_REASON_LDS_BUDGET: return "lds-budget";
     case HXM_REASON_UNSUPPORTED_DTYPE: return "unsupported-dtype";
     case HXM_REASON_NO_KERNEL: return "no-kernel";
+    case HXM_REASON_SELECTED_ALIGNED: return "selected-aligned";
+    case HXM_REASON_SELECTED_TAIL: return "selected-tail";
+    case HXM_REASON_WORKSPACE_BUDGET: return "workspace-budget";
+    case HXM_REASON_INVALID_ARGUMENT: return "invalid-argument";
     default: return "unknown-reason";
   }
 }
@@ -452,19 +479,8 @@ int32_t hxm_gpu_tile_verdict(const hxm_gemm_config* cfg, int32_t ab_dtype,
   if (!cfg) return HXM_REASON_NO_KERNEL;
   const int64_t eb = (ab_dtype == HXM_I8) ? 1 : (ab_dtype == HXM_F16 || ab_dtype == HXM_BF16) ? 2 : 0;
   if (!eb) return HXM_REASON_UNSUPPORTED_DTYPE;
-  const int64_t bm = cfg->bm, bn = cfg->bn, bk = cfg->bk;
-  if (!is_pow2(bm) || !is_pow2(bn) || !is_pow2(bk)) return HXM_REASON_FRONTEND_BLOCK_LIMIT;
-  if (bm * bk > kFrontendMaxBlockNumel || bk * bn > kFrontendMaxBlockNumel ||
-      bm * bn > kFrontendMaxBlockNumel)
-    return HXM_REASON_FRONTEND_BLOCK_LIMIT;
-  if (bm <= kMinRows) return HXM_REASON_MIN_ROWS;
-  if (bm % kTileEdge || bn % kTileEdge || bk % kTileEdge || cfg->waves_m <= 0 ||
-      cfg->waves_n <= 0 || bm % (kTileEdge * cfg->waves_m) ||
-      bn % (kTileEdge * cfg->waves_n))
-    return HXM_REASON_TILE_ALIGNMENT;
-  if (lds_budget <= 0) lds_budget = kDefaultLdsBudget;
-  const int64_t stages = cfg->stages > 0 ? cfg->stages : 2;
-  if (stages * (bm + bn) * bk * eb > lds_budget) return HXM_REASON_LDS_BUDGET;
+  const int32_t lattice = gpu_lattice(*cfg, eb, eb, lds_budget);
+  if (lattice != HXM_REASON_OK) return lattice;
   for (int i = 0; i < num_kernels(); ++i) {
     const hxm_gemm_config k = kernel_config(i, ab_dtype);
     if (k.bm == cfg->bm && k.bn == cfg->bn && k.bk == cfg->bk &&

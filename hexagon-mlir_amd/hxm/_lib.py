@@ -67,6 +67,16 @@ class TilePredictionC(ctypes.Structure):
                 ("heat", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
+class Plan(ctypes.Structure):
+    """hxm_plan: one GEMM call's plan and reason."""
+    _fields_ = [("op", ctypes.c_int32), ("plan", ctypes.c_int32), ("reason", ctypes.c_int32),
+                ("source", ctypes.c_int32), ("config", GemmConfig),
+                ("k_slices", ctypes.c_int32), ("threads", ctypes.c_int32),
+                ("tiles", ctypes.c_int64), ("lds_bytes", ctypes.c_int64),
+                ("workspace_bytes", ctypes.c_int64), ("m", ctypes.c_int64),
+                ("n", ctypes.c_int64), ("k", ctypes.c_int64)]
+
+
 class ArmQuantiles(ctypes.Structure):
     """hxm_arm_quantiles: one measured arm of a search round."""
     _fields_ = [("q20", ctypes.c_double), ("q50", ctypes.c_double), ("q80", ctypes.c_double)]
@@ -99,6 +109,9 @@ SIGNATURES = {
     "hxm_device_count": (_i32, []),
     "hxm_release_cache": (_st, []),
     "hxm_query_contraction": (_st, [_i64, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(_i32)]),
+    "hxm_plan_matmul": (_st, [_i64, _i64, _i64, _i32, _i32, _i32, _i32, _cfgp,
+                              ctypes.POINTER(Plan)]),
+    "hxm_last_plan": (_i32, [ctypes.POINTER(Plan)]),
     "hxm_matmul": (_st, [_p, _i64, _p, _i64, _i32, _p, _i64, _i64, _i64, _i64, _i32, _i32,
                          _i32, _cfgp, _p]),
     "hxm_gemm_i8": (_st, [_p, _i64, _p, _i64, _i32, _p, _i64, _i64, _i64, _i64, _i32, _cfgp, _p]),

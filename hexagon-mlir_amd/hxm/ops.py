@@ -63,11 +63,15 @@ def _ptr_or_none(cfg):
 def matmul(A: torch.Tensor, B: torch.Tensor, out: Optional[torch.Tensor] = None, *,
            b_layout: str = "kn", accumulate: bool = False,
            out_dtype: Optional[torch.dtype] = None, config=None, stream=None) -> torch.Tensor:
-    """C = [C +] A @ B on f16/bf16 with fp32 accumulation (linalg.matmul).
+    """C = [C +] A @ B on f16/bf16/f32 with fp32 accumulation (linalg.matmul).
+    f32 operands are quantised to fp16 by a pack pass (x + 0.0 then round to
+    nearest even, the reference's f32 pack) and multiplied on the fp16 MFMA.
 
     ``b_layout="kn"``: B is [K, N] (packed per call); ``"nk"``: B is the
     resident [N, K] image from :func:`prepack_weight`."""
     _mat(A, "A"), _mat(B, "B")
+    if A.dtype != B.dtype:
+        raise TypeError(f"A and B must share a dtype (got {A.dtype} and {B.dtype})")
     M, K = A.shape
     N = B.shape[1] if b_layout == "kn" else B.shape[0]
     if (B.shape[0] if b_layout == "kn" else B.shape[1]) != K:
@@ -84,6 +88,45 @@ def matmul(A: torch.Tensor, B: torch.Tensor, out: Optional[torch.Tensor] = None,
                         _stream(stream))
     check(st, "hxm_matmul")
     return out
+
+
+_PLAN = {0: "mfma-full", 1: "mfma-tail", -1: "refused"}
+_SOURCE = {0: "default", 1: "tuned", 2: "caller"}
+
+
+def _plan_dict(p) -> dict:
+    return {"op": p.op, "plan": _PLAN.get(p.plan, str(p.plan)),
+            "reason": lib.hxm_reason_string(p.reason).decode(),
+            "source": _SOURCE.get(p.source, str(p.source)), "config": p.config.as_tuple(),
+            "k_slices": p.k_slices, "threads": p.threads, "tiles": p.tiles,
+            "lds_bytes": p.lds_bytes, "workspace_bytes": p.workspace_bytes,
+            "shape": (p.m, p.n, p.k)}
+
+
+def plan_matmul(M: int, N: int, K: int, dtype: torch.dtype,
+                out_dtype: Optional[torch.dtype] = None, *, b_layout: str = "nk",
+                config=None) -> dict:
+    """What a matmul call of this shape would run and why, without launching
+    (hxm_plan_matmul): plan "mfma-full" / "mfma-tail" / "refused", the
+    manifest-style reason, the config and where it came from, the K split,
+    tiles, LDS and library workspace bytes.  A refusal is reported, not
+    raised."""
+    import ctypes
+    from ._lib import Plan
+    p = Plan()
+    od = out_dtype or (torch.int32 if dtype == torch.int8 else dtype)
+    cfg = _cfg(config)
+    lib.hxm_plan_matmul(M, N, K, _DT[dtype], _DT[dtype], _DT[od],
+                        B_KN if b_layout == "kn" else B_NK, _ptr_or_none(cfg), ctypes.byref(p))
+    return _plan_dict(p)
+
+
+def last_plan() -> Optional[dict]:
+    """The plan of this thread's last matmul / GEMM call (hxm_last_plan)."""
+    import ctypes
+    from ._lib import Plan
+    p = Plan()
+    return _plan_dict(p) if lib.hxm_last_plan(ctypes.byref(p)) else None
 
 
 def gemm_i8(A: torch.Tensor, B: torch.Tensor, out: Optional[torch.Tensor] = None, *,

@@ -107,13 +107,62 @@ hxm_status hxm_release_cache(void);
 
 /* ---- admission (HmxTarget::queryContraction, HmxTarget.h:195-218) ----- */
 
-/* Plans a matmul without launching.  plan_out receives 0 = "mfma-full"
- * (every extent a multiple of the 32-wide MFMA edge), 1 = "mfma-tail"
- * (handled with masked edge tiles), -1 = refused (status says why).
+/* Plans a matmul without launching: the answer of hxm_plan_matmul with the
+ * library's own choice of kernel.  plan_out receives 0 = "mfma-full" (every
+ * extent a multiple of the 32-wide MFMA edge), 1 = "mfma-tail" (handled with
+ * masked edge tiles), -1 = refused (status and hxm_last_error say why).
  * Unlike the reference's engine the GPU path admits int8 and tails. */
 hxm_status hxm_query_contraction(int64_t M, int64_t N, int64_t K,
                                  int32_t a_dtype, int32_t b_dtype,
                                  int32_t c_dtype, int32_t* plan_out);
+
+/* The plan of one GEMM call, and why (the manifest's plan/reason record,
+ * HmxManifest.h:78-100; HmxTarget::queryContraction, HmxTarget.h:195-218).
+ *   plan: HXM_PLAN_MFMA_FULL ("full-hmx"'s counterpart), HXM_PLAN_MFMA_TAIL
+ *         ("hmx-tail"), HXM_PLAN_REFUSED (the reference would fall back to
+ *         "hvx"; here the call is refused, there is no CPU path);
+ *   reason: HXM_REASON_SELECTED_ALIGNED / _SELECTED_TAIL for an admitted
+ *         call, else the refusal: unsupported-dtype, invalid-argument,
+ *         tile-alignment, min-rows, frontend-block-limit, lds-budget,
+ *         workspace-budget, no-kernel (hxm_reason_string names each). */
+enum { HXM_PLAN_MFMA_FULL = 0, HXM_PLAN_MFMA_TAIL = 1, HXM_PLAN_REFUSED = -1 };
+/* Where the kernel config came from. */
+enum { HXM_SOURCE_DEFAULT = 0, HXM_SOURCE_TUNED = 1, HXM_SOURCE_CALLER = 2 };
+
+typedef struct hxm_plan {
+  int32_t op;              /* HXM_I8 / HXM_F16 / HXM_BF16 / HXM_F32 (operand dtype of a
+                              matmul) or HXM_OP_W8A16 / HXM_OP_W8A16_SWIGLU */
+  int32_t plan;            /* HXM_PLAN_* */
+  int32_t reason;          /* HXM_REASON_* */
+  int32_t source;          /* HXM_SOURCE_* */
+  hxm_gemm_config config;  /* the compiled config that runs (split_k = the K split
+                              asked for, 1 for none) */
+  int32_t k_slices;        /* workgroup rows along K actually launched (1 = unsplit) */
+  int32_t threads;         /* threads per workgroup */
+  int64_t tiles;           /* output tiles (workgroups per K slice) */
+  int64_t lds_bytes;       /* LDS per workgroup */
+  int64_t workspace_bytes; /* library-owned device bytes the call uses (B pack,
+                              split-K planes) */
+  int64_t m, n, k;         /* the shape planned */
+} hxm_plan;
+
+/* Plans C[M,N] = A[M,K] . B without launching, exactly as the matmul entry
+ * points would run it: a_dtype == b_dtype in {I8, F16, BF16, F32};
+ * c_dtype I32 or F16 for I8 operands (F16 = the dequant epilogue), F16 / BF16
+ * / F32 otherwise; b_layout as the call's (HXM_B_KN costs a pack
+ * workspace); cfg NULL or zeroed = the library's choice (tuned winner, else
+ * the default), else that config.  Operands are taken densely packed
+ * (lda = ldb = K).  Fills *out (also for a refusal: plan
+ * HXM_PLAN_REFUSED and the reason) and returns the status the call would
+ * return. */
+hxm_status hxm_plan_matmul(int64_t M, int64_t N, int64_t K, int32_t a_dtype,
+                           int32_t b_dtype, int32_t c_dtype, int32_t b_layout,
+                           const hxm_gemm_config* cfg, hxm_plan* out);
+
+/* The plan of the last matmul / GEMM call on this host thread that got as
+ * far as choosing a kernel (hxm_matmul, hxm_gemm_i8*, hxm_gemm_w8a16*):
+ * returns 1 and fills *out, or 0 when there is none. */
+int32_t hxm_last_plan(hxm_plan* out);
 
 /* ---- matmuls ------------------------------------------------------------ */
 
@@ -381,7 +430,11 @@ enum {
   HXM_REASON_VTCM_BUDGET = 4,
   HXM_REASON_LDS_BUDGET = 5,
   HXM_REASON_UNSUPPORTED_DTYPE = 6,
-  HXM_REASON_NO_KERNEL = 7
+  HXM_REASON_NO_KERNEL = 7,
+  HXM_REASON_SELECTED_ALIGNED = 8,  /* "selected-aligned" */
+  HXM_REASON_SELECTED_TAIL = 9,     /* "selected-tail" */
+  HXM_REASON_WORKSPACE_BUDGET = 10, /* "workspace-budget" */
+  HXM_REASON_INVALID_ARGUMENT = 11  /* "invalid-argument" */
 };
 
 /* Reason code -> the reference's vocabulary string ("ok", "min-rows", ...). */

@@ -147,7 +147,10 @@ def test_query_contraction_plans():
     assert L.hxm_query_contraction(64, 64, 40, hxm.I8, hxm.I8, hxm.I32,
                                    ctypes.byref(plan)) == _lib.HXM_UNSUPPORTED_SHAPE
     assert plan.value == -1
+    # f32 operands are admitted (quantised to fp16 by the pack, HMXAPI.h:107-137)
     assert L.hxm_query_contraction(64, 64, 64, hxm.F32, hxm.F32, hxm.F32,
+                                   ctypes.byref(plan)) == 0 and plan.value == 0
+    assert L.hxm_query_contraction(64, 64, 64, hxm.I8, hxm.F16, hxm.F32,
                                    ctypes.byref(plan)) == _lib.HXM_UNSUPPORTED_DTYPE
 
 

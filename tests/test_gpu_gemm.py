@@ -348,3 +348,71 @@ def test_split_k_is_int8_only(dev):
     cfg = _split(S.gemm_configs(hxm.F16)[0], 2)
     with pytest.raises(hxm.HxmError):
         ops.matmul(A, B, b_layout="nk", config=cfg)
+
+
+# ---- f32 operands: quantised to fp16 in the pack (HMXAPI.h:107-137) --------
+
+def _f16_image(x):
+    """The reference's f32 pack spelled in numpy: x + 0.0 (-0 -> +0), then
+    IEEE round to nearest even (numpy's float16 cast)."""
+    return (x.astype(np.float32) + np.float32(0.0)).astype(np.float16)
+
+
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+@pytest.mark.parametrize("M,N,K", [(64, 96, 256), (100, 60, 36), (33, 17, 5)])
+def test_matmul_f32_operands_against_the_oracle(dev, layout, M, N, K):
+    print(f"matmul f32 {layout} M={M} N={N} K={K}", flush=True)
+    g = torch.Generator().manual_seed(M * 7 + K)
+    A = (torch.rand(M, K, generator=g) * 2 - 1).float().numpy()
+    B = (torch.rand(K, N, generator=g) * 2 - 1).float().numpy()
+    Bl = B if layout == "kn" else np.ascontiguousarray(B.T)
+    for od in (torch.float32, torch.float16):
+        C = ops.matmul(torch.from_numpy(A).to(dev), torch.from_numpy(Bl).to(dev),
+                       b_layout=layout, out_dtype=od).float().cpu().numpy()
+        a16 = _f16_image(A).view(np.uint16)
+        b16 = _f16_image(B).view(np.uint16)
+        ref = orc.f16_bits_to_f32(orc.matmul(a16, b16)) if od == torch.float16 else \
+            orc.matmul(a16, b16, c_dtype="f32")
+        np.testing.assert_allclose(C, ref, rtol=1e-2, atol=1e-3)
+
+
+def test_matmul_f32_rounds_to_nearest_even_in_the_pack(dev):
+    """Halfway points between fp16 neighbours: with B the identity, C is A's
+    fp16 image itself (one product per output, the others exactly zero), so
+    round-to-nearest-even is checked bit for bit (truncation or rounding half
+    up would give the other neighbour)."""
+    ulp = 2.0 ** -10
+    vals = np.array([1 + ulp / 2, 1 + 1.5 * ulp, -(1 + 1.5 * ulp), 2048 + 1, 3 + 0.75 * ulp,
+                     -0.0, 65504.0, 1e-8, -1e-8, 0.1, -0.3, 7.0], dtype=np.float32)
+    K = 16
+    A = np.zeros((8, K), dtype=np.float32)
+    A.flat[:vals.size] = vals
+    A[4:] = np.random.default_rng(5).uniform(-4, 4, (4, K)).astype(np.float32)
+    eye = np.eye(K, dtype=np.float32)
+    C = ops.matmul(torch.from_numpy(A).to(dev), torch.from_numpy(eye).to(dev),
+                   out_dtype=torch.float16).cpu().numpy()
+    want = _f16_image(A)
+    # Exact bits wherever the image is nonzero; a zero's sign cannot survive
+    # the fp32 sum (it starts at +0), so zeros are compared as values.
+    nz = want.astype(np.float32) != 0
+    assert np.array_equal(C.view(np.uint16)[nz], want.view(np.uint16)[nz])
+    assert np.all(C[~nz] == 0)
+    assert C[0, 0] == np.float16(1.0) and C[0, 1] == np.float16(1 + 2 * ulp)
+
+
+def test_last_plan_records_each_call(dev):
+    A = rand_i8((96, 256), 71).to(dev)
+    B = rand_i8((80, 256), 72).to(dev)
+    cfg = S.gemm_configs(hxm.I8)[1]
+    ops.gemm_i8(A, B, b_layout="nk", config=cfg)
+    p = ops.last_plan()
+    assert p["op"] == hxm.I8 and p["source"] == "caller" and p["plan"] == "mfma-tail"
+    assert p["config"][:6] == cfg.as_tuple()[:6] and p["shape"] == (96, 80, 256)
+    with pytest.raises(hxm.HxmError, match="lds-budget"):
+        ops.gemm_i8(A, B, b_layout="nk", config=(512, 512, 256, 2, 2, 2, 1))
+    p = ops.last_plan()
+    assert p["plan"] == "refused" and p["reason"] == "lds-budget"
+    x = torch.randn(64, 256, device=dev).half()
+    ops.gemm_w8a16(x, B, torch.rand(80, device=dev))
+    p = ops.last_plan()
+    assert p["op"] == hxm._lib.OP_W8A16 and p["plan"] == "mfma-tail" and p["threads"] > 0

@@ -389,6 +389,56 @@ def run_vendor(c):
     return out
 
 
+def run_search(c):
+    """The measured tile search (hxm_tune_gemm) on the 4096^3 shapes: every
+    compiled config -- both wave grids of the large tiles -- timed and checked
+    against the control (the untuned default); then the winner and the
+    default are timed with the headline's protocol (the int8 one with the
+    dequant epilogue).  The tuning cache is cleared afterwards, so nothing
+    else in this bench runs a tuned tile."""
+    import ctypes
+    torch, hxm, L, ops = c.torch, c.hxm, c.L, c.ops
+    n = 4096
+    out = {}
+    A, Bp, rs, cs = int8_operands(c)
+    Ah = (torch.rand(n, n, device=c.dev) * 2 - 1).half()
+    Bh = ops.prepack_weight((torch.rand(n, n, device=c.dev) * 2 - 1).half())
+    C32 = torch.empty(n, n, dtype=torch.int32, device=c.dev)
+    C16 = torch.empty(n, n, dtype=torch.float16, device=c.dev)
+    st = c.stream
+    for name, a, b, cc in (("int8", A, Bp, C32), ("f16", Ah, Bh, C16)):
+        best, rep = ops.tune_gemm(a, b, cc, reps=10)
+        ctl = rep["configs"][rep["control"]]
+        control = hxm.GemmConfig(*ctl["tiles"], *ctl["waves"], ctl["stages"], ctl["split_k"])
+
+        def step(_, cfg=None):
+            if name == "int8":
+                hxm.check(L.hxm_gemm_i8_dequant(a.data_ptr(), n, b.data_ptr(), n, hxm.B_NK,
+                                                rs.data_ptr(), cs.data_ptr(), C16.data_ptr(), n,
+                                                n, n, n, ctypes.byref(cfg), st), "dequant")
+            else:
+                hxm.check(L.hxm_matmul(a.data_ptr(), n, b.data_ptr(), n, hxm.B_NK,
+                                       C16.data_ptr(), n, n, n, n, hxm.F16, hxm.F16, 0,
+                                       ctypes.byref(cfg), st), "matmul")
+        t_best = c.time_ms(lambda i: step(i, best), 100, 200, reps=4)
+        t_ctl = c.time_ms(lambda i: step(i, control), 100, 200, reps=4)
+        work = 2.0 * n ** 3
+        out[f"search_{name}_4096"] = {
+            "winner": list(best.as_tuple()), "default": list(control.as_tuple()),
+            "winner_us": t_best.span * 1e3, "default_us": t_ctl.span * 1e3,
+            "winner_rate": work / (t_best.span * 1e-3) / 1e12,
+            "default_rate": work / (t_ctl.span * 1e-3) / 1e12,
+            "proof": rep.get("proof"), "start": rep.get("start"),
+            "configs": [{"tiles": r["tiles"], "waves": r["waves"], "stages": r["stages"],
+                         "q50_us": r["q50"], "verified": r["verified"]}
+                        for r in rep["configs"]],
+            "what": "hxm_tune_gemm over every compiled config (" + name + " -> " +
+                    ("int32" if name == "int8" else "f16") + "); winner and default then "
+                    "timed on the " + ("dequant GEMM" if name == "int8" else "f16 matmul")}
+    L.hxm_tune_cache_clear()
+    return out
+
+
 def run_copy(c):
     """A plain 256 MiB device copy (torch's elementwise copy kernel): the
     known-size reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE."""
@@ -518,7 +568,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", choices=["int8", "int8_i32", "f16", "ragged", "gemv", "rows", "ffn",
-                                       "copy", "vendor"])
+                                       "copy", "vendor", "search"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build is the single-GPU kernel set of the hot "
@@ -532,7 +582,7 @@ def main() -> int:
             rec = {args.only: run_int8(c, *int8_operands(c), out_i32=args.only == "int8_i32")}
         else:
             rec = {"f16": run_f16, "ragged": run_ragged, "gemv": run_gemv, "rows": run_rows,
-                   "ffn": run_ffn, "copy": run_copy, "vendor": run_vendor}[
+                   "ffn": run_ffn, "copy": run_copy, "vendor": run_vendor, "search": run_search}[
                 args.only](c)
         print(json.dumps(rec), flush=True)
         return 0
@@ -545,7 +595,8 @@ def main() -> int:
     extra = {}
     if not args.no_extra:
         extra["int8_gemm_i32_out_4096"] = run_int8(c, A, Bp, rs, cs, out_i32=True)
-        for fn in (run_f16, run_ragged, run_gemv, run_rows, run_ffn, run_copy, run_vendor):
+        for fn in (run_f16, run_ragged, run_gemv, run_rows, run_ffn, run_copy, run_vendor,
+                   run_search):
             extra.update(fn(c))
         for k, v in extra.items():
             log(k, json.dumps(v))

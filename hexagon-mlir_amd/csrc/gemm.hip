@@ -208,10 +208,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(
 
 namespace {
 
-// The kernels address a tile's rows of an operand with 32-bit offsets from
-// the tile's first row, inside a buffer resource of at most 2 GiB: the
-// kTileRowsMax rows of the tallest tile must span less than that.
-constexpr int64_t kTileRowsMax = 256;
+// kTileRowsMax (host_logic.h) bounds the tallest compiled tile.
 #define HXM_TILE_EDGE(BM, BN, BKB, ST, WM, WN) ((BM) > (BN) ? (BM) : (BN))
 constexpr int kTileEdges[] = {HXM_GEMM_CONFIG_LIST(HXM_TILE_EDGE),
                               HXM_W8_CONFIG_LIST(HXM_TILE_EDGE)};
@@ -223,9 +220,6 @@ constexpr bool tile_edges_fit() {
 }
 static_assert(tile_edges_fit(), "a compiled tile is taller than kTileRowsMax");
 
-bool tile_rows_addressable(int64_t ld_bytes, int64_t row_bytes) {
-  return ld_bytes <= (INT32_MAX - row_bytes) / (kTileRowsMax - 1);
-}
 
 hxm_status validate_common(const char* op, const void* A, int64_t lda,
                            const void* B, int64_t ldb, int32_t b_layout,
@@ -241,7 +235,7 @@ hxm_status validate_common(const char* op, const void* A, int64_t lda,
       (b_layout == HXM_B_NK ? ldb < K : ldb < N))
     return fail(HXM_INVALID_ARG, "invalid-argument: %s leading dimension too small",
                 op);
-  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K * eb > INT32_MAX / 2)
+  if (!extents_fit(M, N, K, eb))
     return fail(HXM_UNSUPPORTED_SHAPE, "tile-alignment: %s extent beyond 2^30", op);
   // A [K,N] B is packed into an [N,K] image with rows of K elements.
   const int64_t ldb_image = b_layout == HXM_B_NK ? ldb : K;
@@ -375,13 +369,8 @@ hxm_status plan_gemm(int32_t op, int32_t table, int epi, int32_t b_layout, int64
     p->tiles = ((M + e->cfg.bm - 1) / e->cfg.bm) * ((N + e->cfg.bn - 1) / e->cfg.bn);
     p->lds_bytes = kernel_lds_bytes(*e, false, epi == kEpiDequant);
     p->workspace_bytes = extra_ws + (b_layout == HXM_B_KN && K > 0 ? N * K * eb : 0);
-    if (split > 1 && K > 0) {
-      // K in S slices of whole stages (the last may be short).
-      const int64_t bkb = e->cfg.bk;
-      const int64_t per = ((K * eb + bkb - 1) / bkb + split - 1) / split;
-      p->k_slices = static_cast<int32_t>((K * eb + per * bkb - 1) / (per * bkb));
-      if (p->k_slices > 1) p->workspace_bytes += p->k_slices * M * N * 4;
-    }
+    p->k_slices = k_slices(K * eb, e->cfg.bk, split);
+    if (p->k_slices > 1) p->workspace_bytes += p->k_slices * M * N * 4;
     if (p->k_slices > 1 && p->k_slices * M * N * 4 > kSplitKPlaneBytesMax) {
       snprintf(why, sizeof(why),
                "split_k=%d needs %lld bytes of int32 partial planes, above the %lld-byte limit",
@@ -746,8 +735,7 @@ hxm_status hxm_plan_matmul(int64_t M, int64_t N, int64_t K, int32_t a_dtype,
     snprintf(why, sizeof(why), "K*elem_bytes=%lld is not a multiple of 16", (long long)(K * eb));
     return refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_TILE_ALIGNMENT, why);
   }
-  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || kk * eb > INT32_MAX / 2 ||
-      !tile_rows_addressable(kk * eb, kk * eb))
+  if (!extents_fit(M, N, kk, eb) || !tile_rows_addressable(kk * eb, kk * eb))
     return refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_TILE_ALIGNMENT,
                   "extents beyond the 32-bit offsets of the kernels");
   const int epi = a_dtype == HXM_I8 ? (c_dtype == HXM_F16 ? kEpiDequant : kEpiI32) : kEpiFloat;
@@ -794,7 +782,7 @@ static hxm_status matmul_f32(const float* A, int64_t lda, const float* B, int64_
   if ((K > 0 && ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3)))
     return fail(HXM_INVALID_ARG, "invalid-argument: matmul f32 operands must be 4-byte aligned");
   const int64_t kp = (K + 7) / 8 * 8;
-  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || kp * 2 > INT32_MAX / 2)
+  if (!extents_fit(M, N, kp, 2))
     return fail(HXM_UNSUPPORTED_SHAPE, "tile-alignment: matmul extent beyond 2^30");
   if (kp > 0 && !tile_rows_addressable(kp * 2, kp * 2))
     return fail(HXM_UNSUPPORTED_SHAPE,

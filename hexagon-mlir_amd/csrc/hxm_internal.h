@@ -11,6 +11,7 @@
 #include <string>
 
 #include "../../include/hxm.h"
+#include "host_logic.h"
 
 namespace hxm {
 
@@ -37,12 +38,6 @@ inline bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
-// A launch holds at most 2^32 - 1 work-items along x (workgroups times
-// threads) and, as used here, at most 65535 workgroups along y.
-inline bool grid_fits(int64_t groups_x, int threads, int64_t groups_y = 1) {
-  return groups_x >= 0 && groups_x <= 0xffffffffLL / threads && groups_y >= 0 &&
-         groups_y <= 65535;
-}
 
 // Refuses a launch that grid_fits rejects ("tile-alignment"); HXM_OK otherwise.
 hxm_status check_grid(const char* what, int64_t groups_x, int threads, int64_t groups_y = 1);

@@ -710,26 +710,14 @@ hxm_status hxm_tune_cache_load(const char* path, int32_t* loaded) {
       }
       continue;
     }
-    // Every field is read as 64-bit and range-checked before it narrows, so
-    // an out-of-range value cannot wrap onto a compiled configuration.
-    long long v[12];
-    if (std::sscanf(line, "%lld %lld %lld %lld %lld %lld %lld %lld %lld %lld %lld %lld", &v[0],
-                    &v[1], &v[2], &v[3], &v[4], &v[5], &v[6], &v[7], &v[8], &v[9], &v[10],
-                    &v[11]) != 12)
-      continue;
-    bool in_range = v[0] >= 0 && v[0] <= INT32_MAX && v[11] >= 1 && v[11] <= 10000;
-    for (int i = 1; i <= 3; ++i) in_range = in_range && v[i] >= 0 && v[i] <= INT32_MAX;
-    for (int i = 4; i <= 10; ++i) in_range = in_range && v[i] >= 0 && v[i] <= 4096;
-    if (!in_range) continue;
-    const int32_t op = static_cast<int32_t>(v[0]);
-    const hxm_gemm_config c = {static_cast<int32_t>(v[4]), static_cast<int32_t>(v[5]),
-                               static_cast<int32_t>(v[6]), static_cast<int32_t>(v[7]),
-                               static_cast<int32_t>(v[8]), static_cast<int32_t>(v[9]),
-                               static_cast<int32_t>(v[10])};
+    CacheEntry ent;
+    if (!parse_cache_entry(line, &ent)) continue;
+    const int32_t op = ent.op;
+    const hxm_gemm_config c = ent.cfg;
     if (!config_compiled(op, c)) continue;
     std::lock_guard<std::mutex> lk(g_tune_mu);
-    g_tuned[TuneKey(op, v[1], v[2], v[3])] = c;
-    g_tuned_reps[TuneKey(op, v[1], v[2], v[3])] = static_cast<int32_t>(v[11]);
+    g_tuned[TuneKey(op, ent.m, ent.n, ent.k)] = c;
+    g_tuned_reps[TuneKey(op, ent.m, ent.n, ent.k)] = ent.reps;
     ++n;
   }
   std::fclose(f);

@@ -162,3 +162,33 @@ def test_product_has_no_oracle_dependency():
             if f.endswith((".py", ".hip", ".h", ".cpp")) or f == "Makefile":
                 text = open(os.path.join(dirpath, f), errors="ignore").read()
                 assert "oracle" not in text.lower().replace("oracle/oracle", ""), f
+
+
+# ---- memref descriptors (test/utils/dsp/include/common.h:15-30) -> (ptr, ld) ----
+
+def test_memref_descriptor_conversion():
+    from hxm import memref as mr
+    d = mr.describe(0x10000, rows=8, cols=24, ld=40, offset=3 * 40 + 8)
+    op = mr.operand(d, hxm.F16)
+    assert op == (0x10000 + (3 * 40 + 8) * 2, 40, 8, 24)
+    assert mr.operand(mr.describe(0x10000, 1, 24, 0), hxm.F32) == (0x10000, 24, 1, 24)
+    with pytest.raises(hxm.HxmError, match="tile-alignment"):
+        mr.operand(mr.describe(0x10000, 8, 24, 48, inner_stride=2), hxm.F16)
+    with pytest.raises(hxm.HxmError, match="invalid-argument"):
+        mr.operand(mr.describe(0x10000, 8, 24, 16), hxm.F16)        # rows overlap
+    with pytest.raises(hxm.HxmError, match="invalid-argument"):
+        mr.operand(mr.describe(0x10000, 8, 24, 24, offset=-1), hxm.F16)
+    assert ctypes.sizeof(mr.MemRefDescriptor2D) == 8 + 8 + 8 + 16 + 16
+
+
+@pytest.mark.skipif("_gpu_present()", reason="stand-in addresses are for machines without a GPU")
+def test_memref_call_reaches_the_abi_and_is_refused_there():
+    """A descriptor-shaped call with K = 12 f16 (24 bytes, not a 16-byte
+    multiple) is converted, handed to hxm_matmul and refused there."""
+    from hxm import memref as mr
+    A = mr.describe(0x10000, 8, 12, 12)
+    B = mr.describe(0x20000, 12, 8, 8)
+    C = mr.describe(0x30000, 8, 8, 8)
+    with pytest.raises(hxm.HxmError, match="tile-alignment"):
+        mr.matmul(A, B, C, ab_dtype=hxm.F16, c_dtype=hxm.F16)
+    assert hxm.last_error().startswith("tile-alignment")

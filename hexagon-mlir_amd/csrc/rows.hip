@@ -149,19 +149,52 @@ __device__ __forceinline__ void fresh(RawVec<T> (&v)[VPL]) {
 // holds more registers for that logic (LayerNorm f16 at 4096 columns: 107
 // VGPRs, four waves per SIMD, against 62 and eight waves); measured 25.7
 // against 25.2 us (8192 rows, one box).
-template <typename T, int OP, int VPL, bool ALIGNED, bool FULL>
+//
+// S > 1 (full rows only): S waves share a row, each holding every S-th
+// vector, and the wave totals meet in LDS behind a barrier.  Each wave's
+// chain of arithmetic after its loads is S times shorter, and that chain is
+// what the last rows of the grid add after the last bytes land.  Measured
+// (8192 x 4096 f16, one box, S = 2): softmax 23.1 -> 22.8 us; RMSNorm 22.3
+// -> 23.9 and LayerNorm 23.1 -> 24.6 us, so only softmax, whose chain holds
+// the exponentials, takes it.
+template <typename T, int OP, int VPL, bool ALIGNED, bool FULL, int S = 1>
 __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
   static_assert(!FULL || ALIGNED, "full rows are aligned rows");
+  static_assert(S == 1 || (FULL && kRowWaves % S == 0), "split rows are full rows");
   constexpr int N = RowVec<T>::N;
   const int lane = threadIdx.x & 63;
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * kRowWaves + (threadIdx.x >> 6);
-  if (r >= a.rows) return;  // whole wave leaves; no barriers below
-  const T* __restrict__ xr = static_cast<const T*>(a.x) + r * a.ldx;
-  T* __restrict__ yr = static_cast<T*>(a.y) + r * a.ldy;
+  const int wv = threadIdx.x >> 6;
+  const int half = wv % S;  // this wave's share of the row
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * (kRowWaves / S) + wv / S;
+  if constexpr (S == 1) {
+    if (r >= a.rows) return;  // whole wave leaves; no barriers below
+  }
+  // S > 1: a wave past the last row stays for the barriers, reads row 0 and
+  // stores nothing.
+  const bool valid = r < a.rows;
+  const int64_t rv = valid ? r : 0;
+  const T* __restrict__ xr = static_cast<const T*>(a.x) + rv * a.ldx;
+  T* __restrict__ yr = static_cast<T*>(a.y) + rv * a.ldy;
+  // Row total: the wave's, then (S > 1) the S waves' in a fixed order, so
+  // every wave of the row holds the same value.  Each slot serves one
+  // reduction of the kernel, so no slot is rewritten after the barrier.
+  __shared__ float red[2][kRowWaves];
+  auto row_reduce = [&](float x, auto op, int slot) {
+    x = wave_reduce(x, op);
+    if constexpr (S > 1) {
+      if (lane == 0) red[slot][wv] = x;
+      __syncthreads();
+      const int base = (wv / S) * S;
+      x = red[slot][base];
+#pragma unroll
+      for (int k = 1; k < S; ++k) x = op(x, red[slot][base + k]);
+    }
+    return x;
+  };
   const int64_t cols = a.cols;
   const T* __restrict__ g = static_cast<const T*>(a.gamma);
   const T* __restrict__ b = static_cast<const T*>(a.beta);
-  auto col0 = [&](int i) { return (static_cast<int64_t>(i) * 64 + lane) * N; };
+  auto col0 = [&](int i) { return ((static_cast<int64_t>(i) * S + half) * 64 + lane) * N; };
 
   const T fill = static_cast<T>(OP == kSoftmax ? -__builtin_huge_valf() : 0.0f);
   // A row that fills every slot takes plain loads: with a fill select the
@@ -211,7 +244,7 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
 #pragma unroll
         for (int j = 0; j < N; ++j) m = fmaxf(m, tof(v[i][j]));
     }
-    m = wave_reduce(m, OpMax());
+    m = row_reduce(m, OpMax(), 0);
     fresh(v);
     // exp(x - m) = 2^(x*log2(e) - m*log2(e)): one (mixed-precision) fma per
     // element feeds the hardware exp2, once per element.  Each numerator is
@@ -243,7 +276,7 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
       asm volatile("" : "+v"(e));
       v[i] = e;
     }
-    s = wave_reduce(s, OpSum());
+    s = row_reduce(s, OpSum(), 1);
     const float inv = 1.0f / s;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
@@ -257,7 +290,7 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
         asm volatile("" : "+v"(p));
         o[j] = fromf<T>(p);
       }
-      store_raw<T, ALIGNED>(yr, col0(i), cols, o);
+      if (valid) store_raw<T, ALIGNED>(yr, col0(i), cols, o);
     }
   } else if constexpr (OP == kRmsNorm) {
     // Every pass is written as fmas whose f16 operands gfx950 takes straight
@@ -272,7 +305,7 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int j = 0; j < N; ++j) ss = fmaf(tof(v[i][j]), tof(v[i][j]), ss);
-    ss = wave_reduce(ss, OpSum());
+    ss = row_reduce(ss, OpSum(), 0);
     fresh(v);
     const float rstd = 1.0f / sqrtf(ss / static_cast<float>(cols) + a.eps);
 #pragma unroll
@@ -282,7 +315,7 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
 #pragma unroll
       for (int j = 0; j < N; ++j)
         o[j] = fromf<T>(fmaf(fmaf(tof(v[i][j]), rstd, nzero), tof(gi[j]), nzero));
-      store_raw<T, ALIGNED>(yr, col0(i), cols, o);
+      if (valid) store_raw<T, ALIGNED>(yr, col0(i), cols, o);
     }
   } else {  // kLayerNorm
     // The row is widened into mixed-precision fmas as in RMSNorm: the sum as
@@ -304,7 +337,7 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
       for (int j = 0; j < N; ++j) s = fmaf(tof(v[i][j]), one, s);
       __builtin_amdgcn_sched_barrier(0);
     }
-    const float mean = wave_reduce(s, OpSum()) / static_cast<float>(cols);
+    const float mean = row_reduce(s, OpSum(), 0) / static_cast<float>(cols);
     const float nmean = -mean;
     fresh(v);
     // Padding slots (columns >= cols, loaded as 0) must not add mean^2: a
@@ -333,10 +366,10 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
           q = fmaf(d, d, q);
         }
     }
-    const float var = wave_reduce(q, OpSum()) / static_cast<float>(cols);
+    const float var = row_reduce(q, OpSum(), 1) / static_cast<float>(cols);
     fresh(v);
     const float rstd = 1.0f / sqrtf(var + a.eps);
-    if (lane == 0) {
+    if (lane == 0 && half == 0 && valid) {
       if (a.mean_out) a.mean_out[r] = mean;
       if (a.rstd_out) a.rstd_out[r] = rstd;
     }
@@ -348,7 +381,7 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
 #pragma unroll
       for (int j = 0; j < N; ++j)
         o[j] = fromf<T>(fmaf(fmaf(tof(v[i][j]), rstd, c0), tof(gi[j]), tof(bi[j])));
-      store_raw<T, ALIGNED>(yr, col0(i), cols, o);
+      if (valid) store_raw<T, ALIGNED>(yr, col0(i), cols, o);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -459,13 +492,23 @@ template <typename T, int OP, bool ALIGNED>
 hxm_status launch_rows_t(const RowArgs& a, hipStream_t stream) {
   constexpr int N = RowVec<T>::N;
   const int64_t vpl = (a.cols + 64 * N - 1) / (64 * N);
-  hxm_status st = check_grid("row kernel", (a.rows + kRowWaves - 1) / kRowWaves, 64 * kRowWaves);
+  // Softmax on full rows of 8 vectors per lane: two waves per row.
+  const bool split = OP == kSoftmax && ALIGNED && a.cols == 8 * 64 * N;
+  const int64_t rows_per_group = split ? kRowWaves / 2 : kRowWaves;
+  const int64_t groups = (a.rows + rows_per_group - 1) / rows_per_group;
+  hxm_status st = check_grid("row kernel", groups, 64 * kRowWaves);
   if (st != HXM_OK) return st;
-  const dim3 grid(static_cast<unsigned>((a.rows + kRowWaves - 1) / kRowWaves));
+  const dim3 grid(static_cast<unsigned>(groups));
   const dim3 block(64 * kRowWaves);
   // FULL kernels for aligned rows that fill the VPL slots exactly.
   auto run = [&](auto VPLC) {
     constexpr int V = decltype(VPLC)::value;
+    if constexpr (OP == kSoftmax && ALIGNED && V == 8) {
+      if (split) {
+        row_kernel<T, OP, V / 2, true, true, 2><<<grid, block, 0, stream>>>(a);
+        return;
+      }
+    }
     if (ALIGNED && a.cols == static_cast<int64_t>(V) * 64 * N)
       row_kernel<T, OP, V, ALIGNED, ALIGNED><<<grid, block, 0, stream>>>(a);
     else

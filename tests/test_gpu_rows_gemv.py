@@ -24,11 +24,11 @@ def tol(name):
     return dict(rtol=1e-2, atol=1e-3) if name != "f32" else dict(rtol=1e-5, atol=1e-6)
 
 
-# (33, 4096) and (5, 2048): full rows of 8 vectors per lane for f16/bf16 and
-# for f32, which softmax splits over two waves, with an odd row count (the
-# last workgroup's second row is past the end).
+# (33, 4096), (5, 2048) and (1, 4096): full rows of 8 vectors per lane for
+# f16/bf16 and for f32, which softmax splits over two waves, with an odd row
+# count (the last workgroup's second row is past the end).
 ROW_SHAPES = [(128, 128), (127, 513), (8192, 4096), (27, 8192), (5, 1), (3, 20000), (64, 1000),
-              (33, 4096), (5, 2048)]
+              (33, 4096), (5, 2048), (1, 4096)]
 
 
 @pytest.mark.parametrize("rows,cols", ROW_SHAPES)

@@ -227,10 +227,27 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
     v4f32 tot = part[0][b][lane];
 #pragma unroll
     for (int w = 1; w < KW; ++w) tot += part[w][b][lane];
+    // The lane's 4 consecutive channels: the fp32 product, then one
+    // rounding to f16 (the pin keeps the backend from fusing the multiply
+    // and the conversion into a single-rounding v_fma_mixlo_f16).  One
+    // 8-byte store where the run lies inside y and is aligned: measured
+    // (N=11008, K=4096, one box) M=1 9.51 -> 9.31 us, M=16 11.75 -> 11.40 us
+    // against four 2-byte stores.
+    const int no0 = n0 + 16 * b + 4 * (lane >> 4);
+    v4f16_t hv;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int no = n0 + 16 * b + 4 * (lane >> 4) + v;
-      if (no < g.N) g.y[static_cast<int64_t>(mo) * g.ldy + no] = static_cast<_Float16>(tot[v] * sc[b][v]);
+      float p = tot[v] * sc[b][v];
+      asm volatile("" : "+v"(p));
+      hv[v] = static_cast<_Float16>(p);
+    }
+    _Float16* yp = g.y + static_cast<int64_t>(mo) * g.ldy + no0;
+    if (no0 + 4 <= g.N && (reinterpret_cast<uintptr_t>(yp) & 7) == 0) {
+      *reinterpret_cast<v4f16_t*>(yp) = hv;
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (no0 + v < g.N) yp[v] = hv[v];
     }
   }
 }

@@ -296,7 +296,11 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
     // Every pass is written as fmas whose f16 operands gfx950 takes straight
     // into v_fma_mix_f32 (no separate widening).  `nzero` (-0) is hidden from
     // the optimizer so x*y + (-0) stays an fma: it rounds exactly like x*y,
-    // the sign of zero included.  Measured (8192 x 4096 f16): 22.23 against
+    // the sign of zero included.  For f16 rows the backend folds the output
+    // fma and the conversion into one v_fma_mix{lo,hi}_f16, which rounds
+    // once to f16 where the oracle rounds to fp32 first (they differ only
+    // next to an f16 rounding midpoint, inside the tolerance; LayerNorm's
+    // output is the same).  Measured (8192 x 4096 f16): 22.23 against
     // 22.30 us with widen-then-multiply, at the copy rate of its bytes.
     float nzero = -0.0f;
     asm volatile("" : "+v"(nzero));

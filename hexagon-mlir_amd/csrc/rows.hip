@@ -298,7 +298,7 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
     // the optimizer so x*y + (-0) stays an fma: it rounds exactly like x*y,
     // the sign of zero included.  For f16 rows the backend folds the output
     // fma and the conversion into one v_fma_mix{lo,hi}_f16, which rounds
-    // once to f16 where the oracle rounds to fp32 first (they differ only
+    // once to f16 instead of to fp32 and then to f16 (the two differ only
     // next to an f16 rounding midpoint, inside the tolerance; LayerNorm's
     // output is the same).  Measured (8192 x 4096 f16): 22.23 against
     // 22.30 us with widen-then-multiply, at the copy rate of its bytes.

@@ -396,6 +396,7 @@ def run_ffn(c):
     t_d = c.time_ms(down, steps, warm, reps=0).span
     t_dr = c.time_ms(down_residual, steps, warm, reps=0).span
     t_blkr = c.time_ms(block_residual, steps, warm, reps=0).span
+    t_blk_graph = c.graph_time(block, 20)  # the three launches per block, 20 blocks per graph
     f_gu, f_d = 2.0 * T * H * (2 * I), 2.0 * T * I * H
     flops = f_gu + f_d
     tf = flops / (t_blk * 1e-3) / 1e12
@@ -405,6 +406,8 @@ def run_ffn(c):
         "stages_us": {"rmsnorm": t_norm * 1e3, "gate_up_swiglu": t_gu * 1e3, "down": t_d * 1e3,
                       "down_with_residual": t_dr * 1e3},
         "block_with_residual_us": t_blkr * 1e3,
+        "graph_us": t_blk_graph * 1e3,
+        "graph_TFLOPS": flops / (t_blk_graph * 1e-3) / 1e12,
         "stage_TFLOPS": {"gate_up_swiglu": f_gu / (t_gu * 1e-3) / 1e12,
                          "down": f_d / (t_d * 1e-3) / 1e12},
         "tuned": {"gate_up_swiglu": list(cfg_gu.as_tuple()), "down": list(cfg_d.as_tuple())}}}

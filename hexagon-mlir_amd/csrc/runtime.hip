@@ -89,6 +89,15 @@ hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out, int sl
   std::lock_guard<std::mutex> lk(g_ws_mu);
   Workspace& w = g_ws[key];
   if (w.bytes < bytes) {
+    // Growing needs hipMalloc (and a stream synchronisation to retire the old
+    // buffer), neither of which a stream under graph capture allows.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+      return fail(HXM_UNSUPPORTED_SHAPE,
+                  "workspace-budget: the stream is capturing a graph and its workspace must "
+                  "grow from %zu to %zu bytes; make one call of this shape on the stream "
+                  "before capturing (the workspace is kept), or use hxm_gemm_i8_noalloc",
+                  w.bytes, bytes);
     if (w.ptr) {
       // The old buffer may still be read by work queued on this stream.
       HXM_HIP_TRY(hipStreamSynchronize(stream));

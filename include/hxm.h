@@ -15,8 +15,15 @@
  *      HmxManifest.h:81-100): "unsupported-dtype", "min-rows",
  *     "tile-alignment", "lds-budget" (the VTCM budget's counterpart), plus
  *     "invalid-argument" and "workspace-budget" (a library-owned scratch
- *     buffer would exceed its stated limit).  There is no silent fallback: a refused call
- *     computes nothing.
+ *     buffer would exceed its stated limit, or would have to grow while the
+ *     stream is capturing a HIP graph).  There is no silent fallback: a
+ *     refused call computes nothing.
+ *   - HIP graphs: the compute entries (matmul, GEMM, GEMV, row ops) may be
+ *     captured; the tuners, the resident-weight cache and hxm_release_cache
+ *     allocate or synchronise and may not.  A compute entry that uses the
+ *     per-stream workspace (f32 operands, a [K,N] B, a K split) needs it
+ *     already large enough: one call of the shape on the stream before the
+ *     capture grows it (it is kept until hxm_release_cache).
  *   - numerics: fp16/bf16 products accumulate in fp32 and are rounded once
  *     to the output dtype; int8 products accumulate exactly in int32.
  *

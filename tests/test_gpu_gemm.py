@@ -342,6 +342,50 @@ def test_split_k_kn_layout_on_special_stream_handles(dev, handle):
     assert np.array_equal(C.cpu().numpy(), acc)
 
 
+def test_graph_capture_needs_a_grown_workspace(dev):
+    """Under HIP graph capture the per-stream workspace cannot grow: a [K,N]
+    B, packed per call into the workspace, is refused with workspace-budget
+    on a stream whose workspace is still empty, and the capture stays valid.
+    One eager call of the shape grows the workspace; the same call then
+    captures, and every replay (with eager work and a synchronisation in
+    between) equals the eager result."""
+    from hxm import _lib
+    M, N, K = 192, 160, 512
+    A = rand_i8((M, K), 81)
+    B = rand_i8((N, K), 82)
+    want = orc.gemm_i8(A.numpy(), B.numpy(), b_nk=True)
+    Ad, Bkn = A.to(dev), B.t().contiguous().to(dev)
+    C = torch.full((M, N), 7, dtype=torch.int32, device=dev)
+    mark = torch.zeros(1, device=dev)
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    assert hxm.lib.hxm_release_cache() == 0  # no workspace left from earlier tests
+
+    def call():
+        return hxm.lib.hxm_gemm_i8(Ad.data_ptr(), K, Bkn.data_ptr(), N, hxm.B_KN, C.data_ptr(),
+                                   N, M, N, K, 0, None, s.cuda_stream)
+    print("gemm_i8 kn layout under graph capture", flush=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        mark.add_(1)
+        st = call()
+    assert st == _lib.HXM_UNSUPPORTED_SHAPE
+    assert hxm.last_error().startswith("workspace-budget")
+    with torch.cuda.stream(s):
+        assert call() == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(C.cpu().numpy(), want)
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2, stream=s):
+        assert call() == 0
+    for _ in range(3):
+        C.fill_(7)
+        torch.cuda.synchronize()
+        g2.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(C.cpu().numpy(), want)
+
+
 def test_split_k_is_int8_only(dev):
     A = torch.zeros(64, 64, dtype=torch.float16, device=dev)
     B = torch.zeros(64, 64, dtype=torch.float16, device=dev)

@@ -251,7 +251,20 @@ struct TuneSpec {
   void* C;
   int64_t ldc, out_eb, out_cols;
   hipStream_t stream;
+  // The cost model's operand and output dtypes (HXM_I8 / HXM_F16 / HXM_BF16
+  // and the C dtype), or -1: the W8A16 GEMMs stream an int8 B the model
+  // does not price, so their candidates are all measured.
+  int32_t price_ab = -1, price_out = -1;
 };
+
+// Constants of the tuner's conservative prune (hmx_search.cost_prune's
+// defaults): a candidate is dropped, unmeasured, only when its modeled lower
+// bound exceeds (1 + margin) * hi / lo times the modeled champion's upper
+// bound.  Calibrated repetitions (reps == 0): calibration_iters with a 10 ms
+// budget per config, between 5 and 1000 timed launches.
+constexpr double kTunePruneMargin = 0.15, kTuneEnvLo = 0.70, kTuneEnvHi = 1.25;
+constexpr double kTuneBudgetUs = 10000.0;
+constexpr int32_t kTuneRepsLo = 5, kTuneRepsHi = 1000;
 
 void sort_configs(std::vector<hxm_gemm_config>* v) {
   std::sort(v->begin(), v->end(), [](const hxm_gemm_config& a, const hxm_gemm_config& b) {
@@ -262,6 +275,7 @@ void sort_configs(std::vector<hxm_gemm_config>* v) {
 
 hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, char* report,
                      int64_t report_cap) {
+  const bool calibrated = reps == 0;
   hipStream_t s = sp.stream;
   hxm_status st = HXM_OK;
   const int32_t op = sp.op;
@@ -285,9 +299,19 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
 
   auto measure = [&](const hxm_gemm_config& c, int64_t m, int64_t n, int64_t k,
                      std::vector<double>* samples) -> hxm_status {
-    hxm_status r = sp.run(c, m, n, k);  // discarded warm call
+    // The discarded warm call; timed when the repetitions are calibrated.
+    HXM_HIP_TRY(hipEventRecord(e0, s));
+    hxm_status r = sp.run(c, m, n, k);
     if (r != HXM_OK) return r;
-    for (int i = 0; i < reps; ++i) {
+    HXM_HIP_TRY(hipEventRecord(e1, s));
+    HXM_HIP_TRY(hipEventSynchronize(e1));
+    int32_t nrep = reps;
+    if (calibrated) {
+      float warm_ms = 0.0f;
+      HXM_HIP_TRY(hipEventElapsedTime(&warm_ms, e0, e1));
+      nrep = hxm_calibration_iters(1000.0 * warm_ms, kTuneBudgetUs, kTuneRepsLo, kTuneRepsHi);
+    }
+    for (int i = 0; i < nrep; ++i) {
       HXM_HIP_TRY(hipEventRecord(e0, s));
       r = sp.run(c, m, n, k);
       if (r != HXM_OK) return r;
@@ -303,9 +327,10 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
   // Canary first: it says whether the device can be read at all.
   std::vector<double> cs_samples;
   const bool canary_ok = measure(sp.canary, sp.cm, sp.cn, sp.ck, &cs_samples) == HXM_OK;
-  const double c20 = canary_ok ? hxm_quantile(cs_samples.data(), reps, 0.2) : INFINITY;
-  const double c50 = canary_ok ? hxm_quantile(cs_samples.data(), reps, 0.5) : INFINITY;
-  const double c80 = canary_ok ? hxm_quantile(cs_samples.data(), reps, 0.8) : INFINITY;
+  const int32_t cn = static_cast<int32_t>(cs_samples.size());
+  const double c20 = canary_ok ? hxm_quantile(cs_samples.data(), cn, 0.2) : INFINITY;
+  const double c50 = canary_ok ? hxm_quantile(cs_samples.data(), cn, 0.5) : INFINITY;
+  const double c80 = canary_ok ? hxm_quantile(cs_samples.data(), cn, 0.8) : INFINITY;
   double cref = NAN;
   {
     std::lock_guard<std::mutex> lk(g_tune_mu);
@@ -327,9 +352,28 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
   }
 
   const int n = static_cast<int>(cands.size());
+  // The modeled cost of every candidate and the conservative prune: a
+  // candidate kept[i] == 0 is priced out and not launched (the control and
+  // anything the model abstains on are always measured).
+  std::vector<hxm_tile_prediction> preds(n);
+  std::vector<int32_t> kept(n, 1);
+  double prune_threshold = NAN;
+  bool priced = false;
+  if (sp.price_ab >= 0 && n > 0) {
+    hxm_device_model model;
+    if (hxm_device_model_query(&model) == HXM_OK) {
+      for (int i = 0; i < n; ++i)
+        hxm_predict_tile_time(M, N, K, &cands[i], sp.price_ab, sp.price_out, &model, &preds[i]);
+      priced = hxm_cost_prune(preds.data(), cands.data(), n, ctl_idx, nullptr, kTunePruneMargin,
+                              kTuneEnvLo, kTuneEnvHi, kept.data(), &prune_threshold) >= 0;
+      if (!priced) std::fill(kept.begin(), kept.end(), 1);
+    }
+  }
   std::vector<double> q20(n, INFINITY), q50(n, INFINITY), q80(n, INFINITY);
   std::vector<int> verified(n, 0);
+  std::vector<int32_t> nsamples(n, 0);
   for (int i = 0; i < n; ++i) {
+    if (kept[i] == 0) continue;  // priced out: scores inf, never launched
     std::vector<double> samples;
     if (measure(cands[i], M, N, K, &samples) != HXM_OK) continue;  // scores inf
     if (have_ref) {
@@ -342,9 +386,10 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
       if (h != 0) continue;  // a wrong config is wrong, not slow
       verified[i] = 1;
     }
-    q20[i] = hxm_quantile(samples.data(), reps, 0.2);
-    q50[i] = hxm_quantile(samples.data(), reps, 0.5);
-    q80[i] = hxm_quantile(samples.data(), reps, 0.8);
+    nsamples[i] = static_cast<int32_t>(samples.size());
+    q20[i] = hxm_quantile(samples.data(), nsamples[i], 0.2);
+    q50[i] = hxm_quantile(samples.data(), nsamples[i], 0.5);
+    q80[i] = hxm_quantile(samples.data(), nsamples[i], 0.8);
   }
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
@@ -367,7 +412,7 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
     std::lock_guard<std::mutex> lk(g_tune_mu);
     if (champ >= 0) {
       g_tuned[TuneKey(op, M, N, K)] = win;
-      g_tuned_reps[TuneKey(op, M, N, K)] = reps;
+      g_tuned_reps[TuneKey(op, M, N, K)] = std::max<int32_t>(1, nsamples[champ]);
     }
     if (canary_ok && round_valid) g_canary_ref[op] = c50;
   }
@@ -388,7 +433,11 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
     };
     std::string r = "{\"kind\":\"hxm-search-champion\",\"op\":" + std::to_string(op) +
                     ",\"shape_mnk\":[" + std::to_string(M) + "," + std::to_string(N) + "," +
-                    std::to_string(K) + "],\"reps\":" + std::to_string(reps) +
+                    std::to_string(K) + "],\"reps\":" +
+                    (calibrated ? std::string("\"calibrated\"") : std::to_string(reps)) +
+                    ",\"prune\":{\"priced\":" + (priced ? "true" : "false") +
+                    ",\"threshold\":" + num(prune_threshold) + ",\"dropped\":" +
+                    std::to_string(std::count(kept.begin(), kept.end(), 0)) + "}" +
                     ",\"unit\":\"us\",\"round_verdict\":\"" +
                     (round_valid ? "valid" : "invalid-canary") +
                     "\",\"start\":\"" + kStart[verdict.start] + "\",\"proof\":\"" +
@@ -411,7 +460,10 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
            (outcome[i] == 1 ? "takeover" : outcome[i] == 0 ? "kept" : "-") +
            "\",\"faced\":" + (faced[i] >= 0 ? std::to_string(faced[i]) : "null") +
            ",\"delta_pct\":" + num(100.0 * delta[i]) + ",\"gate_pct\":" +
-           num(100.0 * gate[i]) + "}";
+           num(100.0 * gate[i]) + ",\"samples\":" + std::to_string(nsamples[i]) +
+           ",\"pruned\":" + (kept[i] == 0 ? "true" : "false") + ",\"model_lb_us\":" +
+           num(priced ? preds[i].lb_us : NAN) + ",\"model_ub_us\":" +
+           num(priced ? preds[i].ub_us : NAN) + "}";
     }
     r += "]}";
     const size_t nb = std::min<size_t>(r.size(), static_cast<size_t>(report_cap - 1));
@@ -739,7 +791,7 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
                          int64_t report_cap, void* stream) {
   if (op != HXM_I8 && op != HXM_F16 && op != HXM_BF16)
     return fail(HXM_UNSUPPORTED_DTYPE, "unsupported-dtype: tune op %d", op);
-  if (M <= 0 || N <= 0 || K <= 0 || reps <= 0 || reps > 10000)
+  if (M <= 0 || N <= 0 || K <= 0 || reps < 0 || reps > 10000)
     return fail(HXM_INVALID_ARG, "invalid-argument: tune extents/reps");
   if (!A || !B || !C || lda < K || ldb < K || ldc < N)
     return fail(HXM_INVALID_ARG, "invalid-argument: tune operands");
@@ -789,6 +841,7 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
   };
   sp.C = C, sp.ldc = ldc, sp.out_eb = dtype_bytes(out_dt), sp.out_cols = N;
   sp.stream = s;
+  sp.price_ab = op, sp.price_out = out_dt;
   return tune_core(sp, reps, best, report, report_cap);
 }
 
@@ -809,7 +862,7 @@ hxm_status hxm_tune_w8a16(int32_t op, const void* x, int64_t ldx, const int8_t* 
   if (op != HXM_OP_W8A16 && op != HXM_OP_W8A16_SWIGLU)
     return fail(HXM_INVALID_ARG, "invalid-argument: tune_w8a16 op %d", op);
   const bool sw = op == HXM_OP_W8A16_SWIGLU;
-  if (M <= 0 || N <= 0 || K <= 0 || reps <= 0 || reps > 10000)
+  if (M <= 0 || N <= 0 || K <= 0 || reps < 0 || reps > 10000)
     return fail(HXM_INVALID_ARG, "invalid-argument: tune extents/reps");
   const int64_t rows = sw ? hxm_swiglu_packed_rows(N) : N;
   if (!x || !W || !scale || !C || ldx < K || ldw < K || ldc < N)

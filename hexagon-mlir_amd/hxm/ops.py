@@ -339,7 +339,8 @@ def tune_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor, out: torch
     """Measured tile search for :func:`gemm_w8a16` (W [N, K], scale [N]) or,
     with swiglu=True, :func:`gemm_w8a16_swiglu` (W = Wgu, scale = sgu, out
     [M, I]).  The winner is cached for later calls; returns (GemmConfig,
-    report dict)."""
+    report dict).  reps=0 calibrates the repetitions per config as in
+    :func:`tune_gemm`; the int8-weight configs are not priced, so all run."""
     import ctypes
     import json
     _mat(x, "x"), _mat(W, "W"), _mat(out, "out")
@@ -468,7 +469,11 @@ def layer_norm(x: torch.Tensor, normalized_shape: Sequence[int],
 
 def tune_gemm(A: torch.Tensor, B_nk: torch.Tensor, out: torch.Tensor, *, reps: int = 5,
               stream=None):
-    """Measured tile search on these operands; returns (GemmConfig, report dict)."""
+    """Measured tile search on these operands; returns (GemmConfig, report dict).
+    reps=0 calibrates the repetitions per config (hxm_calibration_iters of the
+    timed warm call against a 10 ms budget, 5 to 1000 launches).  Configs the
+    cost model prices out of reach are not launched (``pruned`` in the
+    report, with ``model_lb_us`` / ``model_ub_us`` for every config)."""
     import ctypes
     import json
     _mat(A, "A"), _mat(B_nk, "B"), _mat(out, "out")

@@ -555,14 +555,21 @@ int32_t hxm_judge_round(const hxm_arm_quantiles* arms, int32_t n, int32_t contro
 /* Measured tile search for one GEMM shape on the caller's operands (the
  * reference's autotune sweep + hexagon_bench + judge_champion_round,
  * hmx_search.py:1109-1156,1370-1571).  op: HXM_I8 (int8 -> i32, B in
- * layout NK) or HXM_F16 / HXM_BF16 (-> f16, B in layout NK).  Every legal
- * compiled config is launched `reps` times after one discarded warm call;
+ * layout NK) or HXM_F16 / HXM_BF16 (-> f16, B in layout NK).  First the
+ * cost model prices every legal compiled config on this device
+ * (hxm_predict_tile_time) and the conservative prune (hxm_cost_prune, margin
+ * 0.15, envelope 0.70 / 1.25, the control always kept) drops those whose
+ * modeled lower bound is out of reach; a dropped config is not launched.
+ * Every other config is launched `reps` times after one discarded warm call
+ * (reps 0: calibrated per config, hxm_calibration_iters of the timed warm
+ * call against a 10 ms budget, 5 to 1000 launches);
  * its output is checked bit-exact against the control config's (a config
  * that differs scores inf); the champion is the deterministic gated walk
  * from the control config with gate max(3*CV, 15%), preceded by the
  * 32x32x32 canary.  The winner is cached for (op, M, N, K) and used by
  * later calls with cfg == NULL.  report (JSON, may be NULL) receives the
- * per-config quantiles and the verdict.  C is overwritten. */
+ * per-config quantiles, sample counts, modeled bounds and prune marks, and
+ * the verdict.  C is overwritten. */
 hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
                          int64_t ldb, void* C, int64_t ldc, int64_t M,
                          int64_t N, int64_t K, int32_t reps,

@@ -132,3 +132,37 @@ def test_cost_model_floor_holds_and_prune_keeps_the_measured_winner(dev, M, N, K
     print(notes, flush=True)
     fastest = min(measured.values(), key=lambda v: v[1])[0]
     assert fastest.as_tuple() in [c.as_tuple() for c in kept]
+
+
+def rand_i8(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
+
+
+def test_tune_calibrated_repetitions_and_the_cost_model(dev):
+    """reps=0: every launched config gets hxm_calibration_iters' count (5 to
+    1000 timed launches) from its timed warm call; the cost model prices every
+    candidate on this device, the control is never priced out, a priced-out
+    config is not launched (no quantiles) and cannot win, and each measured
+    time is at or above the config's modeled lower bound."""
+    M = N = K = 1024
+    A = rand_i8((M, K), 91).to(dev)
+    B = rand_i8((N, K), 92).to(dev)
+    out = torch.empty(M, N, dtype=torch.int32, device=dev)
+    print("tune int8 1024^3 with calibrated repetitions", flush=True)
+    best, rep = ops.tune_gemm(A, B, out, reps=0)
+    assert rep["reps"] == "calibrated"
+    assert rep["prune"]["priced"] is True
+    cfgs = rep["configs"]
+    assert rep["prune"]["dropped"] == sum(c["pruned"] for c in cfgs)
+    assert not cfgs[rep["control"]]["pruned"]
+    for c in cfgs:
+        assert c["model_lb_us"] is not None and c["model_ub_us"] is not None
+        if c["pruned"]:
+            assert c["q50"] is None and c["samples"] == 0
+        elif c["q50"] is not None:
+            assert 5 <= c["samples"] <= 1000
+            assert c["q50"] >= c["model_lb_us"]
+    assert rep["champion"] is not None and not cfgs[rep["champion"]]["pruned"]
+    C = ops.gemm_i8(A, B, b_layout="nk").cpu().numpy()
+    assert np.array_equal(C, orc.gemm_i8(A.cpu().numpy(), B.cpu().numpy(), b_nk=True))

@@ -38,6 +38,11 @@ struct GemvArgs {
 };
 
 
+// Largest slab count (K / 64) of a packed image the GEMV accepts: every
+// buffer offset of the pipelined kernel, (slabs + 15) * 1024 + 1008, stays
+// below 2^31.
+constexpr int64_t kMaxPackedSlabs = (int64_t(1) << 21) - 32;
+
 // Bytes of the packed (resident) weight image for [N, K]: one 1 KiB block
 // per (16-channel group, 64-wide K slab), zero-padded at the edges.
 inline int64_t packed_bytes(int64_t N, int64_t K) {
@@ -63,6 +68,45 @@ __global__ __launch_bounds__(256) void pack_w8a16_kernel(const int8_t* __restric
   v4i32 v = {0, 0, 0, 0};
   if (n < N && k < K) v = *reinterpret_cast<const v4i32*>(W + n * ldw + k);
   *reinterpret_cast<v4i32*>(out + blk * 1024 + lane * 16) = v;
+}
+
+// Wave 0, after every wave has written its partial 16x16 tiles to part:
+// the sum over the KW waves, the per-channel scale, one rounding to f16, the
+// store.  Lane l holds D[channel 4*(l/16) + v][m = l%16] of each group.
+template <int KW, int CB>
+__device__ __forceinline__ void gemv_finish(const GemvArgs& g, const v4f32 (*part)[CB][64],
+                                            const float (&sc)[CB][4], int n0, int m_base,
+                                            int lane) {
+  const int mo = m_base + (lane & 15);
+  if (mo >= g.M) return;
+#pragma unroll
+  for (int b = 0; b < CB; ++b) {
+    v4f32 tot = part[0][b][lane];
+#pragma unroll
+    for (int w = 1; w < KW; ++w) tot += part[w][b][lane];
+    // The lane's 4 consecutive channels: the fp32 product, then one
+    // rounding to f16 (the pin keeps the backend from fusing the multiply
+    // and the conversion into a single-rounding v_fma_mixlo_f16).  One
+    // 8-byte store where the run lies inside y and is aligned: measured
+    // (N=11008, K=4096, one box) M=1 9.51 -> 9.31 us, M=16 11.75 -> 11.40 us
+    // against four 2-byte stores.
+    const int no0 = n0 + 16 * b + 4 * (lane >> 4);
+    v4f16_t hv;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float p = tot[v] * sc[b][v];
+      asm volatile("" : "+v"(p));
+      hv[v] = static_cast<_Float16>(p);
+    }
+    _Float16* yp = g.y + static_cast<int64_t>(mo) * g.ldy + no0;
+    if (no0 + 4 <= g.N && (reinterpret_cast<uintptr_t>(yp) & 7) == 0) {
+      *reinterpret_cast<v4f16_t*>(yp) = hv;
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (no0 + v < g.N) yp[v] = hv[v];
+    }
+  }
 }
 
 // One workgroup = CB groups of 16 output channels x all of K; its KW waves
@@ -219,37 +263,151 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) sc[b][v] = static_cast<float>(sc_raw[b][v]);
   }
-  // D[row = channel 4*(l/16)+v][col = m l%16]
-  const int mo = m_base + (lane & 15);
-  if (mo >= g.M) return;
+  gemv_finish<KW, CB>(g, part, sc, n0, m_base, lane);
+}
+
+// Pipelined form for the packed image at M > 1.  A K chunk is KW slabs,
+// one per wave, and the next chunk's x and weight loads are issued before
+// this chunk's x staging and MFMAs, so every wave keeps two chunks of loads
+// in flight and the weight stream does not pause at chunk boundaries.  The
+// weight loads are buffer loads whose range is the channel group's image
+// (num_records = slabs * 1 KiB): a slab past K lies past the range and
+// returns zeros without a memory access, so every load is unconditional and
+// the waits the compiler places stay exact (a load under a branch makes the
+// merged wait count conservative, down to waiting for the prefetch itself).
+// Measured at N=11008, K=4096 (one box, 5 runs of 240 launches each): M=4
+// 9.6 us against 9.85 us for the one-chunk kernel, M=16 10.1 against
+// 11.4 us.  Two or four slabs per wave per chunk, all of K in one chunk, 2
+// or 4 channel groups per workgroup, 4 or 16 waves per workgroup: each
+// slower (10.5 to 14.6 us at M=16).
+template <int KW, int MR, int CB, bool LATE_SCALES>
+__global__ __launch_bounds__(KW * 64) void gemv_w8a16_pipe_kernel(GemvArgs g) {
+  constexpr int kChunkK = KW * 64;
+  constexpr int kRowBytes = kChunkK * 2 + 16;   // padded x row in LDS
+  constexpr int kXVecs = MR * kChunkK / 8;      // 16-byte x vectors per chunk
+  constexpr int kXPerThread = (kXVecs + KW * 64 - 1) / (KW * 64);
+  __shared__ __attribute__((aligned(16))) uint8_t xs[MR * kRowBytes];
+  __shared__ v4f32 part[KW][CB][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * 16 * CB;
+  const int m_base = blockIdx.y * 16;
+  const int rows = min(MR, g.M - m_base);
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const int slabs = (g.K + 63) / 64;
+  const int groups = (g.N + 15) / 16;
+  float sc[CB][4];
+  _Float16 sc_raw[CB][4];
+  auto scale_of = [&](int b, int v) {
+    const int no = n0 + 16 * b + 4 * kq + v;
+    return g.scale[no < g.N ? no : g.N - 1];
+  };
+  if (!LATE_SCALES && wave == 0) {
+#pragma unroll
+    for (int b = 0; b < CB; ++b)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sc[b][v] = static_cast<float>(scale_of(b, v));
+  }
+  __amdgpu_buffer_rsrc_t wr[CB];
 #pragma unroll
   for (int b = 0; b < CB; ++b) {
-    v4f32 tot = part[0][b][lane];
-#pragma unroll
-    for (int w = 1; w < KW; ++w) tot += part[w][b][lane];
-    // The lane's 4 consecutive channels: the fp32 product, then one
-    // rounding to f16 (the pin keeps the backend from fusing the multiply
-    // and the conversion into a single-rounding v_fma_mixlo_f16).  One
-    // 8-byte store where the run lies inside y and is aligned: measured
-    // (N=11008, K=4096, one box) M=1 9.51 -> 9.31 us, M=16 11.75 -> 11.40 us
-    // against four 2-byte stores.
-    const int no0 = n0 + 16 * b + 4 * (lane >> 4);
-    v4f16_t hv;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      float p = tot[v] * sc[b][v];
-      asm volatile("" : "+v"(p));
-      hv[v] = static_cast<_Float16>(p);
-    }
-    _Float16* yp = g.y + static_cast<int64_t>(mo) * g.ldy + no0;
-    if (no0 + 4 <= g.N && (reinterpret_cast<uintptr_t>(yp) & 7) == 0) {
-      *reinterpret_cast<v4f16_t*>(yp) = hv;
-    } else {
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        if (no0 + v < g.N) yp[v] = hv[v];
-    }
+    const int grp = min(static_cast<int>(blockIdx.x) * CB + b, groups - 1);
+    wr[b] = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(g.W) + static_cast<int64_t>(grp) * slabs * 1024,
+        static_cast<short>(0), slabs * 1024, 0x00020000);
   }
+  const v4i32 zero = {0, 0, 0, 0};
+  v4f32 acc[CB];
+#pragma unroll
+  for (int b = 0; b < CB; ++b) acc[b] = v4f32{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // x[m_base .. m_base+rows, chunk c's K range), zero past K and rows (the
+  // address is clamped to x itself, an L2 hit).
+  auto load_x = [&](int c, v4i32 (&xv)[kXPerThread]) {
+    const int kc0 = c * 64;
+#pragma unroll
+    for (int q = 0; q < kXPerThread; ++q) {
+      const int idx = threadIdx.x + q * KW * 64;
+      const int r = idx / (kChunkK / 8), k8 = (idx % (kChunkK / 8)) * 8;
+      const bool ok = idx < kXVecs && r < rows && kc0 + k8 < g.K;
+      const v4i32 v = *reinterpret_cast<const v4i32*>(
+          g.x + (ok ? static_cast<int64_t>(m_base + r) * g.ldx + kc0 + k8 : 0));
+      xv[q] = ok ? v : zero;
+    }
+  };
+  // This wave's slab of chunk c, every channel group; nontemporal (aux bit 1):
+  // the weights are streamed once.
+  auto load_w = [&](int c, v4i32 (&w)[CB]) {
+    const int s = c + wave;
+#pragma unroll
+    for (int b = 0; b < CB; ++b)
+      w[b] = __builtin_bit_cast(
+          v4i32, __builtin_amdgcn_raw_buffer_load_b128(wr[b], lane * 16 + s * 1024, 0, 2));
+  };
+  auto consume = [&](const v4i32 (&xv)[kXPerThread], const v4i32 (&w)[CB]) {
+    // The previous chunk's LDS reads are done; then x goes to LDS.  These
+    // barriers wait for LDS operations only, never for the weight loads.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int q = 0; q < kXPerThread; ++q) {
+      const int idx = threadIdx.x + q * KW * 64;
+      if (idx < kXVecs) {
+        const int r = idx / (kChunkK / 8), k8 = (idx % (kChunkK / 8)) * 8;
+        *reinterpret_cast<v4i32*>(xs + r * kRowBytes + k8 * 2) = xv[q];
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const uint8_t* px = xs + (r16 < MR ? r16 : 0) * kRowBytes + (wave * 64 + kq * 16) * 2;
+    v4i32 xa = *reinterpret_cast<const v4i32*>(px);
+    v4i32 xb = *reinterpret_cast<const v4i32*>(px + 16);
+    if (r16 >= rows) xa = xb = zero;
+#pragma unroll
+    for (int b = 0; b < CB; ++b) {
+      const v8f16 wa = i8x8_to_f16(static_cast<uint32_t>(w[b][0]), static_cast<uint32_t>(w[b][1]));
+      const v8f16 wb = i8x8_to_f16(static_cast<uint32_t>(w[b][2]), static_cast<uint32_t>(w[b][3]));
+      acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, __builtin_bit_cast(v8f16, xa), acc[b],
+                                                      0, 0, 0);
+      acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, __builtin_bit_cast(v8f16, xb), acc[b],
+                                                      0, 0, 0);
+    }
+  };
+
+  v4i32 xv0[kXPerThread], xv1[kXPerThread];
+  v4i32 w0[CB], w1[CB];
+  load_x(0, xv0);
+  load_w(0, w0);
+  if (LATE_SCALES && wave == 0) {
+    // After the first weight loads: loads complete in order, so the scales
+    // are in by the time this wave has its first slab.
+#pragma unroll
+    for (int b = 0; b < CB; ++b)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sc_raw[b][v] = scale_of(b, v);
+  }
+  // Two chunks per trip, the buffers alternating; the loads past K fetch
+  // nothing, so only the second chunk's compute needs a (uniform) test.
+  for (int c0 = 0; c0 < slabs; c0 += 2 * KW) {
+    const int c1 = c0 + KW;
+    load_x(c1, xv1);
+    load_w(c1, w1);
+    consume(xv0, w0);
+    load_x(c1 + KW, xv0);
+    load_w(c1 + KW, w0);
+    if (c1 < slabs) consume(xv1, w1);
+  }
+
+#pragma unroll
+  for (int b = 0; b < CB; ++b) part[wave][b][lane] = acc[b];
+  __syncthreads();
+  if (wave != 0) return;
+  if (LATE_SCALES) {
+#pragma unroll
+    for (int b = 0; b < CB; ++b)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sc[b][v] = static_cast<float>(sc_raw[b][v]);
+  }
+  gemv_finish<KW, CB>(g, part, sc, n0, m_base, lane);
 }
 
 }  // namespace hxm
@@ -308,6 +466,12 @@ hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W, int64_t l
                 (long long)K);
   if (N > INT32_MAX - 16 || K > INT32_MAX - 64 || M > 65535LL * 16)
     return fail(HXM_UNSUPPORTED_SHAPE, "tile-alignment: gemv_w8a16 extent too large");
+  // The pipelined kernel addresses a channel group's image with 32-bit
+  // buffer offsets, up to two chunks of 8 slabs past its last slab.
+  if (w_layout == HXM_W_PACKED && (K + 63) / 64 > kMaxPackedSlabs)
+    return fail(HXM_UNSUPPORTED_SHAPE,
+                "tile-alignment: gemv_w8a16 packed image needs K <= %lld (K=%lld)",
+                (long long)kMaxPackedSlabs * 64, (long long)K);
   hxm_status st = require_device(nullptr);
   if (st != HXM_OK) return st;
   if (M == 0 || N == 0) return ok();
@@ -325,18 +489,21 @@ hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W, int64_t l
   const int cb = M <= 4 ? 1 : 3;
   if ((st = check_grid("gemv_w8a16", (N + 16 * cb - 1) / (16 * cb), 512, (M + 15) / 16)) != HXM_OK)
     return st;
-  // Small M: a 4096-wide K chunk (x rows fit LDS), so at K <= 4096 each wave
-  // issues all its weight loads at once and makes one memory round trip.
+  // M = 1 (and the plain [N, K] layout at every M): a 4096-wide K chunk (x
+  // rows fit LDS), so at K <= 4096 each wave issues all its weight loads at
+  // once and makes one memory round trip.  The packed image at M > 1: the
+  // pipelined kernel, 512-wide chunks with the next chunk in flight.
   if (M <= 1) {
     if (pk) gemv_w8a16_kernel<8, 8, true, 1, 1, true><<<grid(1), 512, 0, s>>>(g);
     else gemv_w8a16_kernel<8, 8, false, 1, 1, true><<<grid(1), 512, 0, s>>>(g);
   } else if (M <= 4) {
-    if (pk) gemv_w8a16_kernel<8, 8, true, 4, 1, true><<<grid(1), 512, 0, s>>>(g);
+    if (pk) gemv_w8a16_pipe_kernel<8, 4, 1, true><<<grid(1), 512, 0, s>>>(g);
     else gemv_w8a16_kernel<8, 8, false, 4, 1, true><<<grid(1), 512, 0, s>>>(g);
   } else {
     // 16 x rows: three channel groups per workgroup share each staged x
-    // chunk (measured: 13.1 vs 14.7 us at N=11008, K=4096).
-    if (pk) gemv_w8a16_kernel<8, 4, true, 16, 3, false><<<grid(3), 512, 0, s>>>(g);
+    // chunk (measured with the one-chunk kernel: 13.1 vs 14.7 us at
+    // N=11008, K=4096).
+    if (pk) gemv_w8a16_pipe_kernel<8, 16, 3, false><<<grid(3), 512, 0, s>>>(g);
     else gemv_w8a16_kernel<8, 4, false, 16, 3, false><<<grid(3), 512, 0, s>>>(g);
   }
   return check_launch("gemv_w8a16");

@@ -115,6 +115,15 @@ def _span_refusals():
     assert hxm.last_error().startswith("tile-alignment") and "2 GiB" in hxm.last_error()
     st = L.hxm_gemm_w8a16(16, 32, 16, 1 << 24, 16, 16, 8, 8, 8, 32, None, None)
     assert st == _lib.HXM_UNSUPPORTED_SHAPE and "2 GiB" in hxm.last_error()
+    # A packed W8A16 image past 2^21 - 32 slabs: the GEMV's 32-bit buffer
+    # offsets would wrap.  One slab fewer is admitted up to the device check.
+    for slabs, refused in (((1 << 21) - 31, True), ((1 << 21) - 32, False)):
+        K = slabs * 64
+        st = L.hxm_gemv_w8a16(16, K, 16, K, hxm.W_PACKED, 16, 16, 8, 1, 8, K, None)
+        if refused:
+            assert st == _lib.HXM_UNSUPPORTED_SHAPE and "packed image" in hxm.last_error()
+        else:
+            assert st == _lib.HXM_NO_DEVICE
 
 
 @pytest.mark.skipif("_gpu_present()", reason="stand-in addresses are for machines without a GPU; "

@@ -184,15 +184,22 @@ def test_w8a16_image_layout(dev):
     assert np.array_equal(img.reshape(ng, ns, 64, 16), exp)
 
 
-def test_gemv_golden_and_exact_small_ints(dev, golden):
+@pytest.mark.parametrize("packed", [True, False])
+def test_gemv_golden_and_exact_small_ints(dev, golden, packed):
     gd = golden("gemv_w8a16")
+    Wg = torch.from_numpy(gd["W"]).to(dev)
     y = ops.gemv_w8a16(torch.from_numpy(gd["x_bits"].view(np.float16)).to(dev),
-                       torch.from_numpy(gd["W"]).to(dev),
+                       ops.prepack_w8a16(Wg) if packed else Wg,
                        torch.from_numpy(gd["scale_bits"].view(np.float16)).to(dev))
     np.testing.assert_allclose(y.float().cpu().numpy(), gd["y_f64"], rtol=1e-2, atol=1e-3)
     # every int8 value -128..127 through the exact f16 conversion: x = e_k
     K = 256
     W = torch.arange(-128, 128, dtype=torch.int16).to(torch.int8).repeat(2, 1)  # [2, 256]
     x = torch.eye(K)[:16].half()                                                # picks k=0..15
-    y = ops.gemv_w8a16(x.to(dev), W.to(dev), torch.ones(2).half().to(dev)).cpu()
+    Wd = ops.prepack_w8a16(W.to(dev)) if packed else W.to(dev)
+    y = ops.gemv_w8a16(x.to(dev), Wd, torch.ones(2).half().to(dev)).cpu()
     assert torch.equal(y.float(), W[:, :16].t().float())
+    # M = 1 and 4 through the same rows (the one-chunk and pipelined kernels)
+    for m in (1, 4):
+        y = ops.gemv_w8a16(x[:m].to(dev), Wd, torch.ones(2).half().to(dev)).cpu()
+        assert torch.equal(y.float(), W[:, :m].t().float())

@@ -400,8 +400,12 @@ def run_ffn(c):
     f_gu, f_d = 2.0 * T * H * (2 * I), 2.0 * T * I * H
     flops = f_gu + f_d
     tf = flops / (t_blk * 1e-3) / 1e12
+    clk = sclk_under_load(c, block, what="the FFN block")
     return {"swiglu_ffn_2048x4096x11008": {
         **tb.us(), "TFLOPS": tf, "mfma_frac": tf / PEAK_F16_TFLOPS,
+        "sclk_under_load": clk,
+        "mfma_frac_at_measured_sclk": (tf / (PEAK_F16_TFLOPS * clk["median_mhz"] / 2400.0)
+                                       if clk else None),
         "gemm_flops": flops,
         "stages_us": {"rmsnorm": t_norm * 1e3, "gate_up_swiglu": t_gu * 1e3, "down": t_d * 1e3,
                       "down_with_residual": t_dr * 1e3},
@@ -462,8 +466,12 @@ def run_vendor(c):
         hxm.check(L.hxm_matmul(pa, n, pb, n, hxm.B_NK, pc, n, n, n, n, hxm.F16, hxm.F16, 0,
                                None, st), "hxm_matmul")
     ms = c.time_ms(f16, 100, 10).span
-    out["f16_matmul_4096"] = {"us": ms * 1e3, "TFLOPS": 2 * n ** 3 / (ms * 1e-3) / 1e12,
-                              "mfma_frac": 2 * n ** 3 / (ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS}
+    tf = 2 * n ** 3 / (ms * 1e-3) / 1e12
+    clk = sclk_under_load(c, f16, what="the f16 4096^3 matmul")
+    out["f16_matmul_4096"] = {"us": ms * 1e3, "TFLOPS": tf, "mfma_frac": tf / PEAK_F16_TFLOPS,
+                              "sclk_under_load": clk,
+                              "mfma_frac_at_measured_sclk":
+                                  tf / (PEAK_F16_TFLOPS * clk["median_mhz"] / 2400.0) if clk else None}
     return out
 
 
@@ -591,7 +599,7 @@ def cpu_baseline(A, Bp, seconds):
                       f"OpenMP, {threads} threads), median of 5 runs of {t:.3f} s"}
 
 
-def sclk_under_load(c, fn, seconds=1.0):
+def sclk_under_load(c, fn, seconds=1.0, what="the headline GEMM"):
     """Shader clock (MHz) while `fn` runs back to back for about `seconds`:
     rocm-smi is sampled from a host thread during the loop.  Returns the
     median sample and the raw samples, or None when rocm-smi gives nothing."""
@@ -629,7 +637,7 @@ def sclk_under_load(c, fn, seconds=1.0):
         return None
     steady = samples[len(samples) // 2:]  # the first samples still see the ramp from idle
     return {"median_mhz": statistics.median(steady), "samples_mhz": samples,
-            "source": "rocm-smi --showclocks sampled while the headline GEMM runs back to back"}
+            "source": f"rocm-smi --showclocks sampled while {what} runs back to back"}
 
 
 def main() -> int:

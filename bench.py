@@ -417,6 +417,94 @@ def run_ffn(c):
         "tuned": {"gate_up_swiglu": list(cfg_gu.as_tuple()), "down": list(cfg_d.as_tuple())}}}
 
 
+def run_shard(c):
+    """One GPU's share of an 8-way tensor-parallel split of configs 3 and 5
+    (measured alone: no second GPU, and the all-reduce of the block's
+    [2048, 4096] partial output is not built).  The GEMV keeps N / 8 = 1376
+    output channels of W (5.6 MB per image, so 96 images rotate past the
+    256 MB Infinity Cache); the FFN block keeps I / 8 = 1376 intermediate
+    channels: gate/up column-parallel (its SwiGLU image interleaves 64-channel
+    blocks, the last one half padding), down row-parallel over the same
+    slice.  Tiles are tuned per GEMM at these shapes."""
+    import math
+    torch, hxm, L, ops = c.torch, c.hxm, c.L, c.ops
+    out = {}
+    N, K, R = 11008 // 8, 4096, 96
+    Ws = [ops.prepack_w8a16(torch.randint(-127, 128, (N, K), dtype=torch.int8, device=c.dev))
+          for _ in range(R)]
+    scs = [(torch.rand(N, device=c.dev) * 0.019 + 0.001).half() for _ in range(R)]
+    wp = [w.data_ptr() for w in Ws]
+    sp = [s.data_ptr() for s in scs]
+    for M in (1, 4, 16):
+        xs = torch.randn(M, K, device=c.dev).half()
+        ys = torch.empty(M, N, dtype=torch.float16, device=c.dev)
+        px, py, st = xs.data_ptr(), ys.data_ptr(), c.stream
+
+        def step(i, M=M, px=px, py=py):
+            hxm.check(L.hxm_gemv_w8a16(px, K, wp[i], K, hxm.W_PACKED, sp[i], py, N, M, N, K,
+                                       st), "hxm_gemv_w8a16")
+        t = c.time_ms(step, 480, 48, rotate=R)
+        nbytes = N * K + N * 2 + M * K * 2 + M * N * 2
+        gbs = nbytes / (t.span * 1e-3) / 1e9
+        out[f"tp8_shard_w8a16_gemv_M{M}"] = {
+            **t.us(), "GB/s": gbs, "hbm_frac": gbs / PEAK_HBM_GBS, "bytes": nbytes,
+            "graph_us": c.graph_time(step, 480, rotate=R) * 1e3,
+            "shape": f"M={M} N={N} K={K} (config 3, N split 8 ways)",
+            "note": "a kernel this short is shorter than one host launch: us is the host's "
+                    "launch rate, graph_us the device time per launch"}
+    del Ws, scs
+    T, H, I = 2048, 4096, 11008 // 8
+    x = torch.randn(T, H, device=c.dev).half()
+    gamma = (1 + 0.1 * torch.randn(H, device=c.dev)).half()
+    Wg = torch.randint(-127, 128, (I, H), dtype=torch.int8, device=c.dev)
+    Wu = torch.randint(-127, 128, (I, H), dtype=torch.int8, device=c.dev)
+    Wd = torch.randint(-127, 128, (H, I), dtype=torch.int8, device=c.dev)
+    sc_h, sc_i = 1 / math.sqrt(H * 127 ** 2 / 3), 1 / math.sqrt(11008 * 127 ** 2 / 3)
+    sg = ((torch.rand(I, device=c.dev) + 0.5) * sc_h).half().float()
+    su = ((torch.rand(I, device=c.dev) + 0.5) * sc_h).half().float()
+    sd = ((torch.rand(H, device=c.dev) + 0.5) * sc_i).half().float()
+    Wgu, sgu = ops.swiglu_pack(Wg, Wu, sg, su)
+    xn = torch.empty_like(x)
+    h = torch.empty(T, I, dtype=torch.float16, device=c.dev)
+    y = torch.empty(T, H, dtype=torch.float16, device=c.dev)
+    ops.rms_norm(x, (H,), gamma, eps=1e-6, out=xn)
+    cfg_gu, _ = ops.tune_w8a16(xn, Wgu, sgu, h, swiglu=True, reps=5)
+    cfg_d, _ = ops.tune_w8a16(h, Wd, sd, y, reps=5)
+    st = c.stream
+    px, pg, pxn, ph, py = x.data_ptr(), gamma.data_ptr(), xn.data_ptr(), h.data_ptr(), y.data_ptr()
+    pgu, psgu, pwd, psd = Wgu.data_ptr(), sgu.data_ptr(), Wd.data_ptr(), sd.data_ptr()
+
+    def norm(_):
+        hxm.check(L.hxm_rmsnorm_rows(px, H, pg, pxn, H, T, H, 1e-6, hxm.F16, st),
+                  "hxm_rmsnorm_rows")
+
+    def gateup(_):
+        hxm.check(L.hxm_gemm_w8a16_swiglu(pxn, H, pgu, psgu, ph, I, T, I, H, None, st),
+                  "hxm_gemm_w8a16_swiglu")
+
+    def down(_):
+        hxm.check(L.hxm_gemm_w8a16(ph, I, pwd, I, psd, py, H, T, H, I, None, st),
+                  "hxm_gemm_w8a16")
+
+    def block(i):
+        norm(i), gateup(i), down(i)
+    tb = c.time_ms(block, 100, 10, reps=5)
+    t_gu = c.time_ms(gateup, 100, 10, reps=0).span
+    t_d = c.time_ms(down, 100, 10, reps=0).span
+    f_gu, f_d = 2.0 * T * H * (2 * I), 2.0 * T * I * H
+    tf = (f_gu + f_d) / (tb.span * 1e-3) / 1e12
+    out["tp8_shard_swiglu_ffn_2048x4096x1376"] = {
+        **tb.us(), "TFLOPS": tf, "mfma_frac": tf / PEAK_F16_TFLOPS, "gemm_flops": f_gu + f_d,
+        "stages_us": {"gate_up_swiglu": t_gu * 1e3, "down": t_d * 1e3},
+        "stage_TFLOPS": {"gate_up_swiglu": f_gu / (t_gu * 1e-3) / 1e12,
+                         "down": f_d / (t_d * 1e-3) / 1e12},
+        "graph_us": c.graph_time(block, 20) * 1e3,
+        "tuned": {"gate_up_swiglu": list(cfg_gu.as_tuple()), "down": list(cfg_d.as_tuple())},
+        "shape": "tokens 2048, hidden 4096, intermediate 1376 (config 5, intermediate split 8 "
+                 "ways; the all-reduce of the partial output is not built)"}
+    return out
+
+
 def run_ragged(c):
     """Tail tiles, a partial last K stage and an N-split store: int8 GEMM
     M=N=4000, K=4000 (K bytes not a multiple of the 128-byte stage) with
@@ -654,7 +742,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", choices=["int8", "int8_i32", "f16", "ragged", "gemv", "rows", "ffn",
-                                       "copy", "vendor", "search"])
+                                       "shard", "copy", "vendor", "search"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build is the single-GPU kernel set of the hot "
@@ -668,7 +756,8 @@ def main() -> int:
             rec = {args.only: run_int8(c, *int8_operands(c), out_i32=args.only == "int8_i32")}
         else:
             rec = {"f16": run_f16, "ragged": run_ragged, "gemv": run_gemv, "rows": run_rows,
-                   "ffn": run_ffn, "copy": run_copy, "vendor": run_vendor, "search": run_search}[
+                   "ffn": run_ffn, "shard": run_shard, "copy": run_copy, "vendor": run_vendor,
+                   "search": run_search}[
                 args.only](c)
         print(json.dumps(rec), flush=True)
         return 0
@@ -681,8 +770,8 @@ def main() -> int:
     extra = {}
     if not args.no_extra:
         extra["int8_gemm_i32_out_4096"] = run_int8(c, A, Bp, rs, cs, out_i32=True)
-        for fn in (run_f16, run_ragged, run_gemv, run_rows, run_ffn, run_copy, run_vendor,
-                   run_search):
+        for fn in (run_f16, run_ragged, run_gemv, run_rows, run_ffn, run_shard, run_copy,
+                   run_vendor, run_search):
             extra.update(fn(c))
         for k, v in extra.items():
             log(k, json.dumps(v))

@@ -43,6 +43,19 @@ struct GemvArgs {
 // below 2^31.
 constexpr int64_t kMaxPackedSlabs = (int64_t(1) << 21) - 32;
 
+// Three channel groups per workgroup at M > 4 from this many 16-channel
+// groups up.  Measured at M=16, K=4096 (packed image, one box), one group
+// against three per workgroup: N=1376 6.19 / 8.44 us, 2752 6.34 / 8.59,
+// 4096 6.60 / 8.75, 5504 8.99 / 8.91, 11008 13.0 / 10.0.
+constexpr int64_t kGemvCb3MinGroups = 320;
+
+// The pipelined kernel at 1 < M <= 4 from this many 16-channel groups up;
+// below it, with about one workgroup per CU or fewer, the one-chunk kernel's
+// single round trip wins.  Measured at M=4, K=4096 (packed image, HIP graph
+// of 480 launches, one box), one-chunk against pipelined: N=1376 4.50 /
+// 5.78 us, 4096 5.61 / 6.18, 11008 10.39 / 9.46.
+constexpr int64_t kGemvPipeMinGroups = 320;
+
 // Bytes of the packed (resident) weight image for [N, K]: one 1 KiB block
 // per (16-channel group, 64-wide K slab), zero-padded at the edges.
 inline int64_t packed_bytes(int64_t N, int64_t K) {
@@ -486,25 +499,36 @@ hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W, int64_t l
   // keeps more workgroups resident per CU.
   hipStream_t s = as_stream(stream);
   const bool pk = w_layout == HXM_W_PACKED;
-  const int cb = M <= 4 ? 1 : 3;
+  // Channel groups per workgroup at M > 4: three share each staged x chunk,
+  // which pays while a workgroup per 16 channels would more than fill the
+  // chip; below that (fewer than kGemvCb3MinGroups groups, a column shard
+  // for example) the three-fold grid leaves CUs idle.
+  const int cb = M <= 4 || (N + 15) / 16 < kGemvCb3MinGroups ? 1 : 3;
   if ((st = check_grid("gemv_w8a16", (N + 16 * cb - 1) / (16 * cb), 512, (M + 15) / 16)) != HXM_OK)
     return st;
-  // M = 1 (and the plain [N, K] layout at every M): a 4096-wide K chunk (x
-  // rows fit LDS), so at K <= 4096 each wave issues all its weight loads at
-  // once and makes one memory round trip.  The packed image at M > 1: the
+  // M = 1 (and the plain [N, K] layout at every M, and the packed image at
+  // M <= 4 below kGemvPipeMinGroups): a 4096-wide K chunk (x rows fit LDS),
+  // so at K <= 4096 each wave issues all its weight loads at once and makes
+  // one memory round trip.  Otherwise the packed image at M > 1 takes the
   // pipelined kernel, 512-wide chunks with the next chunk in flight.
   if (M <= 1) {
     if (pk) gemv_w8a16_kernel<8, 8, true, 1, 1, true><<<grid(1), 512, 0, s>>>(g);
     else gemv_w8a16_kernel<8, 8, false, 1, 1, true><<<grid(1), 512, 0, s>>>(g);
   } else if (M <= 4) {
-    if (pk) gemv_w8a16_pipe_kernel<8, 4, 1, true><<<grid(1), 512, 0, s>>>(g);
-    else gemv_w8a16_kernel<8, 8, false, 4, 1, true><<<grid(1), 512, 0, s>>>(g);
+    if (pk && (N + 15) / 16 >= kGemvPipeMinGroups)
+      gemv_w8a16_pipe_kernel<8, 4, 1, true><<<grid(1), 512, 0, s>>>(g);
+    else if (pk)
+      gemv_w8a16_kernel<8, 8, true, 4, 1, true><<<grid(1), 512, 0, s>>>(g);
+    else
+      gemv_w8a16_kernel<8, 8, false, 4, 1, true><<<grid(1), 512, 0, s>>>(g);
   } else {
     // 16 x rows: three channel groups per workgroup share each staged x
     // chunk (measured with the one-chunk kernel: 13.1 vs 14.7 us at
-    // N=11008, K=4096).
-    if (pk) gemv_w8a16_pipe_kernel<8, 16, 3, false><<<grid(3), 512, 0, s>>>(g);
-    else gemv_w8a16_kernel<8, 4, false, 16, 3, false><<<grid(3), 512, 0, s>>>(g);
+    // N=11008, K=4096), one group below kGemvCb3MinGroups.
+    if (pk && cb == 3) gemv_w8a16_pipe_kernel<8, 16, 3, false><<<grid(3), 512, 0, s>>>(g);
+    else if (pk) gemv_w8a16_pipe_kernel<8, 16, 1, false><<<grid(1), 512, 0, s>>>(g);
+    else if (cb == 3) gemv_w8a16_kernel<8, 4, false, 16, 3, false><<<grid(3), 512, 0, s>>>(g);
+    else gemv_w8a16_kernel<8, 4, false, 16, 1, false><<<grid(1), 512, 0, s>>>(g);
   }
   return check_launch("gemv_w8a16");
 }

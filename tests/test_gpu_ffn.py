@@ -267,6 +267,23 @@ def test_swiglu_ffn_baseline_size_row_sample(dev):
     np.testing.assert_allclose(y[rows], f32(ref), rtol=1e-2, atol=2e-3)
 
 
+def test_swiglu_ffn_tp8_shard_row_sample(dev):
+    """One GPU's share of an 8-way tensor-parallel block: intermediate
+    11008 / 8 = 1376 channels (not a multiple of the image's 64-channel
+    blocks: the last block is half padding), gate/up column-parallel, down
+    row-parallel over the same slice, so y is this GPU's partial sum of the
+    block's output.  Oracle on 16 sampled token rows."""
+    T, H, I = 2048, 4096, 1376
+    x, gamma, Wg, Wu, Wd, sg, su, sd = ffn_operands(T, H, I, 37)
+    y = run_ffn(dev, x, gamma, Wg, Wu, Wd, sg, su, sd).float().cpu().numpy()
+    assert np.isfinite(y).all()
+    rows = np.array([0, 1, 255, 256, 511, 777, 1023, 1024, 1290, 1535, 1536, 1800, 2000,
+                     2045, 2046, 2047])
+    ref = orc.swiglu_ffn(bits(x)[rows], bits(gamma), Wg.numpy(), Wu.numpy(), sg.numpy(),
+                         su.numpy(), Wd.numpy(), sd.numpy())
+    np.testing.assert_allclose(y[rows], f32(ref), rtol=1e-2, atol=2e-3)
+
+
 def test_tune_w8a16_caches_a_verified_winner(dev):
     import hxm
     hxm.lib.hxm_tune_cache_clear()

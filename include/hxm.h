@@ -260,7 +260,8 @@ typedef enum hxm_w_layout { HXM_W_NK = 0, HXM_W_PACKED = 1 } hxm_w_layout;
  * y fp16 [M,N] (ldy >= N).  fp32 accumulation in any order (tolerance
  * rtol 1e-2 / atol 1e-3 against the fp32 restatement).  W is streamed once
  * per 16 rows of M.  K multiple of 16, ldx multiple of 8, ldw (HXM_W_NK)
- * multiple of 16, x and W 16-byte aligned. */
+ * multiple of 16, x and W 16-byte aligned; HXM_W_PACKED images up to
+ * K = 134,215,680 (2^21 - 32 slabs of 64). */
 hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W,
                           int64_t ldw, int32_t w_layout, const void* w_scale,
                           void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,

@@ -43,8 +43,49 @@ def _mat(t: torch.Tensor, name: str) -> torch.Tensor:
     return t
 
 
+def _out(out: torch.Tensor, shape, dtypes, like: torch.Tensor, name: str = "out") -> torch.Tensor:
+    """A caller-supplied output: a GPU matrix of exactly ``shape``, one of
+    ``dtypes``, on ``like``'s device.  The C entries write shape[0] rows of
+    shape[1] elements at its pointer and cannot see the allocation, so a
+    wrong shape or dtype here would be a write past the tensor."""
+    _mat(out, name)
+    if tuple(out.shape) != tuple(shape):
+        raise ValueError(f"{name} must be {tuple(shape)} (got {tuple(out.shape)})")
+    if out.dtype not in dtypes:
+        raise TypeError(f"{name} must be {' or '.join(str(d) for d in dtypes)} (got {out.dtype})")
+    if out.device != like.device:
+        raise ValueError(f"{name} must be on {like.device} (got {out.device})")
+    return out
+
+
+def _dtype(t: torch.Tensor, dtypes, name: str) -> torch.Tensor:
+    if t.dtype not in dtypes:
+        raise TypeError(f"{name} must be {' or '.join(str(d) for d in dtypes)} (got {t.dtype})")
+    return t
+
+
+def _vec(t: torch.Tensor, n: int, dtype: torch.dtype, name: str) -> torch.Tensor:
+    """A per-channel vector of n elements of dtype on the GPU, contiguous."""
+    if not t.is_cuda or t.dtype != dtype or t.numel() != n:
+        raise ValueError(f"{name} must be a GPU {dtype} tensor of {n} elements "
+                         f"(got {t.dtype} {tuple(t.shape)} on {t.device})")
+    return t.contiguous()
+
+
 def _ld(t: torch.Tensor) -> int:
     return t.stride(0) if t.shape[0] > 1 else max(t.shape[1], t.stride(0))
+
+
+def _b_extent(A: torch.Tensor, B: torch.Tensor, b_layout: str) -> int:
+    """N of C = A @ B for B [K, N] (``"kn"``) or the [N, K] image (``"nk"``),
+    after checking that B's K matches A's."""
+    if b_layout not in ("kn", "nk"):
+        raise ValueError(f"b_layout must be 'kn' or 'nk' (got {b_layout!r})")
+    K = A.shape[1]
+    kb, n = (B.shape[0], B.shape[1]) if b_layout == "kn" else (B.shape[1], B.shape[0])
+    if kb != K:
+        raise ValueError(f"shape mismatch A{tuple(A.shape)} B{tuple(B.shape)} ({b_layout})")
+    return n
 
 
 def _cfg(config) -> Optional[GemmConfig]:
@@ -73,14 +114,12 @@ def matmul(A: torch.Tensor, B: torch.Tensor, out: Optional[torch.Tensor] = None,
     if A.dtype != B.dtype:
         raise TypeError(f"A and B must share a dtype (got {A.dtype} and {B.dtype})")
     M, K = A.shape
-    N = B.shape[1] if b_layout == "kn" else B.shape[0]
-    if (B.shape[0] if b_layout == "kn" else B.shape[1]) != K:
-        raise ValueError(f"shape mismatch A{tuple(A.shape)} B{tuple(B.shape)} ({b_layout})")
+    N = _b_extent(A, B, b_layout)
     if out is None:
         if accumulate:
             raise ValueError("accumulate=True needs out")
         out = torch.empty((M, N), dtype=out_dtype or A.dtype, device=A.device)
-    _mat(out, "out")
+    _out(out, (M, N), (torch.float16, torch.bfloat16, torch.float32), A)
     cfg = _cfg(config)
     st = lib.hxm_matmul(A.data_ptr(), _ld(A), B.data_ptr(), _ld(B),
                         B_KN if b_layout == "kn" else B_NK, out.data_ptr(), _ld(out),
@@ -134,13 +173,14 @@ def gemm_i8(A: torch.Tensor, B: torch.Tensor, out: Optional[torch.Tensor] = None
             stream=None) -> torch.Tensor:
     """int32 C = [C +] A @ B, exact (the reference's int8 linalg.matmul)."""
     _mat(A, "A"), _mat(B, "B")
+    _dtype(A, (torch.int8,), "A"), _dtype(B, (torch.int8,), "B")
     M, K = A.shape
-    N = B.shape[1] if b_layout == "kn" else B.shape[0]
+    N = _b_extent(A, B, b_layout)
     if out is None:
         if accumulate:
             raise ValueError("accumulate=True needs out")
         out = torch.empty((M, N), dtype=torch.int32, device=A.device)
-    _mat(out, "out")
+    _out(out, (M, N), (torch.int32,), A)
     cfg = _cfg(config)
     st = lib.hxm_gemm_i8(A.data_ptr(), _ld(A), B.data_ptr(), _ld(B),
                          B_KN if b_layout == "kn" else B_NK, out.data_ptr(), _ld(out),
@@ -154,15 +194,18 @@ def gemm_i8_dequant(A: torch.Tensor, B: torch.Tensor, row_scale: torch.Tensor,
                     b_layout: str = "kn", config=None, stream=None) -> torch.Tensor:
     """f16 C = f16(((float)(A @ B) * row_scale[:,None]) * col_scale[None,:])."""
     _mat(A, "A"), _mat(B, "B")
+    _dtype(A, (torch.int8,), "A"), _dtype(B, (torch.int8,), "B")
     M, K = A.shape
-    N = B.shape[1] if b_layout == "kn" else B.shape[0]
+    N = _b_extent(A, B, b_layout)
     if row_scale.dtype != torch.float32 or col_scale.dtype != torch.float32:
         raise TypeError("scales must be float32")
     if row_scale.numel() != M or col_scale.numel() != N:
         raise ValueError("scale lengths must be M and N")
+    row_scale = _vec(row_scale, M, torch.float32, "row_scale")
+    col_scale = _vec(col_scale, N, torch.float32, "col_scale")
     if out is None:
         out = torch.empty((M, N), dtype=torch.float16, device=A.device)
-    _mat(out, "out")
+    _out(out, (M, N), (torch.float16,), A)
     cfg = _cfg(config)
     st = lib.hxm_gemm_i8_dequant(A.data_ptr(), _ld(A), B.data_ptr(), _ld(B),
                                  B_KN if b_layout == "kn" else B_NK,
@@ -180,7 +223,7 @@ def prepack_weight(B: torch.Tensor, out: Optional[torch.Tensor] = None, *,
     K, N = B.shape
     if out is None:
         out = torch.empty((N, K), dtype=B.dtype, device=B.device)
-    _mat(out, "out")
+    _out(out, (N, K), (B.dtype,), B)
     st = lib.hxm_prepack_weight(B.data_ptr(), _ld(B), out.data_ptr(), _ld(out), K, N,
                                 _code(B), _stream(stream))
     check(st, "hxm_prepack_weight")
@@ -206,9 +249,12 @@ def gemv_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor,
     W may also be the flat image from :func:`prepack_w8a16`; then N is taken
     from ``scale`` (or passed explicitly)."""
     _mat(x, "x")
+    _dtype(x, (torch.float16,), "x"), _dtype(W, (torch.int8,), "W")
     M, K = x.shape
     packed = W.dim() == 1
     if packed:
+        if not W.is_cuda:
+            raise ValueError(f"W must be a GPU tensor (got {W.device})")
         N = scale.numel() if N is None else N
         if W.numel() < lib.hxm_w8a16_packed_bytes(N, K):
             raise ValueError("packed image too small for [N, K]")
@@ -219,11 +265,12 @@ def gemv_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor,
         if W.shape[1] != K:
             raise ValueError("W must be [N, K]")
         ldw = _ld(W)
+    scale = _vec(scale, N, torch.float16, "scale")
     if out is None:
         out = torch.empty((M, N), dtype=torch.float16, device=x.device)
-    _mat(out, "out")
+    _out(out, (M, N), (torch.float16,), x)
     st = lib.hxm_gemv_w8a16(x.data_ptr(), _ld(x), W.data_ptr(), ldw,
-                            W_PACKED if packed else W_NK, scale.contiguous().data_ptr(),
+                            W_PACKED if packed else W_NK, scale.data_ptr(),
                             out.data_ptr(), _ld(out), M, N, K, _stream(stream))
     check(st, "hxm_gemv_w8a16")
     return out
@@ -243,6 +290,7 @@ def gemm_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor,
     f16 ``residual`` [M, N]: y = f16(fp32((x @ W.T) * scale) + residual)
     (hxm_gemm_w8a16_residual); ``out`` may be ``residual`` itself."""
     _mat(x, "x"), _mat(W, "W")
+    _dtype(x, (torch.float16,), "x"), _dtype(W, (torch.int8,), "W")
     M, K = x.shape
     N = W.shape[0]
     if W.shape[1] != K:
@@ -250,7 +298,7 @@ def gemm_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor,
     scale = _f32_vec(scale, N, "scale")
     if out is None:
         out = torch.empty((M, N), dtype=torch.float16, device=x.device)
-    _mat(out, "out")
+    _out(out, (M, N), (torch.float16,), x)
     cfg = _cfg(config)
     if residual is not None:
         _mat(residual, "residual")
@@ -296,6 +344,7 @@ def gemm_w8a16_swiglu(x: torch.Tensor, Wgu: torch.Tensor, sgu: torch.Tensor, I: 
     """h = f16(silu(x @ Wg.T * sg) * (x @ Wu.T * su)) from the
     :func:`swiglu_pack` image; h is [M, I]."""
     _mat(x, "x"), _mat(Wgu, "Wgu")
+    _dtype(x, (torch.float16,), "x"), _dtype(Wgu, (torch.int8,), "Wgu")
     M, K = x.shape
     rows = lib.hxm_swiglu_packed_rows(I)
     if tuple(Wgu.shape) != (rows, K) or _ld(Wgu) != K:
@@ -303,7 +352,7 @@ def gemm_w8a16_swiglu(x: torch.Tensor, Wgu: torch.Tensor, sgu: torch.Tensor, I: 
     sgu = _f32_vec(sgu, rows, "sgu")
     if out is None:
         out = torch.empty((M, I), dtype=torch.float16, device=x.device)
-    _mat(out, "out")
+    _out(out, (M, I), (torch.float16,), x)
     cfg = _cfg(config)
     st = lib.hxm_gemm_w8a16_swiglu(x.data_ptr(), _ld(x), Wgu.data_ptr(), sgu.data_ptr(),
                                    out.data_ptr(), _ld(out), M, I, K, _ptr_or_none(cfg),
@@ -343,13 +392,25 @@ def tune_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor, out: torch
     :func:`tune_gemm`; the int8-weight configs are not priced, so all run."""
     import ctypes
     import json
-    _mat(x, "x"), _mat(W, "W"), _mat(out, "out")
+    _mat(x, "x"), _mat(W, "W")
+    _dtype(x, (torch.float16,), "x"), _dtype(W, (torch.int8,), "W")
     M, K = x.shape
-    N = out.shape[1]
+    if swiglu:
+        N = out.shape[1]
+        rows = lib.hxm_swiglu_packed_rows(N)
+        if tuple(W.shape) != (rows, K) or _ld(W) != K:
+            raise ValueError(f"W must be the contiguous [{rows}, {K}] swiglu_pack image")
+        scale = _f32_vec(scale, rows, "scale")
+    else:
+        N = W.shape[0]
+        if W.shape[1] != K:
+            raise ValueError("W must be [N, K]")
+        scale = _f32_vec(scale, N, "scale")
+    _out(out, (M, N), (torch.float16,), x)
     best = GemmConfig()
     buf = ctypes.create_string_buffer(1 << 16)
     st = lib.hxm_tune_w8a16(OP_W8A16_SWIGLU if swiglu else OP_W8A16, x.data_ptr(), _ld(x),
-                            W.data_ptr(), _ld(W), scale.contiguous().data_ptr(),
+                            W.data_ptr(), _ld(W), scale.data_ptr(),
                             out.data_ptr(), _ld(out), M, N, K, reps, ctypes.byref(best), buf,
                             len(buf), _stream(stream))
     check(st, "hxm_tune_w8a16")
@@ -409,15 +470,39 @@ def _rows(x: torch.Tensor):
     return x2, x2.shape[0], cols
 
 
+def _rows_out(out: Optional[torch.Tensor], x: torch.Tensor, cols: int):
+    """The output of a row op: new, or the caller's of x's shape and dtype
+    (rows of it may be strided, its last dimension contiguous)."""
+    if out is None:
+        out = torch.empty_like(x)
+    elif tuple(out.shape) != tuple(x.shape) or out.dtype != x.dtype or out.device != x.device:
+        raise ValueError(f"out must be {x.dtype} {tuple(x.shape)} on {x.device} "
+                         f"(got {out.dtype} {tuple(out.shape)} on {out.device})")
+    elif out.stride(-1) != 1:
+        raise ValueError("out must have a contiguous last dimension")
+    try:
+        return out, out.view(-1, cols)   # a view: the kernel writes into out itself
+    except RuntimeError:
+        raise ValueError("out's rows must be evenly strided (viewable as [rows, cols])") from None
+
+
+def _row_param(t: Optional[torch.Tensor], x: torch.Tensor, cols: int, name: str):
+    """gamma / beta: None, or [cols] of x's dtype on x's device."""
+    if t is None:
+        return None
+    if t.numel() != cols or t.dtype != x.dtype or t.device != x.device:
+        raise ValueError(f"{name} must be {x.dtype} [{cols}] on {x.device} "
+                         f"(got {t.dtype} {tuple(t.shape)} on {t.device})")
+    return t.contiguous()
+
+
 def softmax(x: torch.Tensor, dim: int = -1, out: Optional[torch.Tensor] = None, *,
             stream=None) -> torch.Tensor:
     """Row softmax over the last dimension (F.softmax(x, dim=-1))."""
     if dim not in (-1, x.dim() - 1):
         raise ValueError("only the last dimension is supported")
     x2, rows, cols = _rows(x)
-    if out is None:
-        out = torch.empty_like(x)
-    o2 = out.reshape(-1, cols)
+    out, o2 = _rows_out(out, x, cols)
     st = lib.hxm_softmax_rows(x2.data_ptr(), _ld(x2), o2.data_ptr(), _ld(o2), rows, cols,
                               _code(x), _stream(stream))
     check(st, "hxm_softmax_rows")
@@ -433,11 +518,10 @@ def rms_norm(x: torch.Tensor, normalized_shape: Sequence[int],
         raise ValueError("normalized_shape must be (x.shape[-1],)")
     if eps is None:
         eps = torch.finfo(x.dtype).eps
-    if out is None:
-        out = torch.empty_like(x)
-    o2 = out.reshape(-1, cols)
-    g = 0 if weight is None else weight.contiguous().data_ptr()
-    st = lib.hxm_rmsnorm_rows(x2.data_ptr(), _ld(x2), g or None, o2.data_ptr(), _ld(o2),
+    out, o2 = _rows_out(out, x, cols)
+    weight = _row_param(weight, x, cols, "weight")
+    st = lib.hxm_rmsnorm_rows(x2.data_ptr(), _ld(x2),
+                              None if weight is None else weight.data_ptr(), o2.data_ptr(), _ld(o2),
                               rows, cols, float(eps), _code(x), _stream(stream))
     check(st, "hxm_rmsnorm_rows")
     return out
@@ -451,16 +535,16 @@ def layer_norm(x: torch.Tensor, normalized_shape: Sequence[int],
     x2, rows, cols = _rows(x)
     if tuple(normalized_shape) != (cols,):
         raise ValueError("normalized_shape must be (x.shape[-1],)")
-    if out is None:
-        out = torch.empty_like(x)
-    o2 = out.reshape(-1, cols)
+    out, o2 = _rows_out(out, x, cols)
+    weight = _row_param(weight, x, cols, "weight")
+    bias = _row_param(bias, x, cols, "bias")
     mean = rstd = None
     if return_stats:
         mean = torch.empty(rows, dtype=torch.float32, device=x.device)
         rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
     st = lib.hxm_layernorm_rows(
-        x2.data_ptr(), _ld(x2), None if weight is None else weight.contiguous().data_ptr(),
-        None if bias is None else bias.contiguous().data_ptr(), o2.data_ptr(), _ld(o2),
+        x2.data_ptr(), _ld(x2), None if weight is None else weight.data_ptr(),
+        None if bias is None else bias.data_ptr(), o2.data_ptr(), _ld(o2),
         None if mean is None else mean.data_ptr(), None if rstd is None else rstd.data_ptr(),
         rows, cols, float(eps), _code(x), _stream(stream))
     check(st, "hxm_layernorm_rows")
@@ -476,9 +560,13 @@ def tune_gemm(A: torch.Tensor, B_nk: torch.Tensor, out: torch.Tensor, *, reps: i
     report, with ``model_lb_us`` / ``model_ub_us`` for every config)."""
     import ctypes
     import json
-    _mat(A, "A"), _mat(B_nk, "B"), _mat(out, "out")
+    _mat(A, "A"), _mat(B_nk, "B")
+    _dtype(A, (torch.int8, torch.float16, torch.bfloat16), "A")
+    if B_nk.dtype != A.dtype:
+        raise TypeError(f"A and B must share a dtype (got {A.dtype} and {B_nk.dtype})")
     M, K = A.shape
-    N = B_nk.shape[0]
+    N = _b_extent(A, B_nk, "nk")
+    _out(out, (M, N), (torch.int32,) if A.dtype == torch.int8 else (torch.float16,), A)
     best = GemmConfig()
     buf = ctypes.create_string_buffer(1 << 16)
     st = lib.hxm_tune_gemm(_code(A), A.data_ptr(), _ld(A), B_nk.data_ptr(), _ld(B_nk),

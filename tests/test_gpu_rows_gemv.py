@@ -152,7 +152,10 @@ def test_gemv_baseline_shape(dev, M, packed):
 @pytest.mark.parametrize("M,N,K", [(3, 100, 272), (33, 64, 512), (1, 17, 16), (16, 48, 256),
                                    (5, 40, 2064), (20, 31, 4160),
                                    # one GPU's share of an 8-way column split of config 3
-                                   (1, 1376, 4096), (4, 1376, 4096), (16, 1376, 4096)])
+                                   (1, 1376, 4096), (4, 1376, 4096), (16, 1376, 4096),
+                                   # 322 channel groups: the pipelined kernels (three groups
+                                   # per workgroup at M > 4, the last set partial), K of 33 slabs
+                                   (3, 5140, 2064), (9, 5140, 2064)])
 @pytest.mark.parametrize("packed", [True, False])
 def test_gemv_ragged(dev, M, N, K, packed):
     g = torch.Generator().manual_seed(M * N + K)

@@ -566,7 +566,7 @@ def tune_gemm(A: torch.Tensor, B_nk: torch.Tensor, out: torch.Tensor, *, reps: i
         raise TypeError(f"A and B must share a dtype (got {A.dtype} and {B_nk.dtype})")
     M, K = A.shape
     N = _b_extent(A, B_nk, "nk")
-    _out(out, (M, N), (torch.int32,) if A.dtype == torch.int8 else (torch.float16,), A)
+    _out(out, (M, N), (torch.int32,) if A.dtype == torch.int8 else (A.dtype,), A)
     best = GemmConfig()
     buf = ctypes.create_string_buffer(1 << 16)
     st = lib.hxm_tune_gemm(_code(A), A.data_ptr(), _ld(A), B_nk.data_ptr(), _ld(B_nk),

@@ -556,7 +556,8 @@ int32_t hxm_judge_round(const hxm_arm_quantiles* arms, int32_t n, int32_t contro
 /* Measured tile search for one GEMM shape on the caller's operands (the
  * reference's autotune sweep + hexagon_bench + judge_champion_round,
  * hmx_search.py:1109-1156,1370-1571).  op: HXM_I8 (int8 -> i32, B in
- * layout NK) or HXM_F16 / HXM_BF16 (-> f16, B in layout NK).  First the
+ * layout NK) or HXM_F16 / HXM_BF16 (-> C of the same dtype, B in layout
+ * NK).  First the
  * cost model prices every legal compiled config on this device
  * (hxm_predict_tile_time) and the conservative prune (hxm_cost_prune, margin
  * 0.15, envelope 0.70 / 1.25, the control always kept) drops those whose

@@ -13,7 +13,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("dtype,M,N,K", [(torch.int8, 512, 512, 512),
-                                         (torch.float16, 256, 256, 256)])
+                                         (torch.float16, 256, 256, 256),
+                                         (torch.bfloat16, 256, 256, 256)])
 def test_tune_gemm_picks_a_verified_winner(dev, dtype, M, N, K):
     g = torch.Generator().manual_seed(M)
     if dtype == torch.int8:
@@ -21,9 +22,9 @@ def test_tune_gemm_picks_a_verified_winner(dev, dtype, M, N, K):
         B = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
         out = torch.empty(M, N, dtype=torch.int32, device=dev)
     else:
-        A = (torch.rand(M, K, generator=g) * 2 - 1).half()
-        B = (torch.rand(N, K, generator=g) * 2 - 1).half()
-        out = torch.empty(M, N, dtype=torch.float16, device=dev)
+        A = (torch.rand(M, K, generator=g) * 2 - 1).to(dtype)
+        B = (torch.rand(N, K, generator=g) * 2 - 1).to(dtype)
+        out = torch.empty(M, N, dtype=dtype, device=dev)     # C of the operands' dtype
     Ad, Bd = A.to(dev), B.to(dev)
     best, rep = ops.tune_gemm(Ad, Bd, out, reps=5)
     print(rep, flush=True)
@@ -47,7 +48,9 @@ def test_tune_gemm_picks_a_verified_winner(dev, dtype, M, N, K):
     else:
         C = ops.matmul(Ad, Bd, b_layout="nk").float().cpu().numpy()
         bits = lambda t: t.view(torch.int16).numpy().view(np.uint16)  # noqa: E731
-        ref = orc.f16_bits_to_f32(orc.matmul(bits(A), bits(B), b_nk=True))
+        name = "f16" if dtype == torch.float16 else "bf16"
+        ref = orc.to_f32(orc.matmul(bits(A), bits(B), ab_dtype=name, c_dtype=name, b_nk=True),
+                         name)
         np.testing.assert_allclose(C, ref, rtol=1e-2, atol=1e-3)
 
 

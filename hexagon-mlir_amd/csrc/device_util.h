@@ -84,10 +84,14 @@ __device__ __forceinline__ uint32_t i8x2_flipped_to_f16(uint32_t flipped) {
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2f16, w) - bias);
 }
 
-// 8 int8 (two dwords) -> 8 exact f16.
+// 8 int8 (two dwords) -> 8 exact f16.  OFFSET_BINARY: the bytes are already
+// w ^ 0x80 (the packed GEMV image stores them so), and the flip is skipped.
+template <bool OFFSET_BINARY>
 __device__ __forceinline__ v8f16 i8x8_to_f16(uint32_t lo, uint32_t hi) {
-  lo ^= 0x80808080u;
-  hi ^= 0x80808080u;
+  if constexpr (!OFFSET_BINARY) {
+    lo ^= 0x80808080u;
+    hi ^= 0x80808080u;
+  }
   v4i32 r;
   r[0] = static_cast<int>(i8x2_flipped_to_f16<0>(lo));
   r[1] = static_cast<int>(i8x2_flipped_to_f16<1>(lo));

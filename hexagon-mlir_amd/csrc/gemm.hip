@@ -573,7 +573,9 @@ hxm_gemm_config default_w8_config(int64_t M, int64_t N, bool swiglu) {
 
 // The SwiGLU weight image: rows [128c, 128c+64) are gate channels
 // [64c, 64c+64), rows [128c+64, 128c+128) the same up channels; channels
-// >= I are zero rows with zero scale.  One workgroup per image row.
+// >= I are zero rows with zero scale.  Each weight is stored in offset
+// binary (byte = w ^ 0x80, w + 128 unsigned), the form the GEMM's in-register
+// f16 conversion takes without a sign flip.  One workgroup per image row.
 __global__ __launch_bounds__(256) void swiglu_pack_kernel(
     const int8_t* __restrict__ wg, const int8_t* __restrict__ wu, int64_t ldw,
     const float* __restrict__ sg, const float* __restrict__ su, int64_t I, int64_t K,
@@ -584,7 +586,7 @@ __global__ __launch_bounds__(256) void swiglu_pack_kernel(
   const int8_t* src = up ? wu : wg;
   int8_t* dst = out + r * K;
   for (int64_t k = threadIdx.x; k < K; k += blockDim.x)
-    dst[k] = ch < I ? src[ch * ldw + k] : int8_t(0);
+    dst[k] = static_cast<int8_t>((ch < I ? static_cast<uint8_t>(src[ch * ldw + k]) : 0) ^ 0x80);
   if (threadIdx.x == 0)
     out_scale[r] = ch < I ? (up ? su : sg)[ch] : 0.0f;
 }

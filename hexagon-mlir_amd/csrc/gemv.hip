@@ -80,6 +80,7 @@ __global__ __launch_bounds__(256) void pack_w8a16_kernel(const int8_t* __restric
   const int k = s * 64 + (lane >> 4) * 16;
   v4i32 v = {0, 0, 0, 0};
   if (n < N && k < K) v = *reinterpret_cast<const v4i32*>(W + n * ldw + k);
+  v ^= static_cast<int>(0x80808080u);
   *reinterpret_cast<v4i32*>(out + blk * 1024 + lane * 16) = v;
 }
 
@@ -254,9 +255,9 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
       if (r16 >= rows) xa = xb = zero;
 #pragma unroll
       for (int b = 0; b < CB; ++b) {
-        const v8f16 wa = i8x8_to_f16(static_cast<uint32_t>(w[u][b][0]),
+        const v8f16 wa = i8x8_to_f16<PACKED>(static_cast<uint32_t>(w[u][b][0]),
                                      static_cast<uint32_t>(w[u][b][1]));
-        const v8f16 wb = i8x8_to_f16(static_cast<uint32_t>(w[u][b][2]),
+        const v8f16 wb = i8x8_to_f16<PACKED>(static_cast<uint32_t>(w[u][b][2]),
                                      static_cast<uint32_t>(w[u][b][3]));
         acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, __builtin_bit_cast(v8f16, xa),
                                                         acc[b], 0, 0, 0);
@@ -377,8 +378,8 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_pipe_kernel(GemvArgs g) {
     if (r16 >= rows) xa = xb = zero;
 #pragma unroll
     for (int b = 0; b < CB; ++b) {
-      const v8f16 wa = i8x8_to_f16(static_cast<uint32_t>(w[b][0]), static_cast<uint32_t>(w[b][1]));
-      const v8f16 wb = i8x8_to_f16(static_cast<uint32_t>(w[b][2]), static_cast<uint32_t>(w[b][3]));
+      const v8f16 wa = i8x8_to_f16<true>(static_cast<uint32_t>(w[b][0]), static_cast<uint32_t>(w[b][1]));
+      const v8f16 wb = i8x8_to_f16<true>(static_cast<uint32_t>(w[b][2]), static_cast<uint32_t>(w[b][3]));
       acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, __builtin_bit_cast(v8f16, xa), acc[b],
                                                       0, 0, 0);
       acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, __builtin_bit_cast(v8f16, xb), acc[b],

@@ -231,7 +231,8 @@ def prepack_weight(B: torch.Tensor, out: Optional[torch.Tensor] = None, *,
 
 
 def prepack_w8a16(W: torch.Tensor, *, stream=None) -> torch.Tensor:
-    """int8 W [N, K] -> the resident GEMV image (flat int8 tensor)."""
+    """int8 W [N, K] -> the resident GEMV image (flat int8 tensor; each
+    weight in offset binary, byte = w ^ 0x80)."""
     _mat(W, "W")
     N, K = W.shape
     out = torch.empty(int(lib.hxm_w8a16_packed_bytes(N, K)), dtype=torch.int8, device=W.device)
@@ -319,9 +320,9 @@ def gemm_w8a16(x: torch.Tensor, W: torch.Tensor, scale: torch.Tensor,
 
 def swiglu_pack(Wg: torch.Tensor, Wu: torch.Tensor, gate_scale: torch.Tensor,
                 up_scale: torch.Tensor, *, stream=None):
-    """The fused gate/up image (int8 [128*ceil(I/64), K]) and its fp32 scales
-    from gate/up weights int8 [I, K] and fp32 scales [I]; made once per
-    weight pair."""
+    """The fused gate/up image (int8 [128*ceil(I/64), K], each weight stored
+    in offset binary, byte = w ^ 0x80) and its fp32 scales from gate/up
+    weights int8 [I, K] and fp32 scales [I]; made once per weight pair."""
     _mat(Wg, "Wg"), _mat(Wu, "Wu")
     I, K = Wg.shape
     if tuple(Wu.shape) != (I, K) or _ld(Wu) != _ld(Wg):

@@ -248,8 +248,10 @@ hxm_status hxm_prepack_weight(const void* B, int64_t ldb, void* out,
  *                 ldw >= K.
  *   HXM_W_PACKED: W is the resident image made once by hxm_prepack_w8a16
  *                 (ldw ignored): 1 KiB blocks per (16 channels, 64 K), in the
- *                 order one wave instruction consumes them -- the GEMV's
- *                 counterpart of the reference's weight pre-pack
+ *                 order one wave instruction consumes them, each weight w
+ *                 stored in offset binary (byte = w ^ 0x80; padding holds
+ *                 zero weights, 0x80) -- the GEMV's counterpart of the
+ *                 reference's weight pre-pack
  *                 (backend/hmx_weight_prepack.py:171-183). */
 typedef enum hxm_w_layout { HXM_W_NK = 0, HXM_W_PACKED = 1 } hxm_w_layout;
 
@@ -353,7 +355,11 @@ int64_t hxm_swiglu_packed_rows(int64_t I);
  * contract, WeightResidentPass.cpp:10-53): Wgu int8 [hxm_swiglu_packed_rows(I),
  * K] (row stride K) whose rows [128c, 128c+64) are gate channels
  * [64c, 64c+64) and rows [128c+64, 128c+128) the same up channels, channels
- * >= I zero; sgu fp32 [rows] the matching scales (zero for padding).
+ * >= I zero; sgu fp32 [rows] the matching scales (zero for padding).  Each
+ * weight w is stored in offset binary, byte = w ^ 0x80 (w + 128 unsigned;
+ * a zero weight is 0x80), the form the GEMM converts to f16 without a sign
+ * flip; the image is this library's own and feeds only
+ * hxm_gemm_w8a16_swiglu.
  * Wg, Wu int8 [I,K] (ldw >= K); gate_scale, up_scale fp32 [I]. */
 hxm_status hxm_swiglu_pack(const int8_t* Wg, const int8_t* Wu, int64_t ldw,
                            const float* gate_scale, const float* up_scale,

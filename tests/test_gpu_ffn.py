@@ -156,7 +156,8 @@ def test_gemm_w8a16_residual_refusals(dev):
 
 def test_swiglu_pack_layout(dev):
     """Image rows [128c, 128c+64) = gate channels [64c, 64c+64), the next 64
-    rows the same up channels; channels >= I zero rows with zero scale."""
+    rows the same up channels; channels >= I zero rows with zero scale.
+    Weights are stored in offset binary: byte = w ^ 0x80 (zero -> 0x80)."""
     I, K = 100, 48
     g = torch.Generator().manual_seed(5)
     Wg = torch.randint(-127, 128, (I, K), generator=g, dtype=torch.int8)
@@ -165,13 +166,14 @@ def test_swiglu_pack_layout(dev):
     Wgu, sgu = ops.swiglu_pack(Wg.to(dev), Wu.to(dev), sg.to(dev), su.to(dev))
     rows = 128 * ((I + 63) // 64)
     assert tuple(Wgu.shape) == (rows, K) and sgu.numel() == rows
-    expW = np.zeros((rows, K), np.int8)
+    expW = np.full((rows, K), -128, np.int8)   # 0x80: a zero weight
     exps = np.zeros(rows, np.float32)
     for r in range(rows):
         ch = (r // 128) * 64 + r % 64
         if ch < I:
             src, ss = (Wu, su) if r % 128 >= 64 else (Wg, sg)
-            expW[r], exps[r] = src[ch].numpy(), ss[ch].item()
+            expW[r] = (src[ch].numpy().view(np.uint8) ^ 0x80).view(np.int8)
+            exps[r] = ss[ch].item()
     assert np.array_equal(Wgu.cpu().numpy(), expW)
     assert np.array_equal(sgu.cpu().numpy(), exps)
 

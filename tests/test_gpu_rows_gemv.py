@@ -171,15 +171,16 @@ def test_gemv_ragged(dev, M, N, K, packed):
 
 
 def test_w8a16_image_layout(dev):
-    """The image is a pure permutation of W with zero padding: block (g, s),
-    lane l holds W[16g + l%16][64s + 16(l//16) ... +16]."""
+    """The image is a permutation of W in offset binary (byte = w ^ 0x80)
+    with zero-weight padding (0x80): block (g, s), lane l holds
+    W[16g + l%16][64s + 16(l//16) ... +16] ^ 0x80."""
     N, K = 37, 208
     W = torch.randint(-127, 128, (N, K), dtype=torch.int8)
     img = ops.prepack_w8a16(W.to(dev)).cpu().numpy()
     ng, ns = (N + 15) // 16, (K + 63) // 64
     assert img.size == ng * ns * 1024
-    exp = np.zeros((ng, ns, 64, 16), dtype=np.int8)
-    Wn = W.numpy()
+    exp = np.full((ng, ns, 64, 16), -128, dtype=np.int8)   # 0x80: a zero weight
+    Wn = (W.numpy().view(np.uint8) ^ 0x80).view(np.int8)
     for gi in range(ng):
         for si in range(ns):
             for lane in range(64):

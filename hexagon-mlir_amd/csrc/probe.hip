@@ -1,8 +1,12 @@
 // HBM probes: a streaming copy and a streaming read with the same access
-// pattern as the HBM-bound kernels of this library (16-byte nontemporal
-// accesses, eight in flight per lane).  They measure the practical
-// ceiling those kernels are compared against; they have no counterpart in
-// the reference.
+// pattern as the HBM-bound kernels of this library (16-byte accesses, eight
+// in flight per lane): the copy loads plainly and stores nontemporally, as
+// the row kernels do; the read loads nontemporally, as the GEMV streams its
+// weights.  Each pairing is the faster one for its kind of stream (a copy
+// with nontemporal loads ran 22.2-22.6 us against 20.2 us for 64 MiB; a read
+// with plain loads 8.4 against 8.15 us for 45 MB).  They measure the
+// practical ceiling those kernels are compared against; they have no
+// counterpart in the reference.
 #include "device_util.h"
 #include "hxm_internal.h"
 
@@ -27,14 +31,14 @@ __global__ __launch_bounds__(kProbeThreads) void stream_copy_kernel(
       v4u32_t v[kProbeUnroll];
 #pragma unroll
       for (int u = 0; u < kProbeUnroll; ++u)
-        v[u] = __builtin_nontemporal_load(src + i + u * kProbeThreads);
+        v[u] = src[i + u * kProbeThreads];
 #pragma unroll
       for (int u = 0; u < kProbeUnroll; ++u)
         __builtin_nontemporal_store(v[u], dst + i + u * kProbeThreads);
     } else {
       for (int u = 0; u < kProbeUnroll; ++u)
         if (i + u * kProbeThreads < n16)
-          __builtin_nontemporal_store(__builtin_nontemporal_load(src + i + u * kProbeThreads),
+          __builtin_nontemporal_store(src[i + u * kProbeThreads],
                                       dst + i + u * kProbeThreads);
     }
   }

@@ -92,22 +92,24 @@ using RawVec = T __attribute__((ext_vector_type(RowVec<T>::N)));
 // Loads the vector at column c0 in storage form, columns >= cols set to
 // `fill`.  ALIGNED (16-byte aligned rows, cols a multiple of N): the vector
 // lies wholly inside the row or wholly past it, and one dwordx4 load reads
-// it, nontemporal (NT) for the rows, which are read once; gamma and beta are
-// shared by every row and stay cacheable.  A lane past the row loads column
-// 0 instead (a valid address) and takes the fill, so no branch splits the
-// wave's loads and all of them are in flight together.
-template <typename T, bool ALIGNED, bool NT = true>
+// it.  A lane past the row loads column 0 instead (a valid address) and takes
+// the fill, so no branch splits the wave's loads and all of them are in
+// flight together.
+//
+// Row loads are plain (cacheable) and row stores nontemporal.  On a stream
+// that reads and writes HBM at once this pairing ran fastest of the four
+// (64 MiB copy, one box: plain loads + nontemporal stores 20.2 us,
+// nontemporal both 22.2-22.6, nontemporal loads + plain stores 22.5, plain
+// both 24.6); RMSNorm 22.1 -> 20.8 us and softmax 22.9 -> 20.9 us at
+// 8192 x 4096 f16 with nontemporal loads replaced.  A read-only stream is the
+// other way round (the GEMV's weights stay nontemporal).
+template <typename T, bool ALIGNED>
 __device__ __forceinline__ RawVec<T> load_raw(const T* __restrict__ row, int64_t c0,
                                               int64_t cols, T fill) {
   constexpr int N = RowVec<T>::N;
   if constexpr (ALIGNED) {
     const bool in = c0 < cols;
-    const RawVec<T>* p = reinterpret_cast<const RawVec<T>*>(row + (in ? c0 : 0));
-    RawVec<T> v;
-    if constexpr (NT)
-      v = __builtin_nontemporal_load(p);
-    else
-      v = *p;
+    const RawVec<T> v = *reinterpret_cast<const RawVec<T>*>(row + (in ? c0 : 0));
     return in ? v : RawVec<T>(fill);
   }
   RawVec<T> v;
@@ -153,10 +155,15 @@ __device__ __forceinline__ void fresh(RawVec<T> (&v)[VPL]) {
 // S > 1 (full rows only): S waves share a row, each holding every S-th
 // vector, and the wave totals meet in LDS behind a barrier.  Each wave's
 // chain of arithmetic after its loads is S times shorter, and that chain is
-// what the last rows of the grid add after the last bytes land.  Measured
-// (8192 x 4096 f16, one box, S = 2): softmax 23.1 -> 22.8 us; RMSNorm 22.3
-// -> 23.9 and LayerNorm 23.1 -> 24.6 us, so only softmax, whose chain holds
-// the exponentials, takes it.
+// what the last rows of the grid add after the last bytes land.  Every op
+// takes it on full rows of 8 vectors per lane.  Measured (8192 x 4096 f16,
+// one box, two alternating passes each): S = 1 against S = 2, RMSNorm
+// 20.74 -> 20.20 us, LayerNorm 21.77 -> 20.70 us, softmax 20.86 -> 20.88 us;
+// S = 2 against S = 4 (one row per workgroup), softmax 20.87 -> 19.96 us,
+// RMSNorm 19.97 -> 19.84 us, LayerNorm 20.8 -> 20.94 us.  So softmax and
+// RMSNorm take four waves per row and LayerNorm two.  (With nontemporal row
+// loads S = 2 had gained softmax 23.1 -> 22.8 us and cost RMSNorm and
+// LayerNorm 1.5 us each.)
 template <typename T, int OP, int VPL, bool ALIGNED, bool FULL, int S = 1>
 __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
   static_assert(!FULL || ALIGNED, "full rows are aligned rows");
@@ -208,7 +215,7 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
   if constexpr (full) {
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
-      v[i] = __builtin_nontemporal_load(reinterpret_cast<const RawVec<T>*>(xr + col0(i)));
+      v[i] = *reinterpret_cast<const RawVec<T>*>(xr + col0(i));
   } else {
 #pragma unroll
     for (int i = 0; i < VPL; ++i) v[i] = load_raw<T, ALIGNED>(xr, col0(i), cols, fill);
@@ -218,12 +225,12 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
   auto gamma_at = [&](int i) {
     if (!g) return RawVec<T>(T(1));
     if constexpr (full) return plain(g, i);
-    return load_raw<T, ALIGNED, false>(g, col0(i), cols, T(0));
+    return load_raw<T, ALIGNED>(g, col0(i), cols, T(0));
   };
   auto beta_at = [&](int i) {
     if (!b) return RawVec<T>(T(0));
     if constexpr (full) return plain(b, i);
-    return load_raw<T, ALIGNED, false>(b, col0(i), cols, T(0));
+    return load_raw<T, ALIGNED>(b, col0(i), cols, T(0));
   };
 
   if constexpr (OP == kSoftmax) {
@@ -496,9 +503,12 @@ template <typename T, int OP, bool ALIGNED>
 hxm_status launch_rows_t(const RowArgs& a, hipStream_t stream) {
   constexpr int N = RowVec<T>::N;
   const int64_t vpl = (a.cols + 64 * N - 1) / (64 * N);
-  // Softmax on full rows of 8 vectors per lane: two waves per row.
-  const bool split = OP == kSoftmax && ALIGNED && a.cols == 8 * 64 * N;
-  const int64_t rows_per_group = split ? kRowWaves / 2 : kRowWaves;
+  // Full rows of 8 vectors per lane: SPLIT waves per row, four for softmax
+  // and RMSNorm, two for LayerNorm (its two dependent reductions cross the
+  // LDS twice).
+  constexpr int SPLIT = OP == kLayerNorm ? 2 : 4;
+  const bool split = ALIGNED && a.cols == 8 * 64 * N;
+  const int64_t rows_per_group = split ? kRowWaves / SPLIT : kRowWaves;
   const int64_t groups = (a.rows + rows_per_group - 1) / rows_per_group;
   hxm_status st = check_grid("row kernel", groups, 64 * kRowWaves);
   if (st != HXM_OK) return st;
@@ -507,9 +517,9 @@ hxm_status launch_rows_t(const RowArgs& a, hipStream_t stream) {
   // FULL kernels for aligned rows that fill the VPL slots exactly.
   auto run = [&](auto VPLC) {
     constexpr int V = decltype(VPLC)::value;
-    if constexpr (OP == kSoftmax && ALIGNED && V == 8) {
+    if constexpr (ALIGNED && V == 8) {
       if (split) {
-        row_kernel<T, OP, V / 2, true, true, 2><<<grid, block, 0, stream>>>(a);
+        row_kernel<T, OP, V / SPLIT, true, true, SPLIT><<<grid, block, 0, stream>>>(a);
         return;
       }
     }

@@ -422,8 +422,10 @@ hxm_status hxm_layernorm_rows(const void* x, int64_t ldx, const void* gamma,
 
 /* ---- HBM probes (measurement helpers; no counterpart in the reference) ----
  * The practical ceiling of the HBM-bound kernels above, measured with the
- * same access pattern (16-byte nontemporal accesses, eight in flight per
- * lane).  bytes: a multiple of 16; buffers 16-byte aligned. */
+ * same access pattern (16-byte accesses, eight in flight per lane; the copy
+ * loads plainly and stores nontemporally like the row kernels, the read
+ * loads nontemporally like the GEMV).  bytes: a multiple of 16; buffers
+ * 16-byte aligned. */
 #define HXM_PROBE_SINK_WORDS 8192
 
 /* dst[0, bytes) = src[0, bytes); the buffers must not overlap. */

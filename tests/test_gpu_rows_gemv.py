@@ -25,8 +25,9 @@ def tol(name):
 
 
 # (33, 4096), (5, 2048) and (1, 4096): full rows of 8 vectors per lane for
-# f16/bf16 and for f32, which softmax splits over two waves, with an odd row
-# count (the last workgroup's second row is past the end).
+# f16/bf16 and for f32, which every op splits over several waves (LayerNorm
+# two, with an odd row count the last workgroup's second row is past the
+# end; softmax and RMSNorm four, one row per workgroup).
 ROW_SHAPES = [(128, 128), (127, 513), (8192, 4096), (27, 8192), (5, 1), (3, 20000), (64, 1000),
               (33, 4096), (5, 2048), (1, 4096)]
 
@@ -56,7 +57,8 @@ def test_rmsnorm(dev, rows, cols, name):
     np.testing.assert_allclose(y.float().cpu().numpy(), ref, **tol(name))
 
 
-@pytest.mark.parametrize("rows,cols", [(27, 8192), (8192, 4096), (33, 300), (2, 17000)])
+@pytest.mark.parametrize("rows,cols", [(27, 8192), (8192, 4096), (33, 300), (2, 17000),
+                                       (33, 4096), (5, 2048), (1, 4096)])
 @pytest.mark.parametrize("name", ["f32", "f16"])
 def test_layernorm(dev, rows, cols, name):
     print(f"layernorm {name} {rows}x{cols}", flush=True)

@@ -690,10 +690,19 @@ def cpu_baseline(A, Bp, seconds):
 def sclk_under_load(c, fn, seconds=1.0, what="the headline GEMM"):
     """Shader clock (MHz) while `fn` runs back to back for about `seconds`:
     rocm-smi is sampled from a host thread during the loop.  Returns the
-    median sample and the raw samples, or None when rocm-smi gives nothing."""
+    median sample and the raw samples, or None when rocm-smi gives nothing.
+
+    Under a profiler (rocprofv3 preloads its library into every child
+    process, and that library initialises the GPU) rocm-smi is not started:
+    its launcher script hands over to python3 by exec, which must not happen
+    in a process that has initialised the GPU.  The record then says so."""
     import re
     import subprocess
     import threading
+    if any(k.startswith("ROCPROF") for k in os.environ) or \
+            "rocprofiler" in os.environ.get("LD_PRELOAD", ""):
+        log(f"clock sampling skipped under a profiler ({what})")
+        return None
     samples, stop = [], threading.Event()
 
     def sample():

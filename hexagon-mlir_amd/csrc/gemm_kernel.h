@@ -394,8 +394,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   // Fragments of the k-step being multiplied ([ks & 1]) and of the next one.
   // Read R of a k-step: A block 0, the FN B blocks, then A blocks 1..FM-1 --
   // the order the MFMA slots (i, j) = (s / FN, s % FN) first need them.
-  // With an int8 B the read brings the lane's 8 bytes (K range
-  // [16ks + 8hi, +8) of its row) into braw, and the slots run column-major,
+  // With an int8 B the read brings the lane's 16 bytes of a pair of k-steps
+  // (below) into braw, and the slots run column-major,
   // (i, j) = (s % FM, s / FM), so B block j is first needed at slot j*FM:
   // its conversion to f16 (cvt_word, four words) is spread over the FM slots
   // before that, block 0's over the end of the previous k-step.  A wave is
@@ -403,31 +403,55 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   // the second one needs (ten dependent VALU operations, longer than one
   // MFMA) would leave the matrix core idle.  The B reads come first, then
   // the A blocks.
+  //
+  // int8 B is read a pair of k-steps at a time.  The K order inside a pair
+  // of MFMAs is free as long as A and B follow the same one, so the pair's
+  // 32 K values are split by lane half, not by k-step: lane half hi takes K
+  // [32p + 16hi, +16) of pair p, the first 8 values for the pair's first
+  // MFMA and the next 8 for its second.  Those 16 bytes are one 16-byte
+  // chunk of the B row, so one ds_read_b128 per lane serves both k-steps,
+  // and 16 consecutive rows at one chunk index fall on distinct banks under
+  // the swizzle.  (Per k-step, each lane half took the matching 8 bytes of a
+  // chunk, and the 32 lanes of a half met every bank twice: measured
+  // SQ_LDS_BANK_CONFLICT of the FFN's GEMMs was about one conflict cycle per
+  // LDS instruction.)  A's chunk for k-step ks = 2p + j is then 4p + 2hi + j.
   v4i32 af[2][FM], bf[2][FN];
-  uint2 braw[2][BQ ? FN : 1];
-  uint32_t bflip[2][BQ ? FN : 1][2];  // braw in offset binary (sign bits inverted)
+  uint4 braw[2][BQ ? FN : 1];         // [pair parity]: both k-steps of a pair
+  uint32_t bflip[2][BQ ? FN : 1][2];  // [k-step parity]: its words in offset binary
   const int r32 = lane & 31, hi = lane >> 5;
-  auto read = [&](auto R, int dstb, const uint8_t* stage, int ks) {
+  static_assert(!BQ || KS % 4 == 0, "int8 B pairs: an even number of pairs per stage");
+  auto read = [&](auto R, int dstb, const uint8_t* stage, auto KSC) {
     constexpr int r = decltype(R)::value;
+    constexpr int ks = decltype(KSC)::value;
     constexpr bool is_b = BQ ? r < FN : r >= 1 && r <= FN;
     constexpr int idx = BQ ? (is_b ? r : r - FN) : r == 0 ? 0 : is_b ? r - 1 : r - FN;
     if constexpr (is_b && BQ) {
-      const int row = idx * 32 + r32;
-      braw[dstb][idx] = *reinterpret_cast<const uint2*>(
-          stage + BM * BKB + (wn * TN + row) * BKB_B + ((ks ^ swz<BKB_B>(row)) << 4) + hi * 8);
+      if constexpr (ks % 2 == 0) {  // the pair (ks, ks + 1)
+        const int row = idx * 32 + r32;
+        braw[(ks >> 1) & 1][idx] = *reinterpret_cast<const uint4*>(
+            stage + BM * BKB + (wn * TN + row) * BKB_B + (((ks + hi) ^ swz<BKB_B>(row)) << 4));
+      }
     } else if constexpr (is_b) {
       bf[dstb][idx] = lds_frag<BKB>(stage + (BM + wn * TN) * BKB, idx * 32 + r32, ks * 2 + hi);
+    } else if constexpr (BQ) {
+      af[dstb][idx] = lds_frag<BKB>(stage + (wm * TM) * BKB, idx * 32 + r32,
+                                    4 * (ks >> 1) + 2 * hi + (ks & 1));
     } else {
       af[dstb][idx] = lds_frag<BKB>(stage + (wm * TM) * BKB, idx * 32 + r32, ks * 2 + hi);
     }
   };
-  // Word P of B block j's f16 fragment (elements 2P, 2P+1) from braw[b][j].
-  auto cvt_word = [&](auto P, int b, int j) {
+  // Word P of B block j's f16 fragment (elements 2P, 2P+1) for k-step ks of
+  // a stage, from its pair's braw words 2 * (ks & 1) and 2 * (ks & 1) + 1.
+  auto cvt_word = [&](auto P, auto KSC, int j) {
     constexpr int p = decltype(P)::value;
+    constexpr int ks = decltype(KSC)::value;
+    constexpr int b = ks & 1;
     if constexpr (BQ) {
-      if constexpr (p % 2 == 0)
-        bflip[b][j][p / 2] = (p == 0 ? braw[b][j].x : braw[b][j].y) ^
-                             (b_offset_binary(EPI) ? 0u : 0x80808080u);
+      if constexpr (p % 2 == 0) {
+        const uint4& w = braw[(ks >> 1) & 1][j];
+        const uint32_t raw = b == 0 ? (p == 0 ? w.x : w.y) : (p == 0 ? w.z : w.w);
+        bflip[b][j][p / 2] = raw ^ (b_offset_binary(EPI) ? 0u : 0x80808080u);
+      }
       bf[b][j][p] = static_cast<int>(i8x2_flipped_to_f16<p % 2>(bflip[b][j][p / 2]));
     }
   };
@@ -436,17 +460,17 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   // first use, words of block 0 of the next k-step in the last FM slots (in
   // the last k-step of a stage, whose reads of the next stage start at the
   // barrier, in its last two slots).
-  auto cvt_slot = [&](auto KSI, auto SI, int cb) {
+  auto cvt_slot = [&](auto KSI, auto SI) {
     constexpr int ks = decltype(KSI)::value, sl = decltype(SI)::value;
     if constexpr (BQ) {
       static_for<0, 4>([&](auto P) {
         constexpr int p = decltype(P)::value;
         static_for<1, FN>([&](auto J) {
           constexpr int j = decltype(J)::value;
-          if constexpr ((j - 1) * FM + (p * FM) / 4 == sl) cvt_word(P, cb, j);
+          if constexpr ((j - 1) * FM + (p * FM) / 4 == sl) cvt_word(P, KSI, j);
         });
         constexpr int s0 = ks == KS - 1 ? NF - 2 + p / 2 : (FN - 1) * FM + (p * FM) / 4;
-        if constexpr (s0 == sl) cvt_word(P, cb ^ 1, 0);
+        if constexpr (s0 == sl) cvt_word(P, std::integral_constant<int, (ks + 1) % KS>{}, 0);
       });
     }
   };
@@ -507,14 +531,16 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         static_for<0, NR>([&](auto R) {
           constexpr int r = decltype(R)::value;
           if constexpr (ks < KS - 1) {
-            if constexpr ((r * NF) / NR == sl) read(R, cb ^ 1, cur, ks + 1);
+            if constexpr ((r * NF) / NR == sl)
+              read(R, cb ^ 1, cur, std::integral_constant<int, ks + 1>{});
           } else {
-            if constexpr (HALF + (r * (NF - HALF)) / NR == sl) read(R, cb ^ 1, nxt, 0);
+            if constexpr (HALF + (r * (NF - HALF)) / NR == sl)
+              read(R, cb ^ 1, nxt, std::integral_constant<int, 0>{});
           }
         });
         constexpr int i = BQ ? sl % FM : sl / FN, j = BQ ? sl / FM : sl % FN;
         acc[i][j] = Mfma<T>::run(bf[cb][j], af[cb][i], acc[i][j]);
-        cvt_slot(KSI, SI, cb);
+        cvt_slot(KSI, SI);
         __builtin_amdgcn_sched_barrier(0);
       });
     });
@@ -531,8 +557,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         dma(D, std::true_type{}, buf(STAGES - 1), (STAGES - 1) * BKB);
     });
     wait_and_barrier<(STAGES - 2) * LPW + NEG>();
-    static_for<0, NR>([&](auto R) { read(R, 0, buf(0), 0); });
-    static_for<0, 4>([&](auto P) { cvt_word(P, 0, 0); });
+    static_for<0, NR>([&](auto R) { read(R, 0, buf(0), std::integral_constant<int, 0>{}); });
+    static_for<0, 4>([&](auto P) { cvt_word(P, std::integral_constant<int, 0>{}, 0); });
 
     // Main loop, unrolled by STAGES so every buffer choice is static.  It is
     // compiled twice: without the per-lane K test (K_bytes a multiple of the

@@ -191,7 +191,10 @@ def swiglu_operands(M, I, K, seed):
 
 
 @pytest.mark.parametrize("M,I,K", [(256, 128, 512), (300, 100, 1024), (17, 64, 64),
-                                   (512, 704, 1024)])
+                                   (512, 704, 1024),
+                                   # K not a multiple of the 64-wide stage: the last stage's
+                                   # zero-filled K (zero x against offset-binary zero bytes)
+                                   (40, 96, 656), (9, 64, 48)])
 def test_gemm_w8a16_swiglu(dev, M, I, K):
     print(f"swiglu M={M} I={I} K={K}", flush=True)
     x, Wg, Wu, sg, su = swiglu_operands(M, I, K, M + I)

@@ -11,8 +11,10 @@
 // 64 lanes x 16 vectors x 16 bytes is loaded ONCE into registers with 128-bit
 // coalesced loads (consecutive lanes read consecutive 16-byte chunks), reduced
 // across the wave with DPP + readlane (no LDS, no barriers) and written back
-// from registers: one HBM read and one HBM write per element.  Longer rows use
-// the streaming variant (VPL = 0) that re-reads the row per pass.
+// from registers: one HBM read and one HBM write per element.  Full rows of 8
+// vectors per lane (4096 f16) are split over two or four waves whose totals
+// meet in LDS (see row_kernel).  Longer rows use the streaming variant
+// (VPL = 0) that re-reads the row per pass.
 #include <type_traits>
 
 #include "device_util.h"

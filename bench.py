@@ -782,7 +782,11 @@ def main() -> int:
         extra["int8_gemm_i32_out_4096"] = run_int8(c, A, Bp, rs, cs, out_i32=True)
         for fn in (run_f16, run_ragged, run_gemv, run_rows, run_ffn, run_shard, run_copy,
                    run_vendor, run_search):
-            extra.update(fn(c))
+            try:
+                extra.update(fn(c))
+            except Exception as e:  # a failed context leg is reported, the headline still runs
+                log(f"{fn.__name__} failed: {e!r}")
+                extra[fn.__name__] = {"error": repr(e)}
         for k, v in extra.items():
             log(k, json.dumps(v))
     # The headline last: the legs above have brought the clock to its

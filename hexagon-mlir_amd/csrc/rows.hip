@@ -332,13 +332,14 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
     }
   } else {  // kLayerNorm
     // The row is widened into mixed-precision fmas as in RMSNorm: the sum as
-    // fma(x, 1, s), the centred values as fma(x, 1, -mean) (exactly
-    // x - mean, rounded once), the output as fma(fma(x, rstd, -mean*rstd),
-    // gamma, beta), with `one` hidden from the optimizer so x*1 stays an
-    // fma.  The VALU work per element halves (the kernel is VALU-limited at
-    // four waves per SIMD); measured 25.74 against 26.52 us.  The output
-    // contracts (x - mean)*rstd*gamma + beta into two fmas, which differs
-    // from separately rounded steps in the last fp32 bit only.
+    // fma(x, 1, s), the centred values as fma(x, 1, -mean) (x - mean,
+    // rounded once), with `one` hidden from the optimizer so x*1 stays an
+    // fma.  The output is fma((x - mean) * rstd, gamma, beta) from the same
+    // centred value: it differs from separately rounded steps in the last
+    // fp32 bit only.  (A form that folded the mean into one fma,
+    // fma(fma(x, rstd, -mean*rstd), gamma, beta), saved an operation per
+    // element but lost the cancellation: a constant row gave beta plus the
+    // rounding error of mean*rstd instead of beta.)
     float one = 1.0f;
     asm volatile("" : "+v"(one));
     // A scheduling barrier closes each vector of every pass: the passes
@@ -386,14 +387,15 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
       if (a.mean_out) a.mean_out[r] = mean;
       if (a.rstd_out) a.rstd_out[r] = rstd;
     }
-    const float c0 = nmean * rstd;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const RawVec<T> gi = gamma_at(i), bi = beta_at(i);
       RawVec<T> o;
 #pragma unroll
-      for (int j = 0; j < N; ++j)
-        o[j] = fromf<T>(fmaf(fmaf(tof(v[i][j]), rstd, c0), tof(gi[j]), tof(bi[j])));
+      for (int j = 0; j < N; ++j) {
+        const float d = fmaf(tof(v[i][j]), one, nmean);
+        o[j] = fromf<T>(fmaf(d * rstd, tof(gi[j]), tof(bi[j])));
+      }
       if (valid) store_raw<T, ALIGNED>(yr, col0(i), cols, o);
       __builtin_amdgcn_sched_barrier(0);
     }

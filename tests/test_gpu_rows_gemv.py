@@ -75,6 +75,27 @@ def test_layernorm(dev, rows, cols, name):
     np.testing.assert_allclose(rstd.cpu().numpy(), rr, rtol=1e-4)
 
 
+@pytest.mark.parametrize("rows,cols", [(4, 4096), (5, 2048), (3, 300), (2, 1), (2, 17000)])
+@pytest.mark.parametrize("name", ["f32", "f16"])
+def test_layernorm_constant_rows_give_beta(dev, rows, cols, name):
+    """Closed form: a constant row has x - mean = 0 exactly and variance 0,
+    so LayerNorm returns beta exactly whatever gamma and the constant, with
+    mean = the constant and rstd = 1/sqrt(eps).  The constants keep every
+    partial sum exact in fp32, so no summation order can move the mean."""
+    print(f"layernorm constant rows {name} {rows}x{cols}", flush=True)
+    g = torch.Generator().manual_seed(rows * 3 + cols)
+    consts = torch.tensor([1.5, -3.25, 96.0, 0.375, -7.0][:rows])
+    x = consts[:, None].expand(rows, cols).contiguous().to(TDT[name])
+    w = (1 + 0.1 * torch.randn(cols, generator=g)).to(TDT[name])
+    b = torch.randn(cols, generator=g).to(TDT[name])
+    y, mean, rstd = ops.layer_norm(x.to(dev), (cols,), w.to(dev), b.to(dev), eps=1e-5,
+                                   return_stats=True)
+    assert torch.equal(y.cpu(), b.expand(rows, cols)), "y must equal beta"
+    assert torch.equal(mean.cpu(), consts)
+    want = np.float32(1.0) / np.sqrt(np.float32(1e-5))
+    np.testing.assert_allclose(rstd.cpu().numpy(), np.full(rows, want, np.float32), rtol=1e-6)
+
+
 def test_rows_golden(dev, golden):
     g = golden("rows")
     xs = torch.from_numpy(g["softmax_x_bits"].view(np.float16)).to(dev)

@@ -1,0 +1,168 @@
+"""Seeded random-shape parity sweeps against the CPU oracle: shapes, layouts,
+strides and value patterns drawn from a fixed generator, so every run checks
+the same cases and a failure names its case.
+
+* int8 GEMM (both B layouts, accumulate, dequant) bit-exact, including K
+  splits on every tile shape and outputs written into wider buffers (the
+  columns past N must stay untouched);
+* f16 / bf16 matmul, W8A16 GEMM, GEMV (packed and plain) and the fused
+  SwiGLU gate/up GEMM within rtol 1e-2 / atol 1e-3;
+* softmax / RMSNorm / LayerNorm on f16, bf16 and f32 rows of every kernel
+  shape (register, split, unaligned, streaming) with offset, large, tiny and
+  N(0,1) values; f32 rows are held to rtol 1e-4 / atol 1e-5.
+
+A sweep like this, with f32 held to 1e-5, found the LayerNorm output form
+that lost the cancellation of x - mean (a one-column row was off by 1.6e-5);
+test_layernorm_constant_rows_give_beta pins that case by its closed form.
+Here f32 is held to 1e-4 because offset rows move the fp32 mean with the
+summation order."""
+import random
+
+import numpy as np
+import pytest
+import torch
+
+import hxm
+import hxm.ops as ops
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(rtol=1e-2, atol=1e-3)
+TDT = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def host_bits(t, name):
+    return t.numpy() if name == "f32" else t.view(torch.int16).numpy().view(np.uint16)
+
+
+TILES = [(256, 256, 128, 2, 2, 2), (128, 128, 128, 2, 2, 2), (64, 64, 128, 2, 2, 2),
+         (32, 32, 128, 1, 1, 2), (256, 128, 128, 4, 1, 3), (128, 256, 64, 2, 2, 4)]
+
+
+def test_random_int8_gemms_bit_exact(dev):
+    rng = random.Random(4321)
+    for it in range(24):
+        M, N = rng.randint(1, 600), rng.randint(1, 600)
+        K = 16 * rng.randint(1, 130)
+        lay = rng.choice(["kn", "nk"])
+        case = f"case {it}: {M}x{N}x{K} {lay}"
+        print(case, flush=True)
+        g = torch.Generator().manual_seed(it)
+        A = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+        B = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+        Bd = B.to(dev) if lay == "kn" else ops.prepack_weight(B.to(dev))
+        ref = orc.gemm_i8(A.numpy(), B.numpy())
+        assert np.array_equal(ops.gemm_i8(A.to(dev), Bd, b_layout=lay).cpu().numpy(), ref), case
+        C0 = torch.randint(-1000, 1000, (M, N), generator=g, dtype=torch.int32)
+        Ca = C0.to(dev)
+        ops.gemm_i8(A.to(dev), Bd, out=Ca, b_layout=lay, accumulate=True)
+        assert np.array_equal(Ca.cpu().numpy(), ref + C0.numpy()), case + " accumulate"
+        rs = torch.rand(M, generator=g) * 0.019 + 0.001
+        cs = torch.rand(N, generator=g) * 0.019 + 0.001
+        D = ops.gemm_i8_dequant(A.to(dev), Bd, rs.to(dev), cs.to(dev), b_layout=lay)
+        assert np.array_equal(bits(D), orc.dequant_f16(ref, rs.numpy(), cs.numpy())), case + " dequant"
+
+
+def test_random_int8_split_k_and_strided_outputs(dev):
+    rng = random.Random(99)
+    for it in range(24):
+        M, N = rng.randint(1, 700), rng.randint(1, 700)
+        K = 16 * rng.randint(1, 300)
+        tile, S = rng.choice(TILES), rng.choice([1, 2, 4, 8, 16])
+        ldc = N + rng.choice([0, 8, 64])
+        case = f"case {it}: {M}x{N}x{K} tile {tile} split {S} ldc {ldc}"
+        print(case, flush=True)
+        g = torch.Generator().manual_seed(it)
+        A = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+        B = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+        ref = orc.gemm_i8(A.numpy(), B.numpy())
+        cfg = hxm.GemmConfig(*tile, S)
+        C = ops.gemm_i8(A.to(dev), ops.prepack_weight(B.to(dev)), b_layout="nk", config=cfg)
+        assert np.array_equal(C.cpu().numpy(), ref), case
+        buf = torch.full((M, ldc), -5, dtype=torch.int32, device=dev)
+        ops.gemm_i8(A.to(dev), B.to(dev), out=buf[:, :N], config=cfg)
+        got = buf.cpu().numpy()
+        assert np.array_equal(got[:, :N], ref), case + " strided"
+        assert (got[:, N:] == -5).all(), case + " wrote past N"
+
+
+def test_random_float_and_w8a16_gemms(dev):
+    rng = random.Random(1234)
+    for it in range(20):
+        M, N, K = rng.randint(1, 400), rng.randint(1, 400), 8 * rng.randint(1, 80)
+        dt = rng.choice(["f16", "bf16"])
+        case = f"matmul case {it}: {dt} {M}x{N}x{K}"
+        print(case, flush=True)
+        g = torch.Generator().manual_seed(1000 + it)
+        A = (torch.rand(M, K, generator=g) * 2 - 1).to(TDT[dt])
+        B = (torch.rand(K, N, generator=g) * 2 - 1).to(TDT[dt])
+        ref = orc.to_f32(orc.matmul(bits(A), bits(B), ab_dtype=dt, c_dtype=dt), dt)
+        np.testing.assert_allclose(ops.matmul(A.to(dev), B.to(dev)).float().cpu().numpy(), ref,
+                                   **TOL, err_msg=case)
+    for it in range(20):
+        M = rng.choice([1, 3, 17, 64, 130, 257, 300])
+        N = rng.choice([8, 40, 100, 256, 333, 520])
+        K = 16 * rng.randint(1, 70)
+        I = rng.choice([16, 64, 100, 200])
+        case = f"w8a16 case {it}: M={M} N={N} K={K} I={I}"
+        print(case, flush=True)
+        g = torch.Generator().manual_seed(it)
+        x = torch.randn(M, K, generator=g).half()
+        W = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+        s = (torch.rand(N, generator=g) * 0.019 + 0.001).half().float()
+        ref = orc.f16_bits_to_f32(orc.gemm_w8a16(bits(x), W.numpy(), s.numpy()))
+        y = ops.gemm_w8a16(x.to(dev), W.to(dev), s.to(dev))
+        np.testing.assert_allclose(y.float().cpu().numpy(), ref, **TOL, err_msg=case)
+        if M <= 16:
+            sh = s.half()
+            refv = orc.f16_bits_to_f32(orc.gemv_w8a16(bits(x), W.numpy(), bits(sh)))
+            for packed in (True, False):
+                Wd = ops.prepack_w8a16(W.to(dev)) if packed else W.to(dev)
+                yv = ops.gemv_w8a16(x.to(dev), Wd, sh.to(dev), N=N)
+                np.testing.assert_allclose(yv.float().cpu().numpy(), refv, **TOL,
+                                           err_msg=f"{case} gemv packed={packed}")
+        Wg = torch.randint(-127, 128, (I, K), generator=g, dtype=torch.int8)
+        Wu = torch.randint(-127, 128, (I, K), generator=g, dtype=torch.int8)
+        sg = torch.rand(I, generator=g) * 0.004 + 0.001
+        su = torch.rand(I, generator=g) * 0.004 + 0.001
+        Wgu, sgu = ops.swiglu_pack(Wg.to(dev), Wu.to(dev), sg.to(dev), su.to(dev))
+        h = ops.gemm_w8a16_swiglu(x.to(dev), Wgu, sgu, I)
+        refh = orc.f16_bits_to_f32(orc.swiglu_gateup(bits(x), Wg.numpy(), Wu.numpy(),
+                                                     sg.numpy(), su.numpy()))
+        np.testing.assert_allclose(h.float().cpu().numpy(), refh, **TOL, err_msg=case + " swiglu")
+
+
+def test_random_rows_with_value_patterns(dev):
+    rng = random.Random(2024)
+    for it in range(40):
+        name = rng.choice(["f16", "bf16", "f32"])
+        rows = rng.choice([1, 2, 4, 7, 33])
+        cols = rng.choice([1, 2, 7, 8, 64, 100, 513, 1024, 2048, 4096, 5000, 9000, 20000])
+        kind = rng.choice(["offset", "big", "tiny", "normal"])
+        case = f"case {it}: {name} {rows}x{cols} {kind}"
+        print(case, flush=True)
+        g = torch.Generator().manual_seed(2000 + it)
+        x = torch.randn(rows, cols, generator=g)
+        x = {"offset": x * 0.5 + 20.0, "big": x * 8.0, "tiny": x * 1e-3, "normal": x}[kind]
+        x = x.to(TDT[name])
+        w = (1 + 0.1 * torch.randn(cols, generator=g)).to(TDT[name])
+        tol = TOL if name != "f32" else dict(rtol=1e-4, atol=1e-5)
+        ref = orc.to_f32(orc.softmax_rows(host_bits(x, name), name), name)
+        np.testing.assert_allclose(ops.softmax(x.to(dev)).float().cpu().numpy(), ref, **tol,
+                                   err_msg=case + " softmax")
+        ref = orc.to_f32(orc.rmsnorm_rows(host_bits(x, name), host_bits(w, name), 1e-6, name),
+                         name)
+        y = ops.rms_norm(x.to(dev), (cols,), weight=w.to(dev), eps=1e-6)
+        np.testing.assert_allclose(y.float().cpu().numpy(), ref, **tol, err_msg=case + " rms")
+        if name != "bf16":
+            b = (0.1 * torch.randn(cols, generator=g)).to(TDT[name])
+            ry, _, _ = orc.layernorm_rows(host_bits(x, name), host_bits(w, name),
+                                          host_bits(b, name), 1e-5, name)
+            y = ops.layer_norm(x.to(dev), (cols,), w.to(dev), b.to(dev), eps=1e-5)
+            np.testing.assert_allclose(y.float().cpu().numpy(), orc.to_f32(ry, name), **tol,
+                                       err_msg=case + " layernorm")

@@ -69,8 +69,9 @@ enum { kCanaryOk = 0, kCanaryMissing = 1, kCanaryUnmeasured = 2, kCanaryDrift = 
        kCanaryReference = 4 };
 
 // The gated walk over arms 0..n-1 in index order from the incumbent
-// `start`: a challenger takes the crown only when its median is lower than
-// the incumbent's by more than the gate of the noisier of the two.  Arms
+// `start`: a challenger replaces the current champion only when its median
+// is lower than the champion's by more than the gate of the noisier of the
+// two.  Arms
 // with no finite median are passed over.  arm(i) yields arm i's
 // hxm_arm_quantiles.  Returns the survivor, -1 when `start` is not a
 // measured arm.
@@ -585,8 +586,8 @@ int32_t hxm_calibration_iters(double perf_us, double target_us, int32_t lo, int3
 
 /* The gated walk of judge_champion_round (hmx_search.py:1460-1478): rows
  * in enumeration order; `start` is the incumbent's index; rows whose q50 is
- * not finite are skipped (outcome -1); a challenger takes the crown when
- * (q50_inc - q50_ch) / q50_inc > max(3*max(cv_ch, cv_inc), 15%).
+ * not finite are skipped (outcome -1); a challenger replaces the champion
+ * when (q50_inc - q50_ch) / q50_inc > max(3*max(cv_ch, cv_inc), 15%).
  * outcome[i]: -1 not compared, 0 kept, 1 takeover.  Returns the champion. */
 int32_t hxm_champion_walk(const double* q20, const double* q50, const double* q80,
                           int32_t n, int32_t start, int32_t* outcome,

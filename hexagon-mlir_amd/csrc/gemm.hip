@@ -353,10 +353,34 @@ hxm_status plan_gemm(int32_t op, int32_t table, int epi, int32_t b_layout, int64
   } else if (lookup_tuned(op == HXM_F32 ? HXM_F16 : op, M, N, K, &c)) {
     p->source = HXM_SOURCE_TUNED;
   } else {
-    c = default_config(M, N, table);
+    c = epi == kEpiFloat && small_gemm_fits(M, N, K, table) ? small_gemm_config()
+                                                             : default_config(M, N, table);
     p->source = HXM_SOURCE_DEFAULT;
   }
   p->config = c;
+  if (is_small_gemm_config(c)) {  // the direct-load small-output kernel
+    hxm_status st = HXM_OK;
+    if (epi != kEpiFloat || !small_gemm_fits(M, N, K, table)) {
+      snprintf(why, sizeof(why),
+               "the direct small-output kernel takes f16/bf16 operands, at most %lld 16x16 "
+               "output tiles and 0 < K <= %lld",
+               (long long)kSmallTilesMax, (long long)kSmallKMax);
+      st = refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_NO_KERNEL, why);
+    } else {
+      p->config = small_gemm_config();
+      p->threads = 64;
+      p->tiles = ((M + 15) / 16) * ((N + 15) / 16);
+      p->lds_bytes = 0;
+      p->workspace_bytes = extra_ws + (b_layout == HXM_B_KN ? N * K * eb : 0);
+      p->k_slices = 1;
+      const bool full = M % 16 == 0 && N % 16 == 0 && K % 32 == 0;
+      p->plan = full ? HXM_PLAN_MFMA_FULL : HXM_PLAN_MFMA_TAIL;
+      p->reason = full ? HXM_REASON_SELECTED_ALIGNED : HXM_REASON_SELECTED_TAIL;
+    }
+    g_last_plan = *p;
+    if (entry) *entry = nullptr;
+    return st;
+  }
   hxm_status st = HXM_OK;
   const KernelEntry* e = find_kernel(c, table);
   if (!e) {
@@ -423,6 +447,12 @@ static hxm_status run_gemm_with(int32_t op, int32_t ab_dtype, int epi, const voi
   int64_t ldb_bytes = 0;
   if (K > 0 && (st = resolve_b(B, ldb, b_layout, K, N, eb, stream, &bk, &ldb_bytes)) != HXM_OK)
     return st;
+  if (!e) {  // the plan chose the direct-load small-output kernel
+    if ((st = launch_small_gemm(ab_dtype, A, lda, bk, ldb_bytes, C, ldc, M, N, K, out_dtype,
+                                accumulate, stream)) != HXM_OK)
+      return st;
+    return ok();
+  }
   GemmArgs g;
   g.A = static_cast<const uint8_t*>(A);
   g.B = bk;

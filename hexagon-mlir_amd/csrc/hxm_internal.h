@@ -72,6 +72,20 @@ int32_t gpu_lattice(const hxm_gemm_config& c, int64_t a_bytes, int64_t b_bytes,
 // Frees the resident weight images of device `dev` (resident.hip).
 hxm_status release_images(int dev);
 
+// The direct-load small-output GEMM (gemm_small.hip): f16 / bf16 A [M, K]
+// and B as the [N, K] image, one wave per 16x16 output tile, no LDS.  The
+// default of hxm_matmul for outputs of at most kSmallTilesMax 16x16 tiles
+// and K <= kSmallKMax; a caller names it with small_gemm_config().
+constexpr int64_t kSmallTilesMax = 512;
+constexpr int64_t kSmallKMax = 256;
+hxm_gemm_config small_gemm_config();
+bool is_small_gemm_config(const hxm_gemm_config& c);
+bool small_gemm_fits(int64_t M, int64_t N, int64_t K, int32_t ab_dtype);
+hxm_status launch_small_gemm(int32_t ab_dtype, const void* A, int64_t lda, const uint8_t* B,
+                             int64_t ldb_bytes, void* C, int64_t ldc, int64_t M, int64_t N,
+                             int64_t K, int32_t out_dtype, int32_t accumulate,
+                             hipStream_t stream);
+
 }  // namespace hxm
 
 #define HXM_HIP_TRY(expr)                                                    \

@@ -185,7 +185,12 @@ int32_t hxm_last_plan(hxm_plan* out);
  * A/B 16-byte aligned ("tile-alignment" otherwise); M and N are free.
  * 256 rows of A and of the [N,K] B image must lie within 2 GiB
  * (255 * ld * sizeof(elem) + K * sizeof(elem) < 2^31; "tile-alignment"
- * otherwise): the kernels address a tile's rows with 32-bit offsets. */
+ * otherwise): the kernels address a tile's rows with 32-bit offsets.
+ * With cfg NULL and no tuned winner, an output of at most 512 16x16 tiles
+ * with K <= 256 runs on the direct-load small-output kernel (config
+ * {16,16,32,1,1,0,1}, one wave per 16x16 tile, no LDS); the same config
+ * passed in cfg asks for it and is refused (HXM_UNSUPPORTED_SHAPE,
+ * "no-kernel") outside those limits. */
 hxm_status hxm_matmul(const void* A, int64_t lda, const void* B, int64_t ldb,
                       int32_t b_layout, void* C, int64_t ldc, int64_t M,
                       int64_t N, int64_t K, int32_t ab_dtype, int32_t c_dtype,

@@ -485,3 +485,56 @@ def test_matmul_through_memref_descriptors(dev):
     ref = orc.matmul(bits(a), bits(b), c_dtype="f32")
     np.testing.assert_allclose(got[:, 8:8 + N].numpy(), ref, rtol=1e-2, atol=1e-3)
     assert torch.count_nonzero(got[:, :8]) == 0
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (1, 1, 8), (17, 33, 40), (100, 70, 72),
+                                   (300, 260, 200), (16, 512, 256)])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_small_output_kernel(dev, M, N, K, dt):
+    """The direct-load small-output kernel, the default for f16 / bf16 outputs
+    of at most 512 16x16 tiles with K <= 256 (BASELINE config 1 is 256^3):
+    the plan names it, and its f16 / bf16 / f32 outputs, with and without
+    accumulate, from [K, N] and [N, K] B, are within tolerance of the oracle.
+    K = 8, 40, 72, 200 end inside a 32-wide k-step."""
+    print(f"small kernel {dt} M={M} N={N} K={K}", flush=True)
+    small = (16, 16, 32, 1, 1, 0, 1)
+    name = "f16" if dt == torch.float16 else "bf16"
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    a = (torch.rand(M, K, generator=g) * 2 - 1).to(dt)
+    b = (torch.rand(K, N, generator=g) * 2 - 1).to(dt)
+    ad, bd = a.to(dev), b.to(dev)
+    c = ops.matmul(ad, bd)
+    assert ops.last_plan()["config"] == small
+    ref = orc.to_f32(orc.matmul(bits(a), bits(b), ab_dtype=name, c_dtype=name), name)
+    np.testing.assert_allclose(c.float().cpu().numpy(), ref, rtol=1e-2, atol=1e-3)
+    c32 = ops.matmul(ad, b.t().contiguous().to(dev), b_layout="nk", out_dtype=torch.float32)
+    assert ops.last_plan()["config"] == small
+    ref32 = orc.matmul(bits(a), bits(b), ab_dtype=name, c_dtype="f32")
+    np.testing.assert_allclose(c32.cpu().numpy(), ref32, rtol=1e-4, atol=1e-4)
+    C0 = torch.randn(M, N, generator=g)
+    acc32 = C0.to(dev)
+    ops.matmul(ad, bd, out=acc32, accumulate=True)
+    ref_acc = orc.matmul(bits(a), bits(b), ab_dtype=name, c_dtype="f32", C=C0.numpy(),
+                         accumulate=True)
+    np.testing.assert_allclose(acc32.cpu().numpy(), ref_acc, rtol=1e-4, atol=1e-4)
+    C0h = C0.to(dt)
+    acch = C0h.to(dev)
+    ops.matmul(ad, bd, out=acch, accumulate=True)
+    ref_acch = orc.to_f32(orc.matmul(bits(a), bits(b), ab_dtype=name, c_dtype=name,
+                                     C=bits(C0h), accumulate=True), name)
+    np.testing.assert_allclose(acch.float().cpu().numpy(), ref_acch, rtol=1e-2, atol=1e-3)
+    # the same product on the LDS-staged 32x32 tile agrees within tolerance
+    staged = ops.matmul(ad, bd, config=(32, 32, 64, 1, 1, 2, 1))
+    np.testing.assert_allclose(staged.float().cpu().numpy(), c.float().cpu().numpy(),
+                               rtol=1e-2, atol=1e-3)
+
+
+def test_small_output_kernel_refusals(dev):
+    small = (16, 16, 32, 1, 1, 0, 1)
+    a = torch.randn(1024, 512, device=dev).half()
+    b = torch.randn(512, 1024, device=dev).half()
+    with pytest.raises(hxm.HxmError, match="no-kernel"):
+        ops.matmul(a, b, config=small)                   # 4096 tiles, K = 512
+    with pytest.raises(hxm.HxmError, match="no-kernel"):
+        ops.gemm_i8(torch.zeros(64, 64, dtype=torch.int8, device=dev),
+                    torch.zeros(64, 64, dtype=torch.int8, device=dev), config=small)

@@ -9,6 +9,7 @@ import pytest
 import torch
 
 import hxm
+import hxm.search  # noqa: F401  (hxm.search.gemm_configs below)
 from hxm import ops
 
 I8, F16, BF16, F32 = torch.int8, torch.float16, torch.bfloat16, torch.float32
@@ -89,3 +90,28 @@ def test_a_query_leaves_the_last_call_record_alone():
     before = ops.last_plan()
     plan(1024, 1024, 1024, I8, config=(2, 32, 128, 1, 1, 2, 1))
     assert ops.last_plan() == before
+
+
+def test_small_outputs_plan_the_direct_kernel():
+    """f16 / bf16 outputs of at most 512 16x16 tiles with 0 < K <= 256 default to
+    the direct-load small kernel (one 64-thread wave per 16x16 tile, no LDS);
+    larger outputs, larger K and int8 keep the LDS-staged tiles; a caller may
+    name the small config, and is refused where it does not apply."""
+    small = (16, 16, 32, 1, 1, 0, 1)
+    for dt in (F16, BF16):
+        p = plan(256, 256, 256, dt)                      # BASELINE config 1
+        assert p["config"] == small and p["source"] == "default"
+        assert p["threads"] == 64 and p["tiles"] == 256 and p["lds_bytes"] == 0
+        assert p["plan"] == "mfma-full" and p["workspace_bytes"] == 0
+    t = plan(300, 260, 200, F16)
+    assert t["config"] == small and t["plan"] == "mfma-tail" and t["tiles"] == 19 * 17
+    assert plan(256, 256, 512, F16)["config"] != small                # K above 256
+    assert plan(512, 512, 256, F16)["config"] != small                # 1024 tiles
+    assert plan(256, 256, 256, I8)["config"] != small
+    kn = plan(128, 128, 128, F16, b_layout="kn")
+    assert kn["config"] == small and kn["workspace_bytes"] == 128 * 128 * 2
+    named = plan(64, 64, 64, F16, config=small)
+    assert named["config"] == small and named["source"] == "caller"
+    refused = plan(1024, 1024, 1024, F16, config=small)
+    assert refused["plan"] == "refused" and refused["reason"] == "no-kernel"
+    assert plan(64, 64, 64, I8, config=small)["reason"] == "no-kernel"

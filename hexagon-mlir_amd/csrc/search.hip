@@ -228,6 +228,36 @@ __global__ void count_mismatch_kernel(const uint32_t* a, int64_t lda_words,
   if (bad) atomicAdd(out, bad);
 }
 
+// Outputs of two kernel families -- the direct-load small-output kernel
+// (v_mfma_f32_16x16x32, two accumulator chains) and the LDS-staged tiles
+// (v_mfma_f32_32x32x16, one chain per block) -- sum each dot product in a
+// different order, so their f16 / bf16 results agree within the float
+// tolerance, not bit for bit.  Counts the halves of a word that differ by
+// more than 1e-3 + 1e-2 |r| (NaN against anything but the same bits counts).
+__device__ __forceinline__ float half_bits_to_f32(uint32_t h, int bf16) {
+  return bf16 ? __uint_as_float(h << 16)
+              : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+__global__ void count_far_kernel(const uint32_t* a, int64_t lda_words, const uint32_t* b,
+                                 int64_t rows, int64_t row_words, int bf16, unsigned* out) {
+  const int64_t total = rows * row_words;
+  unsigned bad = 0;
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t r = i / row_words, c = i % row_words;
+    const uint32_t x = a[r * lda_words + c], y = b[i];
+    if (x == y) continue;
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t xh = (x >> (16 * h)) & 0xffffu, yh = (y >> (16 * h)) & 0xffffu;
+      if (xh == yh) continue;
+      const float xv = half_bits_to_f32(xh, bf16), yv = half_bits_to_f32(yh, bf16);
+      bad += !(fabsf(xv - yv) <= 1e-3f + 1e-2f * fabsf(yv));
+    }
+  }
+  if (bad) atomicAdd(out, bad);
+}
+
 __global__ void copy_rows_kernel(const uint32_t* a, int64_t lda_words,
                                  uint32_t* b, int64_t rows, int64_t row_words) {
   const int64_t total = rows * row_words;
@@ -379,8 +409,13 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
     if (measure(cands[i], M, N, K, &samples) != HXM_OK) continue;  // scores inf
     if (have_ref) {
       HXM_HIP_TRY(hipMemsetAsync(bad, 0, sizeof(unsigned), s));
-      count_mismatch_kernel<<<1024, 256, 0, s>>>(static_cast<const uint32_t*>(C),
-                                                 (ldc * out_eb) / 4, ref, M, row_words, bad);
+      if (is_small_gemm_config(cands[i]) != is_small_gemm_config(control))
+        count_far_kernel<<<1024, 256, 0, s>>>(static_cast<const uint32_t*>(C),
+                                              (ldc * out_eb) / 4, ref, M, row_words,
+                                              op == HXM_BF16, bad);
+      else
+        count_mismatch_kernel<<<1024, 256, 0, s>>>(static_cast<const uint32_t*>(C),
+                                                   (ldc * out_eb) / 4, ref, M, row_words, bad);
       unsigned h = 1;
       HXM_HIP_TRY(hipMemcpyAsync(&h, bad, sizeof(unsigned), hipMemcpyDeviceToHost, s));
       HXM_HIP_TRY(hipStreamSynchronize(s));
@@ -767,7 +802,10 @@ hxm_status hxm_tune_cache_load(const char* path, int32_t* loaded) {
     if (!parse_cache_entry(line, &ent)) continue;
     const int32_t op = ent.op;
     const hxm_gemm_config c = ent.cfg;
-    if (!config_compiled(op, c)) continue;
+    // The small-output kernel is a winner only for shapes it takes.
+    const bool small_ok = (op == HXM_F16 || op == HXM_BF16) && is_small_gemm_config(c) &&
+                          small_gemm_fits(ent.m, ent.n, ent.k, op);
+    if (!small_ok && !config_compiled(op, c)) continue;
     std::lock_guard<std::mutex> lk(g_tune_mu);
     g_tuned[TuneKey(op, ent.m, ent.n, ent.k)] = c;
     g_tuned_reps[TuneKey(op, ent.m, ent.n, ent.k)] = ent.reps;
@@ -830,8 +868,12 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
       }
     }
   }
+  // f16 / bf16 outputs that fit the direct-load small-output kernel run it
+  // when untuned: it is a candidate and the control.
+  const bool small = op != HXM_I8 && small_gemm_fits(M, N, K, op);
+  if (small) sp.cands.push_back(small_gemm_config());
   sort_configs(&sp.cands);
-  sp.control = default_config(M, N, op);
+  sp.control = small ? small_gemm_config() : default_config(M, N, op);
   sp.canary = hxm_gemm_config{32, 32, static_cast<int32_t>(op == HXM_I8 ? 128 : 64), 1, 1, 2, 1};
   sp.cm = std::min<int64_t>(32, M), sp.cn = std::min<int64_t>(32, N);
   const int64_t ck = std::min<int64_t>(K, 32);

@@ -570,7 +570,9 @@ int32_t hxm_judge_round(const hxm_arm_quantiles* arms, int32_t n, int32_t contro
  * reference's autotune sweep + hexagon_bench + judge_champion_round,
  * hmx_search.py:1109-1156,1370-1571).  op: HXM_I8 (int8 -> i32, B in
  * layout NK) or HXM_F16 / HXM_BF16 (-> C of the same dtype, B in layout
- * NK).  First the
+ * NK).  The control is what an untuned call runs: the default config, or
+ * for f16 / bf16 shapes the small-output kernel takes (see hxm_matmul)
+ * that kernel, also a candidate.  First the
  * cost model prices every legal compiled config on this device
  * (hxm_predict_tile_time) and the conservative prune (hxm_cost_prune, margin
  * 0.15, envelope 0.70 / 1.25, the control always kept) drops those whose
@@ -578,8 +580,10 @@ int32_t hxm_judge_round(const hxm_arm_quantiles* arms, int32_t n, int32_t contro
  * Every other config is launched `reps` times after one discarded warm call
  * (reps 0: calibrated per config, hxm_calibration_iters of the timed warm
  * call against a 10 ms budget, 5 to 1000 launches);
- * its output is checked bit-exact against the control config's (a config
- * that differs scores inf); the champion is the deterministic gated walk
+ * its output is checked against the control config's, bit-exact within a
+ * kernel family and within |c - r| <= 1e-3 + 1e-2 |r| between the
+ * small-output kernel and the LDS-staged tiles, whose dot products sum in
+ * different orders (a config that differs scores inf); the champion is the deterministic gated walk
  * from the control config with gate max(3*CV, 15%), preceded by the
  * 32x32x32 canary.  The winner is cached for (op, M, N, K) and used by
  * later calls with cfg == NULL.  report (JSON, may be NULL) receives the

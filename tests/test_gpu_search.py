@@ -39,6 +39,11 @@ def test_tune_gemm_picks_a_verified_winner(dev, dtype, M, N, K):
     assert ctl["split_k"] == 1
     if dtype == torch.int8:
         assert ctl["tiles"][:2] == [64, 64]
+    else:
+        # 256 16x16 output tiles, K = 256: the direct-load small-output kernel,
+        # against which the LDS-staged tiles are verified within tolerance
+        assert ctl["tiles"] == [16, 16, 32] and ctl["stages"] == 0
+        assert len(measured) > 1
     assert rep["start"] == "control" and rep["proof"] in (
         "proven", "control-held", "within-gate", "void")
     # later calls with no config use the cached winner and stay correct
@@ -52,6 +57,7 @@ def test_tune_gemm_picks_a_verified_winner(dev, dtype, M, N, K):
         ref = orc.to_f32(orc.matmul(bits(A), bits(B), ab_dtype=name, c_dtype=name, b_nk=True),
                          name)
         np.testing.assert_allclose(C, ref, rtol=1e-2, atol=1e-3)
+        assert ops.last_plan()["config"] == best.as_tuple()
 
 
 def test_tune_cache_save_load_round_trip(dev, tmp_path):

@@ -529,6 +529,39 @@ def test_small_output_kernel(dev, M, N, K, dt):
                                rtol=1e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_small_output_kernel_strided_operands(dev, dt):
+    """The small-output kernel on row views of wider buffers: lda > K, an
+    [N, K] image with ldb > K, and C inside a wider buffer whose columns past
+    N must stay untouched (f16 / bf16 and f32 outputs, with accumulate)."""
+    M, N, K, lda, ldb, ldc = 37, 45, 88, 104, 120, 64
+    print(f"small kernel strided {dt} M={M} N={N} K={K} lda={lda} ldb={ldb} ldc={ldc}",
+          flush=True)
+    name = "f16" if dt == torch.float16 else "bf16"
+    g = torch.Generator().manual_seed(77)
+    abuf = (torch.rand(M, lda, generator=g) * 2 - 1).to(dt)
+    bbuf = (torch.rand(N, ldb, generator=g) * 2 - 1).to(dt)
+    a, b_nk = abuf[:, :K], bbuf[:, :K]
+    ref = orc.to_f32(orc.matmul(bits(a.contiguous()), bits(b_nk.t().contiguous()),
+                                ab_dtype=name, c_dtype=name), name)
+    ad, bd = abuf.to(dev)[:, :K], bbuf.to(dev)[:, :K]
+    cbuf = torch.full((M, ldc), 7.0, dtype=dt, device=dev)
+    ops.matmul(ad, bd, out=cbuf[:, :N], b_layout="nk")
+    assert ops.last_plan()["config"] == (16, 16, 32, 1, 1, 0, 1)
+    got = cbuf.float().cpu().numpy()
+    np.testing.assert_allclose(got[:, :N], ref, rtol=1e-2, atol=1e-3)
+    assert (got[:, N:] == 7.0).all(), "wrote past N"
+    C0 = torch.randn(M, N, generator=g)
+    fbuf = torch.full((M, ldc), -3.0, dtype=torch.float32, device=dev)
+    fbuf[:, :N] = C0.to(dev)
+    ops.matmul(ad, bd, out=fbuf[:, :N], b_layout="nk", accumulate=True)
+    ref_acc = orc.matmul(bits(a.contiguous()), bits(b_nk.t().contiguous()), ab_dtype=name,
+                         c_dtype="f32", C=C0.numpy(), accumulate=True)
+    got = fbuf.cpu().numpy()
+    np.testing.assert_allclose(got[:, :N], ref_acc, rtol=1e-4, atol=1e-4)
+    assert (got[:, N:] == -3.0).all(), "wrote past N"
+
+
 def test_small_output_kernel_refusals(dev):
     small = (16, 16, 32, 1, 1, 0, 1)
     a = torch.randn(1024, 512, device=dev).half()

@@ -180,13 +180,14 @@ def run_int8(c, A, Bp, rs, cs, out_i32=False):
     C = torch.empty(M, N, dtype=torch.int32 if out_i32 else torch.float16, device=c.dev)
     a, b, r, s, o, st = (A.data_ptr(), Bp.data_ptr(), rs.data_ptr(), cs.data_ptr(),
                          C.data_ptr(), c.stream)
+    ldb = Bp.stride(0)                          # K: 4096-byte rows need no padding
     if out_i32:
         def step(_):
-            hxm.check(L.hxm_gemm_i8(a, K, b, K, hxm.B_NK, o, N, M, N, K, 0, None, st),
+            hxm.check(L.hxm_gemm_i8(a, K, b, ldb, hxm.B_NK, o, N, M, N, K, 0, None, st),
                       "hxm_gemm_i8")
     else:
         def step(_):
-            hxm.check(L.hxm_gemm_i8_dequant(a, K, b, K, hxm.B_NK, r, s, o, N, M, N, K, None,
+            hxm.check(L.hxm_gemm_i8_dequant(a, K, b, ldb, hxm.B_NK, r, s, o, N, M, N, K, None,
                                             st), "hxm_gemm_i8_dequant")
     t = c.time_ms(step, c.args.steps, c.args.warmup)
     c.last_step = step
@@ -523,9 +524,10 @@ def run_ragged(c):
     cs = torch.rand(N, device=c.dev) * 0.019 + 0.001
     C = torch.empty(M, 4096, dtype=torch.float16, device=c.dev)
     a, b, r, s, o, st = A.data_ptr(), Bp.data_ptr(), rs.data_ptr(), cs.data_ptr(), C.data_ptr(), c.stream
+    ldb = Bp.stride(0)                          # the image's rows are padded to 128 bytes
 
     def step(_):
-        hxm.check(L.hxm_gemm_i8_dequant(a, K, b, K, hxm.B_NK, r, s, o, 4096, M, N, K, None, st),
+        hxm.check(L.hxm_gemm_i8_dequant(a, K, b, ldb, hxm.B_NK, r, s, o, 4096, M, N, K, None, st),
                   "hxm_gemm_i8_dequant")
     t = c.time_ms(step, 200, 200)
     ops_per = 2.0 * M * N * K

@@ -213,6 +213,15 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(
 }
 
 namespace {
+// Row stride (elements) of the per-call [N, K] image of a [K, N] B: rows
+// start on 128-byte lines, so each row's K chunk of a stage is whole lines,
+// when 256 such rows still lie within 2 GiB (else rows of K elements).
+// Measured with an int8 [N, K] image at 4000^3 + dequant (one box): row
+// stride 4000 bytes 59.5 us, 4096 bytes 56.7 us.
+int64_t kn_image_ld(int64_t K, int64_t eb) {
+  const int64_t padded = ((K * eb + 127) / 128) * 128 / eb;
+  return tile_rows_addressable(padded * eb, K * eb) ? padded : K;
+}
 
 // kTileRowsMax (host_logic.h) bounds the tallest compiled tile.
 #define HXM_TILE_EDGE(BM, BN, BKB, ST, WM, WN) ((BM) > (BN) ? (BM) : (BN))
@@ -243,8 +252,8 @@ hxm_status validate_common(const char* op, const void* A, int64_t lda,
                 op);
   if (!extents_fit(M, N, K, eb))
     return fail(HXM_UNSUPPORTED_SHAPE, "tile-alignment: %s extent beyond 2^30", op);
-  // A [K,N] B is packed into an [N,K] image with rows of K elements.
-  const int64_t ldb_image = b_layout == HXM_B_NK ? ldb : K;
+  // A [K,N] B is packed into an [N,K] image (rows of kn_image_ld elements).
+  const int64_t ldb_image = b_layout == HXM_B_NK ? ldb : kn_image_ld(K, eb);
   if (K > 0 && (!tile_rows_addressable(lda * eb, K * eb) ||
                 !tile_rows_addressable(ldb_image * eb, K * eb)))
     return fail(HXM_UNSUPPORTED_SHAPE,
@@ -277,17 +286,19 @@ hxm_status resolve_b(const void* B, int64_t ldb, int32_t b_layout, int64_t K,
   hxm_status st = check_grid("weight pack", (N + 31) / 32, 256, (K + 31) / 32);
   if (st != HXM_OK) return st;
   void* ws = nullptr;
-  if ((st = stream_workspace(stream, static_cast<size_t>(N * K * eb), &ws)) != HXM_OK) return st;
+  const int64_t ldo = kn_image_ld(K, eb);
+  if ((st = stream_workspace(stream, static_cast<size_t>(N * ldo * eb), &ws)) != HXM_OK)
+    return st;
   const dim3 grid(static_cast<unsigned>((N + 31) / 32), static_cast<unsigned>((K + 31) / 32));
   if (eb == 1)
     transpose_kernel<uint8_t><<<grid, 256, 0, stream>>>(
-        static_cast<const uint8_t*>(B), ldb, static_cast<uint8_t*>(ws), K, K, N);
+        static_cast<const uint8_t*>(B), ldb, static_cast<uint8_t*>(ws), ldo, K, N);
   else
     transpose_kernel<uint16_t><<<grid, 256, 0, stream>>>(
-        static_cast<const uint16_t*>(B), ldb, static_cast<uint16_t*>(ws), K, K, N);
+        static_cast<const uint16_t*>(B), ldb, static_cast<uint16_t*>(ws), ldo, K, N);
   if ((st = check_launch("weight pack")) != HXM_OK) return st;
   *b_out = static_cast<const uint8_t*>(ws);
-  *ldb_bytes_out = K * eb;
+  *ldb_bytes_out = ldo * eb;
   return HXM_OK;
 }
 
@@ -371,7 +382,7 @@ hxm_status plan_gemm(int32_t op, int32_t table, int epi, int32_t b_layout, int64
       p->threads = 64;
       p->tiles = ((M + 15) / 16) * ((N + 15) / 16);
       p->lds_bytes = 0;
-      p->workspace_bytes = extra_ws + (b_layout == HXM_B_KN ? N * K * eb : 0);
+      p->workspace_bytes = extra_ws + (b_layout == HXM_B_KN ? N * kn_image_ld(K, eb) * eb : 0);
       p->k_slices = 1;
       const bool full = M % 16 == 0 && N % 16 == 0 && K % 32 == 0;
       p->plan = full ? HXM_PLAN_MFMA_FULL : HXM_PLAN_MFMA_TAIL;
@@ -398,7 +409,8 @@ hxm_status plan_gemm(int32_t op, int32_t table, int epi, int32_t b_layout, int64
     p->threads = e->threads;
     p->tiles = ((M + e->cfg.bm - 1) / e->cfg.bm) * ((N + e->cfg.bn - 1) / e->cfg.bn);
     p->lds_bytes = kernel_lds_bytes(*e, false, epi == kEpiDequant);
-    p->workspace_bytes = extra_ws + (b_layout == HXM_B_KN && K > 0 ? N * K * eb : 0);
+    p->workspace_bytes =
+        extra_ws + (b_layout == HXM_B_KN && K > 0 ? N * kn_image_ld(K, eb) * eb : 0);
     p->k_slices = k_slices(K * eb, e->cfg.bk, split);
     if (p->k_slices > 1) p->workspace_bytes += p->k_slices * M * N * 4;
     if (p->k_slices > 1 && p->k_slices * M * N * 4 > kSplitKPlaneBytesMax) {

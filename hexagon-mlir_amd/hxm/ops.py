@@ -218,11 +218,17 @@ def gemm_i8_dequant(A: torch.Tensor, B: torch.Tensor, row_scale: torch.Tensor,
 
 def prepack_weight(B: torch.Tensor, out: Optional[torch.Tensor] = None, *,
                    stream=None) -> torch.Tensor:
-    """[K, N] -> resident [N, K] image (hmx_weight_prepack's role)."""
+    """[K, N] -> resident [N, K] image (hmx_weight_prepack's role).  Without
+    ``out`` the image is a [N, K] view of rows padded to 128 bytes (its
+    stride(0) is the row stride to pass as ldb), so every row starts on a
+    cache line: int8 4000^3 + dequant ran 59.5 us on 4000-byte rows and
+    56.7 us on 4096-byte ones."""
     _mat(B, "B")
     K, N = B.shape
     if out is None:
-        out = torch.empty((N, K), dtype=B.dtype, device=B.device)
+        eb = B.element_size()
+        kp = -(-K * eb // 128) * 128 // eb
+        out = torch.empty((N, kp), dtype=B.dtype, device=B.device)[:, :K]
     _out(out, (N, K), (B.dtype,), B)
     st = lib.hxm_prepack_weight(B.data_ptr(), _ld(B), out.data_ptr(), _ld(out), K, N,
                                 _code(B), _stream(stream))

@@ -243,7 +243,10 @@ hxm_status hxm_gemm_i8_dequant(const int8_t* A, int64_t lda, const int8_t* B,
  * the device.  Transposes B [K,N] (ldb >= N) into the resident image
  * out [N,K] (ldo >= K), K contiguous -- the operand order every MFMA kernel
  * here reads.  dtype in {I8, F16, BF16}.  Run once per weight; matmuls then
- * take b_layout = HXM_B_NK. */
+ * take b_layout = HXM_B_NK.  An ldo whose rows start on 128-byte lines
+ * (ldo * elem a multiple of 128) streams fastest: int8 4000^3 + dequant
+ * 56.7 us against 59.5 us with ldo = K = 4000 (one box); the per-call pack
+ * of a [K,N] B uses such rows. */
 hxm_status hxm_prepack_weight(const void* B, int64_t ldb, void* out,
                               int64_t ldo, int64_t K, int64_t N, int32_t dtype,
                               void* stream);

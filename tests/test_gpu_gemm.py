@@ -571,3 +571,30 @@ def test_small_output_kernel_refusals(dev):
     with pytest.raises(hxm.HxmError, match="no-kernel"):
         ops.gemm_i8(torch.zeros(64, 64, dtype=torch.int8, device=dev),
                     torch.zeros(64, 64, dtype=torch.int8, device=dev), config=small)
+
+
+@pytest.mark.parametrize("dt,K,kp", [(torch.int8, 4000, 4096), (torch.int8, 128, 128),
+                                     (torch.float16, 200, 256), (torch.bfloat16, 64, 64)])
+def test_prepacked_rows_start_on_cache_lines(dev, dt, K, kp):
+    """prepack_weight pads the image's rows to 128 bytes (a [N, K] view of
+    [N, kp] storage) and the GEMMs read it through its row stride."""
+    print(f"prepack rows {dt} K={K}", flush=True)
+    N, M = 40, 24
+    g = torch.Generator().manual_seed(K)
+    if dt == torch.int8:
+        A = torch.randint(-127, 128, (M, K), generator=g, dtype=dt)
+        B = torch.randint(-127, 128, (K, N), generator=g, dtype=dt)
+    else:
+        A = (torch.rand(M, K, generator=g) * 2 - 1).to(dt)
+        B = (torch.rand(K, N, generator=g) * 2 - 1).to(dt)
+    img = ops.prepack_weight(B.to(dev))
+    assert img.shape == (N, K) and img.stride() == (kp, 1)
+    assert torch.equal(img.cpu(), B.t())
+    if dt == torch.int8:
+        C = ops.gemm_i8(A.to(dev), img, b_layout="nk").cpu().numpy()
+        assert np.array_equal(C, orc.gemm_i8(A.numpy(), B.numpy()))
+    else:
+        name = "f16" if dt == torch.float16 else "bf16"
+        ref = orc.to_f32(orc.matmul(bits(A), bits(B), ab_dtype=name, c_dtype=name), name)
+        got = ops.matmul(A.to(dev), img, b_layout="nk").float().cpu().numpy()
+        np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-3)

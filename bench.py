@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X hot path; prints ONE JSON line on stdout.
 
-Headline: int8 GEMM M=N=K=4096, A,B ~ U{-127..127},
+Headline (the benchmark's metric and configuration): int8 GEMM M=N=K=4096, A,B ~ U{-127..127},
 exact int32 accumulation, per-row x per-col fp32 scales dequantised to fp16
 (hxm_gemm_i8_dequant).  B is the resident [N,K] image made once before the
 timed region (the reference's weight-resident path).  One step = one GEMM
@@ -197,7 +197,7 @@ def run_int8(c, A, Bp, rs, cs, out_i32=False):
 
 
 def run_f16(c):
-    """BASELINE config 1, f16 256^3 (a handful of workgroups: launch-bound).
+    """The f16 256^3 matmul (a handful of workgroups: launch-bound).
     A Python loop of ctypes calls issues a launch every ~4 us, slower than
     the GPU runs them, so that loop times the host.  `us` comes from the
     launches replayed back to back from a HIP graph (50 per graph, captured
@@ -342,7 +342,7 @@ def run_rows(c):
 
 
 def run_ffn(c):
-    """the SwiGLU FFN block, tokens 2048, hidden 4096,
+    """The SwiGLU FFN block, tokens 2048, hidden 4096,
     intermediate 11008.  RMSNorm (eps 1e-6) -> fused gate/up W8A16 GEMM with
     SiLU * mul -> down W8A16 GEMM; fp16 activations N(0,1), int8 weights
     U{-127..127} with per-channel scales.  Each GEMM's tile is autotuned on
@@ -762,7 +762,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build is the single-GPU kernel set of the hot "
-              "path and has no multi-GPU path (DESIGN.md describes how it would shard).",
+              "path and has no multi-GPU path; the design notes describe how it would shard.",
               file=sys.stderr)
         return 2
     c = Ctx(args)

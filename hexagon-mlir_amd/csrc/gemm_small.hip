@@ -1,6 +1,6 @@
 // Small-output f16 / bf16 GEMM: the default kernel of hxm_matmul when the
 // output is at most kSmallTilesMax 16x16 tiles and K at most kSmallKMax
-// (fp16 256^3, is 256 such tiles).
+// (an fp16 256^3 matmul is 256 such tiles).
 //
 // Such a call is launch-bound: the LDS-staged kernel spends most of its
 // time on its staging round trips, barriers and the staged epilogue, not on

@@ -263,7 +263,7 @@ hxm_status hxm_prepack_weight(const void* B, int64_t ldb, void* out,
  *                 (backend/hmx_weight_prepack.py:171-183). */
 typedef enum hxm_w_layout { HXM_W_NK = 0, HXM_W_PACKED = 1 } hxm_w_layout;
 
-/* W8A16 weight-resident skinny GEMM / GEMV (the
+/* W8A16 weight-resident skinny GEMM / GEMV (M in {1, 4, 16}; the
  * reference's int8 matmul on the HVX path, ScheduleMatmulForHVXPass.cpp:44-80):
  *   y[m,n] = rne_f16( (sum_k f32(x[m,k]) * f32(W[n,k])) * f32(w_scale[n]) )
  * x fp16 [M,K] (ldx >= K); W int8 in layout w_layout; w_scale fp16 [N];
@@ -315,7 +315,7 @@ hxm_status hxm_resident_weight(const void* src, int64_t ld, int64_t rows,
                                int32_t kind, const void** image,
                                int32_t* image_dtype, void* stream);
 
-/* ---- SwiGLU FFN block (BASELINE config 5: RMSNorm -> int8-weight gate/up
+/* ---- SwiGLU FFN block (RMSNorm -> int8-weight gate/up
  *      GEMMs -> SiLU*mul -> down GEMM).  The reference composes it from the
  *      linalg ops its pipeline lowers: linalg.matmul (MatmulToHmxPass.cpp
  *      :101-121 admission; int8 operands take the HVX path,

@@ -17,7 +17,7 @@
  *                      wide accumulate (fp32 here), one rounding to C.
  *   hxo_gemv_w8a16     int8-weight matmul, fp32 accumulate, per-channel scale.
  *   hxo_gemm_w8a16     the same with fp32 scales (the FFN projections of the
- *                      BASELINE SwiGLU block; int8 operands of linalg.matmul
+ *                      SwiGLU FFN block; int8 operands of linalg.matmul
  *                      take the HVX path, ScheduleMatmulForHVXPass.cpp:44-80).
  *   hxo_gemm_w8a16_residual  the same plus a residual (x + FFN(x)):
  *                      f16(f32(acc * scale) + f32(r)).

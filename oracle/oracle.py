@@ -290,7 +290,7 @@ def swiglu_gateup(x_bits: np.ndarray, Wg: np.ndarray, Wu: np.ndarray, sg: np.nda
 
 def swiglu_ffn(x_bits: np.ndarray, gamma_bits: np.ndarray, Wg, Wu, sg, su, Wd, sd,
                eps: float = 1e-6, threads: int = 0, residual: bool = False) -> np.ndarray:
-    """The BASELINE SwiGLU FFN block with fp16 tensors between the stages:
+    """The SwiGLU FFN block with fp16 tensors between the stages:
     xn = rmsnorm(x) (f16), h = swiglu_gateup(xn) (f16), y = gemm_w8a16(h, Wd);
     with residual, y = gemm_w8a16_residual(h, Wd, r=x) = x + FFN(x)."""
     xn = rmsnorm_rows(x_bits, gamma_bits, eps, "f16")

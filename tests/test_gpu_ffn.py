@@ -1,10 +1,10 @@
-"""GPU parity of the SwiGLU FFN block against the CPU
+"""GPU parity of the SwiGLU FFN block (tokens 2048, hidden 4096, intermediate 11008) against the CPU
 oracle: the large-M W8A16 GEMM, the gate/up image, the fused gate/up GEMM
 with SiLU * mul, and the whole block RMSNorm -> gate/up -> down.
 
 fp16 outputs are held to rtol 1e-2 / atol 1e-3 (fp32 accumulation in MFMA
 order vs the oracle's increasing-k fp32 sums); a small-integer case makes
-every sum exact, so the W8A16 GEMM must match bit for bit.  At the BASELINE
+every sum exact, so the W8A16 GEMM must match bit for bit.  At the benchmark
 size (tokens 2048, hidden 4096, intermediate 11008) the oracle runs on a row
 sample of the same inputs."""
 import numpy as np

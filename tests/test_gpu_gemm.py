@@ -140,7 +140,7 @@ def test_gemm_i8_accumulate_and_strides(dev):
 
 
 def test_gemm_i8_4096_cube(dev):
-    """4096^3, int32 exact and the dequant epilogue."""
+    """The int8 4096^3 benchmark shape: int32 exact and the dequant epilogue."""
     n = 4096
     A = rand_i8((n, n), 11)
     B = rand_i8((n, n), 12)       # as [N, K]
@@ -189,7 +189,7 @@ def test_prepack_is_the_transpose(dev):
                                    (256, 64, 2048), (128, 128, 128), (77, 150, 200)])
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
 def test_matmul_within_tolerance(dev, M, N, K, dt):
-    """BASELINE config 1 (256^3) and the reference's S1/S2/S3 shapes
+    """The fp16 256^3 benchmark shape and the reference's S1/S2/S3 shapes
     (ROADMAP.md:98-100), U[-1,1] inputs."""
     print(f"matmul {dt} M={M} N={N} K={K}", flush=True)
     g = torch.Generator().manual_seed(M + N + K)
@@ -492,7 +492,7 @@ def test_matmul_through_memref_descriptors(dev):
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
 def test_small_output_kernel(dev, M, N, K, dt):
     """The direct-load small-output kernel, the default for f16 / bf16 outputs
-    of at most 512 16x16 tiles with K <= 256 (BASELINE config 1 is 256^3):
+    of at most 512 16x16 tiles with K <= 256 (256^3 is 256 tiles):
     the plan names it, and its f16 / bf16 / f32 outputs, with and without
     accumulate, from [K, N] and [N, K] B, are within tolerance of the oracle.
     K = 8, 40, 72, 200 end inside a 32-wide k-step."""

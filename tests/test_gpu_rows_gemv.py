@@ -156,7 +156,7 @@ def test_grid_beyond_the_launch_limit_is_refused(dev):
 @pytest.mark.parametrize("M", [1, 4, 16])
 @pytest.mark.parametrize("packed", [True, False])
 def test_gemv_baseline_shape(dev, M, packed):
-    """N=11008, K=4096, M in {1,4,16}; resident image and
+    """The GEMV benchmark shapes: N=11008, K=4096, M in {1,4,16}; resident image and
     plain [N, K] weights."""
     print(f"gemv M={M} packed={packed}", flush=True)
     N, K = 11008, 4096

@@ -99,7 +99,7 @@ def test_small_outputs_plan_the_direct_kernel():
     name the small config, and is refused where it does not apply."""
     small = (16, 16, 32, 1, 1, 0, 1)
     for dt in (F16, BF16):
-        p = plan(256, 256, 256, dt)                      # BASELINE config 1
+        p = plan(256, 256, 256, dt)                      # the fp16 256^3 benchmark shape
         assert p["config"] == small and p["source"] == "default"
         assert p["threads"] == 64 and p["tiles"] == 256 and p["lds_bytes"] == 0
         assert p["plan"] == "mfma-full" and p["workspace_bytes"] == 0

@@ -159,10 +159,9 @@ def test_random_rows_with_value_patterns(dev):
                          name)
         y = ops.rms_norm(x.to(dev), (cols,), weight=w.to(dev), eps=1e-6)
         np.testing.assert_allclose(y.float().cpu().numpy(), ref, **tol, err_msg=case + " rms")
-        if name != "bf16":
-            b = (0.1 * torch.randn(cols, generator=g)).to(TDT[name])
-            ry, _, _ = orc.layernorm_rows(host_bits(x, name), host_bits(w, name),
-                                          host_bits(b, name), 1e-5, name)
-            y = ops.layer_norm(x.to(dev), (cols,), w.to(dev), b.to(dev), eps=1e-5)
-            np.testing.assert_allclose(y.float().cpu().numpy(), orc.to_f32(ry, name), **tol,
-                                       err_msg=case + " layernorm")
+        b = (0.1 * torch.randn(cols, generator=g)).to(TDT[name])
+        ry, _, _ = orc.layernorm_rows(host_bits(x, name), host_bits(w, name),
+                                      host_bits(b, name), 1e-5, name)
+        y = ops.layer_norm(x.to(dev), (cols,), w.to(dev), b.to(dev), eps=1e-5)
+        np.testing.assert_allclose(y.float().cpu().numpy(), orc.to_f32(ry, name), **tol,
+                                   err_msg=case + " layernorm")

@@ -59,7 +59,7 @@ def test_rmsnorm(dev, rows, cols, name):
 
 @pytest.mark.parametrize("rows,cols", [(27, 8192), (8192, 4096), (33, 300), (2, 17000),
                                        (33, 4096), (5, 2048), (1, 4096)])
-@pytest.mark.parametrize("name", ["f32", "f16"])
+@pytest.mark.parametrize("name", ["f32", "f16", "bf16"])
 def test_layernorm(dev, rows, cols, name):
     print(f"layernorm {name} {rows}x{cols}", flush=True)
     g = torch.Generator().manual_seed(rows + cols)

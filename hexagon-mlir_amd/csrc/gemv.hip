@@ -123,6 +123,20 @@ __device__ __forceinline__ void gemv_finish(const GemvArgs& g, const v4f32 (*par
   }
 }
 
+// K == 0: every dot product is the empty sum, so y[m, n] = f16(0.0f *
+// scale[n]) (+0, -0 for a negative scale, NaN for an infinite or NaN one),
+// the same product the GEMV kernels round.  A kernel of its own keeps the
+// K loop's structure out of this case: the M <= 4 kernels load the scales
+// inside their first K chunk, which K == 0 does not have.
+__global__ __launch_bounds__(256) void gemv_empty_k_kernel(GemvArgs g) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= static_cast<int64_t>(g.M) * g.N) return;
+  const int m = static_cast<int>(t / g.N), n = static_cast<int>(t % g.N);
+  float p = 0.0f * static_cast<float>(g.scale[n]);
+  asm volatile("" : "+v"(p));
+  g.y[static_cast<int64_t>(m) * g.ldy + n] = static_cast<_Float16>(p);
+}
+
 // One workgroup = CB groups of 16 output channels x all of K; its KW waves
 // split each K chunk of KW*SPW slabs, SPW contiguous slabs per wave, and
 // every wave applies the same x fragment to the CB channel groups (more
@@ -499,6 +513,12 @@ hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W, int64_t l
   // x rows staged per workgroup: a single small M tile needs less LDS, which
   // keeps more workgroups resident per CU.
   hipStream_t s = as_stream(stream);
+  if (K == 0) {
+    const int64_t blocks = (M * N + 255) / 256;
+    if ((st = check_grid("gemv_w8a16", blocks, 256)) != HXM_OK) return st;
+    gemv_empty_k_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(g);
+    return check_launch("gemv_w8a16");
+  }
   const bool pk = w_layout == HXM_W_PACKED;
   // Channel groups per workgroup at M > 4: three share each staged x chunk,
   // which pays while a workgroup per 16 channels would more than fill the

@@ -172,6 +172,27 @@ def test_gemv_baseline_shape(dev, M, packed):
     np.testing.assert_allclose(y.float().numpy(), ref, rtol=1e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("packed", [True, False])
+def test_gemv_empty_k(dev, M, packed):
+    """K == 0: every dot product is the empty sum, so y = f16(0.0 * scale)
+    bit for bit (+0, and -0 where the scale is negative), whatever y held
+    before; x and W may be null.  Called through the C ABI, since a torch
+    tensor with no columns has no 8-aligned row stride."""
+    import hxm
+    N = 40
+    sc = torch.linspace(-1.5, 1.5, N).half()
+    sc[7] = -0.0
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    st = hxm.lib.hxm_gemv_w8a16(None, 8, None, 16, hxm.W_PACKED if packed else hxm.W_NK,
+                                sc.to(dev).data_ptr(), y.data_ptr(), N, M, N, 0,
+                                torch.cuda.current_stream().cuda_stream)
+    hxm.check(st, "hxm_gemv_w8a16")
+    want = (torch.zeros(M, N) * sc.float()).half()
+    assert np.array_equal(host_bits(y.cpu(), "f16"), host_bits(want, "f16"))
+    assert (host_bits(want, "f16")[:, :20] == 0x8000).all()   # the negative scales give -0
+
+
 @pytest.mark.parametrize("M,N,K", [(3, 100, 272), (33, 64, 512), (1, 17, 16), (16, 48, 256),
                                    (5, 40, 2064), (20, 31, 4160),
                                    # one GPU's share of an 8-way column split of config 3

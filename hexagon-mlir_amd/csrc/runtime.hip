@@ -90,14 +90,20 @@ hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out, int sl
   Workspace& w = g_ws[key];
   if (w.bytes < bytes) {
     // Growing needs hipMalloc (and a stream synchronisation to retire the old
-    // buffer), neither of which a stream under graph capture allows.
+    // buffer), neither of which a stream under graph capture allows.  A query
+    // that fails counts as a capture: the null stream, for one, reports an
+    // implicit-capture error while another stream captures in global mode,
+    // and a synchronisation or hipMalloc then would invalidate that capture.
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+    const hipError_t qe = hipStreamIsCapturing(stream, &cap);
+    if (qe != hipSuccess) (void)hipGetLastError();  // clear the sticky query error
+    if (qe != hipSuccess || cap != hipStreamCaptureStatusNone)
       return fail(HXM_UNSUPPORTED_SHAPE,
-                  "workspace-budget: the stream is capturing a graph and its workspace must "
-                  "grow from %zu to %zu bytes; make one call of this shape on the stream "
-                  "before capturing (the workspace is kept), or use hxm_gemm_i8_noalloc",
-                  w.bytes, bytes);
+                  "workspace-budget: the stream is capturing a graph (or its capture state "
+                  "cannot be read: %s) and its workspace must grow from %zu to %zu bytes; "
+                  "make one call of this shape on the stream before capturing (the workspace "
+                  "is kept), or use hxm_gemm_i8_noalloc",
+                  qe == hipSuccess ? "capturing" : hipGetErrorString(qe), w.bytes, bytes);
     if (w.ptr) {
       // The old buffer may still be read by work queued on this stream.
       HXM_HIP_TRY(hipStreamSynchronize(stream));

@@ -384,7 +384,10 @@ hxm_status plan_gemm(int32_t op, int32_t table, int epi, int32_t b_layout, int64
       p->lds_bytes = 0;
       p->workspace_bytes = extra_ws + (b_layout == HXM_B_KN ? N * kn_image_ld(K, eb) * eb : 0);
       p->k_slices = 1;
-      const bool full = M % 16 == 0 && N % 16 == 0 && K % 32 == 0;
+      // The plan's classes use the 32-wide MFMA edge for every kernel (the
+      // reference's queryContraction tile edge), also where this kernel's
+      // own tiles are 16 wide.
+      const bool full = M % 32 == 0 && N % 32 == 0 && K % 32 == 0;
       p->plan = full ? HXM_PLAN_MFMA_FULL : HXM_PLAN_MFMA_TAIL;
       p->reason = full ? HXM_REASON_SELECTED_ALIGNED : HXM_REASON_SELECTED_TAIL;
     }
@@ -452,6 +455,9 @@ static hxm_status run_gemm_with(int32_t op, int32_t ab_dtype, int epi, const voi
   hxm_plan plan;
   hxm_status st = plan_gemm(op, ab_dtype, epi, b_layout, M, N, K, cfg, extra_ws, &plan, &e);
   if (st != HXM_OK) return st;
+  // Caller-provided planes (the allocation-free entry's static array): the
+  // call takes no library workspace, and its plan record says so.
+  if (planes) g_last_plan.workspace_bytes = plan.workspace_bytes = 0;
   const int split = plan.config.split_k;
   if ((st = require_device(nullptr)) != HXM_OK) return st;
   if (M == 0 || N == 0) return ok();

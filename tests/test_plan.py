@@ -63,6 +63,18 @@ def test_refusal_order_dtype_then_arguments_then_shape():
     assert plan(8, 8, 4, F32)["plan"] == "mfma-tail"             # f32: K padded in the pack
 
 
+def test_plan_class_uses_the_32_wide_edge_for_every_kernel():
+    """The plan classes follow the 32-wide MFMA edge (the reference's
+    queryContraction tileEdge) also where the direct small-output kernel,
+    whose own tiles are 16 wide, takes the shape."""
+    p = plan(48, 48, 64, F16)
+    assert p["config"][:3] == (16, 16, 32)          # the small-output kernel
+    assert p["plan"] == "mfma-tail" and p["reason"] == "selected-tail"
+    q = plan(64, 96, 64, F16)
+    assert q["config"][:3] == (16, 16, 32)
+    assert q["plan"] == "mfma-full" and q["reason"] == "selected-aligned"
+
+
 def test_split_k_limits():
     base = hxm.search.gemm_configs(hxm.I8)[0].as_tuple()[:6]
     ok = plan(512, 512, 16384, I8, config=base + (16,))

@@ -257,9 +257,11 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
     fresh(v);
     // exp(x - m) = 2^(x*log2(e) - m*log2(e)): one (mixed-precision) fma per
     // element feeds the hardware exp2, once per element.  Each numerator is
-    // rounded to the storage type in place of its input (as the reference's
-    // kernel rounds exp(z) to x's type before the division), so the row
-    // stays in the registers it arrived in; the sum takes the fp32 values.
+    // rounded to the storage type in place of its input, and the fp32 sum
+    // adds those rounded numerators: the reference's kernel computes
+    // num = exp(z).to(x.dtype), denom = sum(num) in fp32, y = num / denom
+    // (test/python/triton/test_softmax.py:64-66).  The row stays in the
+    // registers it arrived in.
     // The output pass is one mixed-precision fma per element, x * inv +
     // (-0), with `nzero` hidden from the optimizer so it stays an fma (it
     // rounds exactly like the product).  Padded -inf columns give 0.
@@ -276,8 +278,8 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
 #pragma unroll
       for (int j = 0; j < N; ++j) {
         const float ej = __builtin_amdgcn_exp2f(fmaf(tof(v[i][j]), kLog2e, mb));
-        s += ej;
         e[j] = fromf<T>(ej);
+        s += tof(e[j]);
       }
       // The numerators exist in the storage type here, one vector at a
       // time: otherwise the compiler sinks the roundings into the output
@@ -403,7 +405,7 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
 }
 
 // Streaming kernel for rows longer than the register budget: the row is
-// re-read per pass (softmax keeps an online max/sum so it needs 2 passes,
+// re-read per pass (softmax 3: max, sum of rounded numerators, output;
 // RMSNorm 2, LayerNorm 3).
 template <typename T, int OP, bool ALIGNED>
 __global__ __launch_bounds__(256) void row_kernel_stream(RowArgs a) {
@@ -421,24 +423,25 @@ __global__ __launch_bounds__(256) void row_kernel_stream(RowArgs a) {
   float scale = 1.0f, shift = 0.0f;  // y = (x - shift) * scale [* g + b]
   float m = 0.0f;
   if constexpr (OP == kSoftmax) {
-    float lm = -__builtin_huge_valf(), ls = 0.0f;
+    // The row max, then the fp32 sum of the numerators rounded to the
+    // storage type (the reference's arithmetic, as in row_kernel): an online
+    // max/sum would rescale sums of unrounded numerators instead.
+    float lm = -__builtin_huge_valf();
     for (int64_t c0 = lane * N; c0 < cols; c0 += step) {
       float f[N];
       load_vec<T, ALIGNED>(xr, c0, cols, -__builtin_huge_valf(), f);
-      float cm = lm;
 #pragma unroll
-      for (int j = 0; j < N; ++j) cm = fmaxf(cm, f[j]);
-      if (cm > lm) {
-        ls = (lm == -__builtin_huge_valf()) ? 0.0f : ls * exp_f32(lm - cm);
-        lm = cm;
-      }
-      if (lm != -__builtin_huge_valf())
-#pragma unroll
-        for (int j = 0; j < N; ++j) ls += exp_f32(f[j] - lm);
+      for (int j = 0; j < N; ++j) lm = fmaxf(lm, f[j]);
     }
     m = wave_reduce(lm, OpMax());
-    float part = (lm == -__builtin_huge_valf()) ? 0.0f : ls * exp_f32(lm - m);
-    const float s = wave_reduce(part, OpSum());
+    float ls = 0.0f;
+    for (int64_t c0 = lane * N; c0 < cols; c0 += step) {
+      float f[N];
+      load_vec<T, ALIGNED>(xr, c0, cols, -__builtin_huge_valf(), f);
+#pragma unroll
+      for (int j = 0; j < N; ++j) ls += tof(fromf<T>(exp_f32(f[j] - m)));
+    }
+    const float s = wave_reduce(ls, OpSum());
     scale = 1.0f / s;
   } else if constexpr (OP == kRmsNorm) {
     float ss = 0.0f;
@@ -483,7 +486,7 @@ __global__ __launch_bounds__(256) void row_kernel_stream(RowArgs a) {
     load_vec<T, ALIGNED>(xr, c0, cols, 0.0f, f);
     if constexpr (OP == kSoftmax) {
 #pragma unroll
-      for (int j = 0; j < N; ++j) f[j] = exp_f32(f[j] - m) * scale;
+      for (int j = 0; j < N; ++j) f[j] = tof(fromf<T>(exp_f32(f[j] - m))) * scale;
     } else if constexpr (OP == kRmsNorm) {
       float gv[N];
       if (g) load_vec<T, ALIGNED>(g, c0, cols, 0.0f, gv);

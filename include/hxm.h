@@ -215,10 +215,15 @@ hxm_status hxm_gemm_i8(const int8_t* A, int64_t lda, const int8_t* B,
  * (b_layout HXM_B_NK; the per-call pack of a [K,N] B would need a
  * workspace).  A K split (cfg->split_k, or a tuned winner that has one)
  * keeps its S*M*N int32 partial planes in a library-static device array of
- * HXM_NOALLOC_SCRATCH_BYTES per device, which each device holds until the
- * process ends; a split needing more is refused ("workspace-budget").
- * Every call on a device shares that array: calls that overlap on one device
- * (on different streams) race; calls on one stream are ordered. */
+ * HXM_NOALLOC_SCRATCH_BYTES per device; a split needing more is refused
+ * ("workspace-budget").  The array is part of the library's code object: every
+ * process that loads libhxm.so holds those 64 MiB on each device it uses,
+ * until the process ends, whether or not it ever calls this entry.  Its plan
+ * record (hxm_last_plan) reports no library workspace.  Every call on a
+ * device shares that array: calls that overlap on one device (on different
+ * streams) race, and nothing detects it; calls on one stream are ordered.
+ * The call may be captured in a HIP graph (it allocates, frees and
+ * synchronises nothing, and records no memset). */
 #define HXM_NOALLOC_SCRATCH_BYTES (64ll << 20)
 hxm_status hxm_gemm_i8_noalloc(const int8_t* A, int64_t lda, const int8_t* B_nk,
                                int64_t ldb, int32_t* C, int64_t ldc, int64_t M,

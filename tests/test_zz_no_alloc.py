@@ -1,7 +1,8 @@
 """The allocation-free int8 GEMM (hxm_gemm_i8_noalloc) against hxm_gemm_i8,
 both called through the C ABI: bit-identical int32 results on two calls in a
 row (the second smaller, so the shared static scratch holds the first call's
-planes), with and without a K split, plus the host-side refusals."""
+planes), with and without a K split, captured in a HIP graph and replayed,
+plus the host-side refusals."""
 import ctypes
 
 import numpy as np
@@ -89,3 +90,51 @@ def test_noalloc_refuses_on_the_host(dev):
     assert st == hxm._lib.HXM_UNSUPPORTED_SHAPE and "workspace-budget" in hxm.last_error()
     torch.cuda.synchronize()
     assert int(C.abs().sum()) == 0
+
+
+def test_noalloc_plan_reports_no_workspace(dev):
+    M, N, K = 512, 512, 8192
+    A, B = _i8((M, K), 5).to(dev), _i8((N, K), 6).to(dev)
+    C = torch.empty(M, N, dtype=torch.int32, device=dev)
+    hxm.check(_call(lib.hxm_gemm_i8_noalloc, A, B, C, M, N, K, False, _cfg(8)),
+              "hxm_gemm_i8_noalloc")
+    import hxm.ops as ops
+    p = ops.last_plan()
+    assert p["k_slices"] == 8 and p["workspace_bytes"] == 0
+    hxm.check(_gemm_i8(A, B, C, M, N, K, False, _cfg(8)), "hxm_gemm_i8")
+    assert ops.last_plan()["workspace_bytes"] == 8 * M * N * 4   # the library's own planes
+    torch.cuda.synchronize()
+
+
+def test_noalloc_split_captured_in_a_graph(dev):
+    """With every library workspace released, the K-split call is captured on
+    a fresh stream (it must not allocate there) and replayed three times, with
+    eager work (inputs touched, output poisoned) and a synchronisation between
+    replays; each replay equals the eager result bit for bit."""
+    M, N, K = 512, 512, 8192
+    A, B = _i8((M, K), 7), _i8((N, K), 8)
+    Ad, Bd = A.to(dev), B.to(dev)
+    cfg = _cfg(8)
+    want = torch.empty(M, N, dtype=torch.int32, device=dev)
+    got = torch.empty(M, N, dtype=torch.int32, device=dev)
+    hxm.check(_gemm_i8(Ad, Bd, want, M, N, K, False, cfg), "hxm_gemm_i8")
+    hxm.check(_call(lib.hxm_gemm_i8_noalloc, Ad, Bd, got, M, N, K, False, cfg),
+              "hxm_gemm_i8_noalloc")            # eager, on this device first
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    hxm.check(lib.hxm_release_cache(), "hxm_release_cache")
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    print("capturing hxm_gemm_i8_noalloc split=8", flush=True)
+    with torch.cuda.graph(graph, stream=s):
+        st = _call(lib.hxm_gemm_i8_noalloc, Ad, Bd, got, M, N, K, False, cfg)
+    assert st == 0, hxm.last_error()
+    keep = Ad.clone()
+    for rep in range(3):
+        got.fill_(-7)
+        Ad.mul_(2).copy_(keep)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {rep}"
+    del graph

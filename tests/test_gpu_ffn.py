@@ -6,7 +6,8 @@ fp16 outputs are held to rtol 1e-2 / atol 1e-3 (fp32 accumulation in MFMA
 order vs the oracle's increasing-k fp32 sums); a small-integer case makes
 every sum exact, so the W8A16 GEMM must match bit for bit.  At the benchmark
 size (tokens 2048, hidden 4096, intermediate 11008) the oracle runs on a row
-sample of the same inputs."""
+sample of the same inputs.  The block is checked stage by stage (each stage
+fed the GPU's own input to it) and end to end, all at that tolerance."""
 import numpy as np
 import pytest
 import torch
@@ -230,63 +231,107 @@ def ffn_operands(T, H, I, seed):
     return x, gamma, Wg, Wu, Wd, sg, su, sd
 
 
-def run_ffn(dev, x, gamma, Wg, Wu, Wd, sg, su, sd, residual=False):
+def run_ffn_stages(dev, x, gamma, Wg, Wu, Wd, sg, su, sd, residual=False):
+    """The block on the GPU stage by stage -- RMSNorm, fused gate/up with
+    SiLU * mul, down (with the residual in its epilogue) -- and, separately,
+    through swiglu_ffn, which must launch exactly that composition (same
+    bits).  Returns the f16 tensors xn, h, y on the host."""
+    T, H = x.shape
     I = Wg.shape[0]
     Wgu, sgu = ops.swiglu_pack(Wg.to(dev), Wu.to(dev), sg.to(dev), su.to(dev))
-    return ops.swiglu_ffn(x.to(dev), gamma.to(dev), Wgu, sgu, Wd.to(dev), sd.to(dev), I,
-                          residual=residual)
+    xd, gd, Wdd, sdd = x.to(dev), gamma.to(dev), Wd.to(dev), sd.to(dev)
+    xn = ops.rms_norm(xd, (H,), gd, eps=1e-6)
+    h = ops.gemm_w8a16_swiglu(xn, Wgu, sgu, I)
+    y = ops.gemm_w8a16(h, Wdd, sdd, residual=xd if residual else None)
+    y_block = ops.swiglu_ffn(xd, gd, Wgu, sgu, Wdd, sdd, I, residual=residual)
+    assert torch.equal(y, y_block), "swiglu_ffn differs from its own stages"
+    return xn.cpu(), h.cpu(), y.cpu()
+
+
+def check_ffn_stages(ops_, xn, h, y, rows, residual=False):
+    """Each stage against the oracle fed the GPU's own input to that stage,
+    at rtol 1e-2 / atol 1e-3:
+      1. xn = RMSNorm(x) against orc.rmsnorm_rows(x);
+      2. h against orc.swiglu_gateup(GPU xn);
+      3. y against the oracle's down projection of the GPU's h (with x as the
+         residual when the block adds it);
+    then the whole block against the oracle's own chain (x -> xn_o -> h_o ->
+    y_o) at the same tolerance.  Stage by stage, a difference cannot hide
+    behind a looser end-to-end bound: a one-ulp difference of an f16 h
+    element between the two chains moves y by up to |Wd| * sd * ulp(h),
+    which rtol does not absorb where y is near 0, and the stage checks show
+    which stage such a difference would come from."""
+    x, gamma, Wg, Wu, Wd, sg, su, sd = ops_
+    xb = bits(x)[rows]
+    xn_b, h_b, y_b = bits(xn)[rows], bits(h)[rows], bits(y)[rows]
+    xn_ref = orc.rmsnorm_rows(xb, bits(gamma), 1e-6, "f16")
+    np.testing.assert_allclose(f32(xn_b), f32(xn_ref), **TOL, err_msg="RMSNorm stage")
+    h_ref = orc.swiglu_gateup(xn_b, Wg.numpy(), Wu.numpy(), sg.numpy(), su.numpy())
+    np.testing.assert_allclose(f32(h_b), f32(h_ref), **TOL, err_msg="gate/up stage")
+    if residual:
+        y_ref = orc.gemm_w8a16_residual(h_b, Wd.numpy(), sd.numpy(), xb)
+    else:
+        y_ref = orc.gemm_w8a16(h_b, Wd.numpy(), sd.numpy())
+    np.testing.assert_allclose(f32(y_b), f32(y_ref), **TOL, err_msg="down stage")
+    y_o = orc.swiglu_ffn(xb, bits(gamma), Wg.numpy(), Wu.numpy(), sg.numpy(), su.numpy(),
+                         Wd.numpy(), sd.numpy(), residual=residual)
+    np.testing.assert_allclose(f32(y_b), f32(y_o), **TOL, err_msg="block end to end")
 
 
 def test_swiglu_ffn_block(dev):
     T, H, I = 256, 512, 704
     ops_ = ffn_operands(T, H, I, 21)
-    y = run_ffn(dev, *ops_)
-    x, gamma, Wg, Wu, Wd, sg, su, sd = ops_
-    ref = orc.swiglu_ffn(bits(x), bits(gamma), Wg.numpy(), Wu.numpy(), sg.numpy(),
-                         su.numpy(), Wd.numpy(), sd.numpy())
-    np.testing.assert_allclose(y.float().cpu().numpy(), f32(ref), rtol=1e-2, atol=2e-3)
+    xn, h, y = run_ffn_stages(dev, *ops_)
+    check_ffn_stages(ops_, xn, h, y, np.arange(T))
 
 
 def test_swiglu_ffn_block_with_residual(dev):
     """x + FFN(x): the residual is added in the down GEMM's epilogue."""
     T, H, I = 256, 512, 704
     ops_ = ffn_operands(T, H, I, 22)
-    y = run_ffn(dev, *ops_, residual=True)
-    x, gamma, Wg, Wu, Wd, sg, su, sd = ops_
-    ref = orc.swiglu_ffn(bits(x), bits(gamma), Wg.numpy(), Wu.numpy(), sg.numpy(),
-                         su.numpy(), Wd.numpy(), sd.numpy(), residual=True)
-    np.testing.assert_allclose(y.float().cpu().numpy(), f32(ref), rtol=1e-2, atol=2e-3)
+    xn, h, y = run_ffn_stages(dev, *ops_, residual=True)
+    check_ffn_stages(ops_, xn, h, y, np.arange(T), residual=True)
 
 
-def test_swiglu_ffn_baseline_size_row_sample(dev):
-    """tokens 2048, hidden 4096, intermediate 11008: the whole block on the GPU,
-    the oracle on 16 sampled token rows (rows are independent in every stage)."""
+SAMPLE_ROWS = np.array([0, 1, 255, 256, 511, 777, 1023, 1024, 1290, 1535, 1536, 1800, 2000,
+                        2045, 2046, 2047])
+
+
+def test_swiglu_ffn_baseline_size_stages(dev):
+    """tokens 2048, hidden 4096, intermediate 11008: the whole block on the
+    GPU, every stage checked against the oracle on 16 sampled token rows
+    (rows are independent in every stage) at rtol 1e-2 / atol 1e-3, then the
+    block end to end at the same tolerance."""
     T, H, I = 2048, 4096, 11008
-    x, gamma, Wg, Wu, Wd, sg, su, sd = ffn_operands(T, H, I, 31)
-    y = run_ffn(dev, x, gamma, Wg, Wu, Wd, sg, su, sd).float().cpu().numpy()
-    assert np.isfinite(y).all()
-    rows = np.array([0, 1, 255, 256, 511, 777, 1023, 1024, 1290, 1535, 1536, 1800, 2000,
-                     2045, 2046, 2047])
-    ref = orc.swiglu_ffn(bits(x)[rows], bits(gamma), Wg.numpy(), Wu.numpy(), sg.numpy(),
-                         su.numpy(), Wd.numpy(), sd.numpy())
-    np.testing.assert_allclose(y[rows], f32(ref), rtol=1e-2, atol=2e-3)
+    ops_ = ffn_operands(T, H, I, 31)
+    xn, h, y = run_ffn_stages(dev, *ops_)
+    assert torch.isfinite(y.float()).all()
+    check_ffn_stages(ops_, xn, h, y, SAMPLE_ROWS)
 
 
-def test_swiglu_ffn_tp8_shard_row_sample(dev):
+def test_swiglu_gateup_baseline_size_alone(dev):
+    """The gate/up + SiLU * mul stage alone at its benchmark size
+    (2048 x 11008 x 4096, x ~ N(0, 1)) against the oracle on 16 sampled rows."""
+    T, H, I = 2048, 4096, 11008
+    x, Wg, Wu, sg, su = swiglu_operands(T, I, H, 33)
+    Wgu, sgu = ops.swiglu_pack(Wg.to(dev), Wu.to(dev), sg.to(dev), su.to(dev))
+    h = ops.gemm_w8a16_swiglu(x.to(dev), Wgu, sgu, I).cpu()
+    ref = orc.swiglu_gateup(bits(x)[SAMPLE_ROWS], Wg.numpy(), Wu.numpy(), sg.numpy(),
+                            su.numpy())
+    np.testing.assert_allclose(f32(bits(h)[SAMPLE_ROWS]), f32(ref), **TOL)
+
+
+def test_swiglu_ffn_tp8_shard_stages(dev):
     """One GPU's share of an 8-way tensor-parallel block: intermediate
     11008 / 8 = 1376 channels (not a multiple of the image's 64-channel
     blocks: the last block is half padding), gate/up column-parallel, down
     row-parallel over the same slice, so y is this GPU's partial sum of the
-    block's output.  Oracle on 16 sampled token rows."""
+    block's output.  Stage checks on 16 sampled token rows."""
     T, H, I = 2048, 4096, 1376
-    x, gamma, Wg, Wu, Wd, sg, su, sd = ffn_operands(T, H, I, 37)
-    y = run_ffn(dev, x, gamma, Wg, Wu, Wd, sg, su, sd).float().cpu().numpy()
-    assert np.isfinite(y).all()
-    rows = np.array([0, 1, 255, 256, 511, 777, 1023, 1024, 1290, 1535, 1536, 1800, 2000,
-                     2045, 2046, 2047])
-    ref = orc.swiglu_ffn(bits(x)[rows], bits(gamma), Wg.numpy(), Wu.numpy(), sg.numpy(),
-                         su.numpy(), Wd.numpy(), sd.numpy())
-    np.testing.assert_allclose(y[rows], f32(ref), rtol=1e-2, atol=2e-3)
+    ops_ = ffn_operands(T, H, I, 37)
+    xn, h, y = run_ffn_stages(dev, *ops_)
+    assert torch.isfinite(y.float()).all()
+    check_ffn_stages(ops_, xn, h, y, SAMPLE_ROWS)
 
 
 def test_tune_w8a16_caches_a_verified_winner(dev):

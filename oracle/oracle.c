@@ -230,7 +230,11 @@ void hxo_gemv_w8a16(const uint16_t* x, int64_t ldx, const int8_t* W, int64_t ldw
 /* y = exp(x - max) / sum exp(x - max); exp in fp32, sum in fp64 (the most
  * accurate reading of "fp32 sum"), one rounding of the quotient. */
 void hxo_softmax_rows(const void* x, int64_t ldx, void* y, int64_t ldy,
-                      int64_t rows, int64_t cols, int dtype) {
+                      int64_t rows, int64_t cols, int dtype, int threads) {
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+#endif
   for (int64_t r = 0; r < rows; ++r) {
     float m = -INFINITY;
     for (int64_t c = 0; c < cols; ++c) {
@@ -315,7 +319,11 @@ void hxo_swiglu_gateup(const uint16_t* x, int64_t ldx, const int8_t* Wg, const i
 
 void hxo_rmsnorm_rows(const void* x, int64_t ldx, const void* gamma, void* y,
                       int64_t ldy, int64_t rows, int64_t cols, float eps,
-                      int dtype) {
+                      int dtype, int threads) {
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+#endif
   for (int64_t r = 0; r < rows; ++r) {
     double ss = 0.0;
     for (int64_t c = 0; c < cols; ++c) {
@@ -335,7 +343,11 @@ void hxo_rmsnorm_rows(const void* x, int64_t ldx, const void* gamma, void* y,
 void hxo_layernorm_rows(const void* x, int64_t ldx, const void* gamma,
                         const void* beta, void* y, int64_t ldy, float* mean_out,
                         float* rstd_out, int64_t rows, int64_t cols, float eps,
-                        int dtype) {
+                        int dtype, int threads) {
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+#endif
   for (int64_t r = 0; r < rows; ++r) {
     double s = 0.0;
     for (int64_t c = 0; c < cols; ++c) s += ld(x, r * ldx + c, dtype);

@@ -85,9 +85,10 @@ _SIGS = {
                                        _i64, _i32]),
     "hxo_swiglu_gateup": (None, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64,
                                  _i32]),
-    "hxo_softmax_rows": (None, [_p, _i64, _p, _i64, _i64, _i64, _i32]),
-    "hxo_rmsnorm_rows": (None, [_p, _i64, _p, _p, _i64, _i64, _i64, _f32, _i32]),
-    "hxo_layernorm_rows": (None, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i64, _i64, _f32, _i32]),
+    "hxo_softmax_rows": (None, [_p, _i64, _p, _i64, _i64, _i64, _i32, _i32]),
+    "hxo_rmsnorm_rows": (None, [_p, _i64, _p, _p, _i64, _i64, _i64, _f32, _i32, _i32]),
+    "hxo_layernorm_rows": (None, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i64, _i64, _f32, _i32,
+                                  _i32]),
     "hxo_max_threads": (ctypes.c_int, []),
 }
 
@@ -119,8 +120,32 @@ def native_lib():
         return None, f"{type(e).__name__}: {e}"
 
 
+_using = None
+
+
+class using:
+    """``with using(native_lib()[0]): ...`` runs every wrapper below on that
+    build of the same source (bench.py's CPU baselines) instead of the
+    checker build."""
+
+    def __init__(self, l):
+        self.l = l
+
+    def __enter__(self):
+        global _using
+        self.prev, _using = _using, self.l
+        return self.l
+
+    def __exit__(self, *exc):
+        global _using
+        _using = self.prev
+        return False
+
+
 def lib():
     global _lib
+    if _using is not None:
+        return _using
     if _lib is None:
         if not os.path.exists(_LIB_PATH):
             build()
@@ -306,22 +331,25 @@ def _rows_io(x, dtype):
     return x, dt, np.empty_like(x)
 
 
-def softmax_rows(x, dtype="f16") -> np.ndarray:
+def softmax_rows(x, dtype="f16", threads: int = 0) -> np.ndarray:
     x, dt, y = _rows_io(x, dtype)
     rows, cols = x.shape
-    lib().hxo_softmax_rows(_ptr(x), cols, _ptr(y), cols, rows, cols, dt)
+    lib().hxo_softmax_rows(_ptr(x), cols, _ptr(y), cols, rows, cols, dt, threads)
     return y
 
 
-def rmsnorm_rows(x, gamma=None, eps: float = 1e-6, dtype="f16") -> np.ndarray:
+def rmsnorm_rows(x, gamma=None, eps: float = 1e-6, dtype="f16",
+                 threads: int = 0) -> np.ndarray:
     x, dt, y = _rows_io(x, dtype)
     rows, cols = x.shape
     g = None if gamma is None else np.ascontiguousarray(gamma, dtype=x.dtype)
-    lib().hxo_rmsnorm_rows(_ptr(x), cols, _ptr(g), _ptr(y), cols, rows, cols, eps, dt)
+    lib().hxo_rmsnorm_rows(_ptr(x), cols, _ptr(g), _ptr(y), cols, rows, cols, eps, dt,
+                           threads)
     return y
 
 
-def layernorm_rows(x, gamma=None, beta=None, eps: float = 1e-5, dtype="f32"):
+def layernorm_rows(x, gamma=None, beta=None, eps: float = 1e-5, dtype="f32",
+                   threads: int = 0):
     """Returns (y, mean, rstd) with mean/rstd fp32."""
     x, dt, y = _rows_io(x, dtype)
     rows, cols = x.shape
@@ -330,7 +358,7 @@ def layernorm_rows(x, gamma=None, beta=None, eps: float = 1e-5, dtype="f32"):
     mean = np.empty(rows, dtype=np.float32)
     rstd = np.empty(rows, dtype=np.float32)
     lib().hxo_layernorm_rows(_ptr(x), cols, _ptr(g), _ptr(b), _ptr(y), cols,
-                             _ptr(mean), _ptr(rstd), rows, cols, eps, dt)
+                             _ptr(mean), _ptr(rstd), rows, cols, eps, dt, threads)
     return y, mean, rstd
 
 

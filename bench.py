@@ -51,8 +51,8 @@ well (one box: 57.5-57.9 us, against 58.0 us with 2000 warmup launches and
 still runs exactly W untimed launches and then exactly K timed ones.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-       python bench.py --only {int8,int8_i32,f16,ragged,gemv,rows,ffn,copy,vendor}  (one workload,
-       for rocprofv3 runs; prints that workload's record)
+       python bench.py --only {int8,int8_i32,f16,ragged,gemv,rows,ffn,shard,copy,vendor,search,
+                               ceilings}  (one workload, for rocprofv3 runs; prints its record)
 """
 from __future__ import annotations
 
@@ -630,6 +630,49 @@ def run_search(c):
     return out
 
 
+def run_mfma_ceilings(c, A, Bp):
+    """The practical MFMA ceiling of the MFMA-bound configs: hxm_probe_mfma
+    runs the same number of 32x32 MFMAs as the GEMM, one workgroup of four
+    waves per CU (the GEMM kernels' occupancy), on the GEMM's own operand
+    bytes, with no staging and no epilogue.  The chip is power-limited, so
+    with real data this is well below the nominal peak; each GEMM's
+    ceiling_frac is probe time / GEMM time."""
+    torch, hxm, L = c.torch, c.hxm, c.L
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    waves = 4 * cus
+    sink = torch.empty(8192, dtype=torch.int32, device=c.dev)
+    g = torch.Generator().manual_seed(11)
+    xh = torch.randn(2048, 4096, generator=g).half().to(c.dev)     # FFN activations N(0, 1)
+    wq = torch.randint(-127, 128, (11008, 4096), generator=g, dtype=torch.int8).to(c.dev)
+    ah = (torch.rand(4096, 4096, generator=g) * 2 - 1).half().to(c.dev)
+    bh = (torch.rand(4096, 4096, generator=g) * 2 - 1).half().to(c.dev)
+    n = 4096
+    cases = (
+        ("int8_gemm_4096", A, Bp, hxm.I8, hxm.I8, 2.0 * n ** 3, 32 * 32 * 32 * 2, "TOPS"),
+        ("f16_matmul_4096", ah, bh, hxm.F16, hxm.F16, 2.0 * n ** 3, 32 * 32 * 16 * 2, "TFLOPS"),
+        ("swiglu_ffn_2048x4096x11008", xh, wq, hxm.F16, hxm.I8,
+         2.0 * 2048 * 4096 * (2 * 11008) + 2.0 * 2048 * 11008 * 4096, 32 * 32 * 16 * 2, "TFLOPS"),
+    )
+    out = {}
+    for name, a, b, adt, bdt, work, per_mfma, unit in cases:
+        per_wave = int(-(-work // per_mfma // waves))
+        per_wave = -(-per_wave // 32) * 32
+        pa, pb, na, nb = a.data_ptr(), b.data_ptr(), a.numel() * a.element_size(), \
+            b.numel() * b.element_size()
+
+        def step(_, pa=pa, pb=pb, na=na, nb=nb, adt=adt, bdt=bdt, per_wave=per_wave):
+            hxm.check(L.hxm_probe_mfma(pa, na, pb, nb, adt, bdt, per_wave, cus, sink.data_ptr(),
+                                       c.stream), "hxm_probe_mfma")
+        t = c.time_ms(step, 100 if work < 2e12 else 20, 200 if work < 2e12 else 20, reps=4)
+        done = per_wave * waves * per_mfma
+        out[f"mfma_ceiling_{name}"] = {
+            **t.us(), unit: done / (t.median * 1e-3) / 1e12, "mfma_per_wave": per_wave,
+            "workgroups": cus, "work": done,
+            "what": "hxm_probe_mfma: the GEMM's MFMA count on its own operand bytes, nothing "
+                    "else"}
+    return out
+
+
 def run_copy(c):
     """A plain 256 MiB device copy (torch's elementwise copy kernel): the
     known-size reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE."""
@@ -845,7 +888,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", choices=["int8", "int8_i32", "f16", "ragged", "gemv", "rows", "ffn",
-                                       "shard", "copy", "vendor", "search"])
+                                       "shard", "copy", "vendor", "search", "ceilings"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build is the single-GPU kernel set of the hot "
@@ -857,6 +900,8 @@ def main() -> int:
     if args.only:
         if args.only in ("int8", "int8_i32"):
             rec = {args.only: run_int8(c, *int8_operands(c), out_i32=args.only == "int8_i32")}
+        elif args.only == "ceilings":
+            rec = run_mfma_ceilings(c, *int8_operands(c)[:2])
         else:
             rec = {"f16": run_f16, "ragged": run_ragged, "gemv": run_gemv, "rows": run_rows,
                    "ffn": run_ffn, "shard": run_shard, "copy": run_copy, "vendor": run_vendor,
@@ -869,6 +914,11 @@ def main() -> int:
     legs = {}
     if not args.no_extra:
         legs["int8_gemm_i32_out_4096"] = run_int8(c, A, Bp, rs, cs, out_i32=True)
+        try:
+            legs.update(run_mfma_ceilings(c, A, Bp))
+        except Exception as e:
+            log(f"run_mfma_ceilings failed: {e!r}")
+            legs["run_mfma_ceilings"] = {"error": repr(e)}
         for fn in (run_f16, run_ragged, run_gemv, run_rows, run_ffn, run_shard, run_copy,
                    run_vendor, run_search):
             try:
@@ -888,6 +938,9 @@ def main() -> int:
                                                                            args.cpu_seconds)
     log("cpu baselines", json.dumps([cpu_common, {str(k): v for k, v in cpu.items()}]))
 
+    f16l, f16c = legs.get("f16_matmul_4096", {}), legs.get("mfma_ceiling_f16_matmul_4096", {})
+    if "us" in f16l and "q50_us" in f16c:
+        f16l["ceiling_frac"] = f16c["q50_us"] / f16l["us"]
     tops = head["TOPS"]
     cpu2 = cpu.get(2)
     out = {
@@ -961,7 +1014,10 @@ def config_records(head, legs, cpu):
                                    "note": "launch-bound: time per launch replayed from a HIP "
                                            "graph; no roofline fraction",
                                    "cpu": cpu_of(1)}
+    ceil2 = legs.get("mfma_ceiling_int8_gemm_4096", {})
     out["2_int8_gemm_4096_dequant"] = {**base(head, "TOPS", "TOPS", PEAK_INT8_TOPS),
+                                       "ceiling_frac": (_r(ceil2["q50_us"] / head["q50_us"])
+                                                        if "q50_us" in ceil2 else None),
                                        "cpu": cpu_of(2)}
     for M in (1, 4, 16):
         g = legs.get(f"w8a16_gemv_M{M}")
@@ -979,8 +1035,10 @@ def config_records(head, legs, cpu):
                                "graph_us": _r(g["graph_us"], 3), "cpu": cpu_of(f"4_{name}")}
     g = legs.get("swiglu_ffn_2048x4096x11008")
     if g:
+        ceil5 = legs.get("mfma_ceiling_swiglu_ffn_2048x4096x11008", {})
         out["5_swiglu_ffn_2048x4096x11008"] = {
             **base(g, "TFLOPS", "TFLOPS", PEAK_F16_TFLOPS),
+            "ceiling_frac": (_r(ceil5["q50_us"] / g["q50_us"]) if "q50_us" in ceil5 else None),
             "stages_us": {k: _r(v, 2) for k, v in g["stages_us"].items()},
             "graph_us": _r(g["graph_us"], 2),
             "sclk_mhz": g["sclk_under_load"]["median_mhz"] if g.get("sclk_under_load") else None,
@@ -992,7 +1050,7 @@ def compact_extra(legs):
     """The context legs in a few numbers each (their full records go to
     stderr)."""
     keep = ("us", "TOPS", "TFLOPS", "GB/s", "mfma_frac", "hbm_frac", "ceiling_frac", "graph_us",
-            "winner", "default", "winner_us", "default_us", "proof", "error")
+            "winner", "default", "winner_us", "default_us", "proof", "mfma_per_wave", "error")
     out = {}
     for k, v in legs.items():
         if k in ("f16_matmul_256", "swiglu_ffn_2048x4096x11008", "softmax_f16_8192x4096",

@@ -1,3 +1,8 @@
+// Ceiling probes.  MFMA: the matrix cores alone, fed a GEMM's own operand
+// bytes, with the GEMM kernels' occupancy (one wave per SIMD) and their MFMA
+// shapes; it measures what the power-limited clock leaves of the dense peak
+// for that data, the practical ceiling of the MFMA-bound kernels.
+//
 // HBM probes: a streaming copy and a streaming read with the same access
 // pattern as the HBM-bound kernels of this library (16-byte accesses, eight
 // in flight per lane): the copy loads plainly and stores nontemporally, as
@@ -7,6 +12,8 @@
 // with plain loads 8.4 against 8.15 us for 45 MB).  They measure the
 // practical ceiling those kernels are compared against; they have no
 // counterpart in the reference.
+#include <type_traits>
+
 #include "device_util.h"
 #include "hxm_internal.h"
 
@@ -69,6 +76,74 @@ __global__ __launch_bounds__(kProbeThreads) void stream_read_kernel(
   if (acc == never) sink[blockIdx.x] = acc;
 }
 
+// MFMA probe.  Each wave takes two sets of four A and four B fragments
+// (16 bytes per lane each) from the operand bytes -- wave w reads A bytes
+// [8 KiB * w, +8 KiB) and the same window of B, wrapped at the buffers' ends
+// -- and then runs `steps` rounds of 2 x 16 MFMAs over a 4 x 4 grid of 32x32
+// accumulator blocks, the sets alternating, so every instruction sees other
+// data than the one before (the operand toggling, and so the power, of a
+// GEMM's k-steps).  MODE: 0 int8 x int8 (v_mfma_i32_32x32x32_i8), 1 f16,
+// 2 bf16 (v_mfma_f32_32x32x16_*), 3 f16 x int8 (B bytes converted exactly to
+// f16 once, as the W8A16 kernels convert theirs).  Every accumulator is
+// folded into one word per lane, stored only when it equals `never`, so the
+// MFMAs stay and almost nothing is written.
+template <int MODE>
+__global__ __launch_bounds__(256) void mfma_probe_kernel(const uint8_t* __restrict__ a,
+                                                          int64_t a16, const uint8_t* __restrict__ b,
+                                                          int64_t b16, int64_t steps,
+                                                          uint32_t never, uint32_t* __restrict__ sink) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  v4i32 fa[2][4], fb[2][4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int64_t off = w * 8192 + j * 1024 + lane * 16;
+    fa[j / 4][j % 4] = *reinterpret_cast<const v4i32*>(a + (off % a16));
+    fb[j / 4][j % 4] = *reinterpret_cast<const v4i32*>(b + (off % b16));
+    if constexpr (MODE == 3) {  // 16 int8 -> the 8 f16 of the first 8 bytes
+      const v8f16 h = i8x8_to_f16<false>(static_cast<uint32_t>(fb[j / 4][j % 4][0]),
+                                         static_cast<uint32_t>(fb[j / 4][j % 4][1]));
+      fb[j / 4][j % 4] = __builtin_bit_cast(v4i32, h);
+    }
+  }
+  using acc_t = typename std::conditional<MODE == 0, v16i32, v16f32>::type;
+  acc_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = acc_t{};
+  for (int64_t it = 0; it < steps; ++it) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (MODE == 0)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[s][j], fa[s][i], acc[i][j], 0, 0, 0);
+          else if constexpr (MODE == 2)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(v8bf16, fb[s][j]), __builtin_bit_cast(v8bf16, fa[s][i]),
+                acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                __builtin_bit_cast(v8f16, fb[s][j]), __builtin_bit_cast(v8f16, fa[s][i]),
+                acc[i][j], 0, 0, 0);
+        }
+  }
+  uint32_t fold = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const auto v = acc[i][j][e];  // copy the element out (see gemm_kernel.h)
+        fold ^= __builtin_bit_cast(uint32_t, v);
+      }
+  if (fold == never) sink[blockIdx.x] = fold;
+}
+
 // One chunk per workgroup, at most HXM_PROBE_SINK_WORDS workgroups (32 per
 // CU); larger buffers loop.
 int64_t probe_groups(int64_t n16) {
@@ -119,6 +194,45 @@ hxm_status hxm_probe_read(const void* src, int64_t bytes, uint32_t* sink, void* 
                        as_stream(stream)>>>(static_cast<const v4u32_t*>(src), n16, 0xffffffffu,
                                             sink);
   return check_launch("probe_read");
+}
+
+hxm_status hxm_probe_mfma(const void* a, int64_t a_bytes, const void* b, int64_t b_bytes,
+                          int32_t a_dtype, int32_t b_dtype, int64_t mfma_per_wave,
+                          int32_t workgroups, uint32_t* sink, void* stream) {
+  int mode = -1;
+  if (a_dtype == HXM_I8 && b_dtype == HXM_I8) mode = 0;
+  else if (a_dtype == HXM_F16 && b_dtype == HXM_F16) mode = 1;
+  else if (a_dtype == HXM_BF16 && b_dtype == HXM_BF16) mode = 2;
+  else if (a_dtype == HXM_F16 && b_dtype == HXM_I8) mode = 3;
+  if (mode < 0)
+    return fail(HXM_UNSUPPORTED_DTYPE,
+                "unsupported-dtype: probe_mfma takes int8 x int8, f16 x f16, bf16 x bf16 or "
+                "f16 x int8 (got %d x %d)", a_dtype, b_dtype);
+  if (a_bytes < 16 || b_bytes < 16 || a_bytes % 16 || b_bytes % 16)
+    return fail(HXM_INVALID_ARG, "invalid-argument: probe_mfma operand bytes must be positive "
+                                 "multiples of 16");
+  if (!a || !b || !aligned16(a) || !aligned16(b) || !sink)
+    return fail(HXM_INVALID_ARG, "invalid-argument: probe_mfma needs 16-byte aligned operands "
+                                 "and a sink");
+  if (mfma_per_wave <= 0 || mfma_per_wave % 32)
+    return fail(HXM_INVALID_ARG, "invalid-argument: probe_mfma mfma_per_wave must be a positive "
+                                 "multiple of 32 (got %lld)", (long long)mfma_per_wave);
+  if (workgroups < 1 || workgroups > HXM_PROBE_SINK_WORDS)
+    return fail(HXM_INVALID_ARG, "invalid-argument: probe_mfma workgroups in [1, %d]",
+                HXM_PROBE_SINK_WORDS);
+  hxm_status st = require_device(nullptr);
+  if (st != HXM_OK) return st;
+  const int64_t steps = mfma_per_wave / 32;
+  const uint8_t* pa = static_cast<const uint8_t*>(a);
+  const uint8_t* pb = static_cast<const uint8_t*>(b);
+  hipStream_t s = as_stream(stream);
+  switch (mode) {
+    case 0: mfma_probe_kernel<0><<<workgroups, 256, 0, s>>>(pa, a_bytes, pb, b_bytes, steps, 0xffffffffu, sink); break;
+    case 1: mfma_probe_kernel<1><<<workgroups, 256, 0, s>>>(pa, a_bytes, pb, b_bytes, steps, 0xffffffffu, sink); break;
+    case 2: mfma_probe_kernel<2><<<workgroups, 256, 0, s>>>(pa, a_bytes, pb, b_bytes, steps, 0xffffffffu, sink); break;
+    default: mfma_probe_kernel<3><<<workgroups, 256, 0, s>>>(pa, a_bytes, pb, b_bytes, steps, 0xffffffffu, sink); break;
+  }
+  return check_launch("probe_mfma");
 }
 
 }  // extern "C"

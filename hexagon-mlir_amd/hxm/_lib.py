@@ -140,6 +140,7 @@ SIGNATURES = {
                                  _p]),
     "hxm_probe_copy": (_st, [_p, _p, _i64, _p]),
     "hxm_probe_read": (_st, [_p, _i64, _p, _p]),
+    "hxm_probe_mfma": (_st, [_p, _i64, _p, _i64, _i32, _i32, _i64, _i32, _p, _p]),
     "hxm_reason_string": (ctypes.c_char_p, [_i32]),
     "hxm_tile_ladder": (_i32, [_i64, ctypes.POINTER(_i64), _i32]),
     "hxm_hmx_tile_verdict": (_i32, [_i64, _i64, _i64, _i64]),

@@ -433,7 +433,7 @@ hxm_status hxm_layernorm_rows(const void* x, int64_t ldx, const void* gamma,
                               int64_t cols, float eps, int32_t dtype,
                               void* stream);
 
-/* ---- HBM probes (measurement helpers; no counterpart in the reference) ----
+/* ---- ceiling probes (measurement helpers; no counterpart in the reference) --
  * The practical ceiling of the HBM-bound kernels above, measured with the
  * same access pattern (16-byte accesses, eight in flight per lane; the copy
  * loads plainly and stores nontemporally like the row kernels, the read
@@ -447,6 +447,21 @@ hxm_status hxm_probe_copy(const void* src, void* dst, int64_t bytes, void* strea
 /* Reads src[0, bytes) and folds it; sink (at least HXM_PROBE_SINK_WORDS
  * uint32 of device memory) receives a word only for one rare fold value. */
 hxm_status hxm_probe_read(const void* src, int64_t bytes, uint32_t* sink, void* stream);
+
+/* MFMA probe (measurement helper; no counterpart in the reference): the
+ * practical ceiling of the MFMA-bound kernels.  `workgroups` workgroups of
+ * four waves (one per SIMD, the GEMM kernels' occupancy: one per CU) each run
+ * mfma_per_wave 32x32 MFMAs (a positive multiple of 32) of the GEMMs' shapes
+ * -- int8 x int8 (v_mfma_i32_32x32x32_i8), f16 x f16 or bf16 x bf16
+ * (v_mfma_f32_32x32x16_*), or f16 x int8 (B converted to f16 as the W8A16
+ * kernels do) -- on operand fragments read once from a[0, a_bytes) and
+ * b[0, b_bytes) (multiples of 16, 16-byte aligned): a GEMM's own operands
+ * give its data-dependent power draw, and so its clock.  Nothing else runs:
+ * no staging, no epilogue.  sink: at least HXM_PROBE_SINK_WORDS uint32,
+ * written only for one rare fold value of the accumulators. */
+hxm_status hxm_probe_mfma(const void* a, int64_t a_bytes, const void* b, int64_t b_bytes,
+                          int32_t a_dtype, int32_t b_dtype, int64_t mfma_per_wave,
+                          int32_t workgroups, uint32_t* sink, void* stream);
 
 /* ---- tile search (backend/hmx_search.py) -------------------------------- */
 

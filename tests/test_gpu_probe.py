@@ -1,6 +1,8 @@
-"""The HBM probes bench.py measures its ceilings with: the streaming copy
-reproduces its source exactly (whole passes and a ragged tail), and the
-streaming read runs and leaves its inputs untouched."""
+"""The ceiling probes bench.py measures its ceilings with: the streaming copy
+reproduces its source exactly (whole passes and a ragged tail), the
+streaming read runs and leaves its inputs untouched, and the MFMA probe runs
+every operand pairing, leaves its operands untouched and refuses what it
+cannot run."""
 import pytest
 import torch
 
@@ -33,3 +35,37 @@ def test_probe_read_runs_and_writes_at_most_the_sink(dev):
                                  torch.cuda.current_stream().cuda_stream), "hxm_probe_read")
     torch.cuda.synchronize()
     assert torch.equal(src, keep)
+
+
+@pytest.mark.parametrize("a_dt,b_dt", [(hxm.I8, hxm.I8), (hxm.F16, hxm.F16), (hxm.BF16, hxm.BF16),
+                                       (hxm.F16, hxm.I8)])
+def test_probe_mfma_runs_and_leaves_its_operands(dev, a_dt, b_dt):
+    """The MFMA ceiling probe runs every operand pairing on a small grid,
+    reads its operands without changing them, and writes the sink at most
+    where the fold equals the rare value; wrapped windows (operands smaller
+    than a wave's 8 KiB) stay inside the buffers."""
+    print(f"probe_mfma {a_dt} x {b_dt}", flush=True)
+    g = torch.Generator().manual_seed(a_dt * 10 + b_dt)
+    a = torch.randint(-127, 128, (64 << 10,), generator=g, dtype=torch.int8).to(dev)
+    b = torch.randint(-127, 128, (4096 + 48,), generator=g, dtype=torch.int8).to(dev)
+    ka, kb = a.clone(), b.clone()
+    sink = torch.zeros(8192, dtype=torch.int32, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    hxm.check(lib.hxm_probe_mfma(a.data_ptr(), a.numel(), b.data_ptr(), b.numel(), a_dt, b_dt,
+                                 64, 16, sink.data_ptr(), st), "hxm_probe_mfma")
+    torch.cuda.synchronize()
+    assert torch.equal(a, ka) and torch.equal(b, kb)
+    assert int((sink[16:] != 0).sum()) == 0
+
+
+def test_probe_mfma_refusals(dev):
+    a = torch.zeros(8192, dtype=torch.int8, device=dev)
+    sink = torch.zeros(8192, dtype=torch.int32, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    p, s = a.data_ptr(), sink.data_ptr()
+    assert lib.hxm_probe_mfma(p, 8192, p, 8192, hxm.I8, hxm.F16, 32, 1, s, st) != 0
+    assert "unsupported-dtype" in hxm.last_error()
+    assert lib.hxm_probe_mfma(p, 8192, p, 8192, hxm.I8, hxm.I8, 48, 1, s, st) != 0
+    assert lib.hxm_probe_mfma(p, 8000 + 8, p, 8192, hxm.I8, hxm.I8, 32, 1, s, st) != 0
+    assert lib.hxm_probe_mfma(p, 8192, p, 8192, hxm.I8, hxm.I8, 32, 0, s, st) != 0
+    assert lib.hxm_probe_mfma(p, 8192, p, 8192, hxm.I8, hxm.I8, 32, 1, None, st) != 0

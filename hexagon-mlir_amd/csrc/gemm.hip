@@ -115,7 +115,7 @@ static gemm_fn part_fn(const gemm_fn (*const parts[kGemmParts])[E], int i, int e
 }
 static const gemm_fn (*const kI8Parts[kGemmParts])[2] = {kI8Fns_p0, kI8Fns_p1, kI8Fns_p2};
 static const gemm_fn (*const kF16Parts[kGemmParts])[2] = {kF16Fns_p0, kF16Fns_p1, kF16Fns_p2};
-static const gemm_fn (*const kW8Parts[kGemmParts])[3] = {kW8Fns_p0, kW8Fns_p1, kW8Fns_p2};
+static const gemm_fn (*const kW8Parts[kGemmParts])[6] = {kW8Fns_p0, kW8Fns_p1, kW8Fns_p2};
 
 static int elem_bytes(int32_t dt) { return dt == HXM_I8 ? 1 : 2; }
 
@@ -590,6 +590,8 @@ hxm_gemm_config w8_kernel_config(int i) {
   return c;
 }
 bool w8_kernel_has_swiglu(int i) { return part_fn(kW8Parts, i, 1) != nullptr; }
+// Entry i has a stream-K form (split_k = HXM_STREAM_K).
+bool w8_kernel_has_stream_k(int i) { return part_fn(kW8Parts, i, 3) != nullptr; }
 
 static const KernelEntry* find_w8_kernel(const hxm_gemm_config& c, bool swiglu) {
   for (int i = 0; i < kNumW8Kernels; ++i) {
@@ -597,7 +599,9 @@ static const KernelEntry* find_w8_kernel(const hxm_gemm_config& c, bool swiglu) 
     if (k.bm == c.bm && k.bn == c.bn && (c.bk == 0 || c.bk == k.bk) &&
         (c.waves_m == 0 || c.waves_m == k.waves_m) &&
         (c.waves_n == 0 || c.waves_n == k.waves_n) &&
-        (c.stages == 0 || c.stages == k.stages) && (c.split_k == 0 || c.split_k == 1) &&
+        (c.stages == 0 || c.stages == k.stages) &&
+        (c.split_k == 0 || c.split_k == 1 ||
+         (c.split_k == HXM_STREAM_K && w8_kernel_has_stream_k(i))) &&
         (!swiglu || w8_kernel_has_swiglu(i)))
       return &kW8Kernels[i];
   }
@@ -639,6 +643,17 @@ __global__ __launch_bounds__(256) void swiglu_pack_kernel(
     out_scale[r] = ch < I ? (up ? su : sg)[ch] : 0.0f;
 }
 
+// Stream-K buffer of a W8A16 launch: the arrival counters (one per
+// stream-K tile, padded to 256 bytes) and then sk.tiles * sk.maxseg fp32
+// partial tiles of BM x BN.
+static int64_t stream_k_counter_bytes(const StreamKLayout& sk) {
+  return (static_cast<int64_t>(sk.tiles) * 4 + 255) / 256 * 256;
+}
+static int64_t stream_k_bytes(const KernelEntry& e, const StreamKLayout& sk) {
+  return stream_k_counter_bytes(sk) +
+         static_cast<int64_t>(sk.tiles) * sk.maxseg * e.cfg.bm * e.cfg.bn * 4;
+}
+
 // plan_gemm for the W8A16 GEMMs (f16 A, int8 [N, K] B): N is the B rows
 // (the SwiGLU image's), n_out the output columns.
 hxm_status plan_gemm_w8(int32_t op, bool sw, int64_t M, int64_t N, int64_t n_out, int64_t K,
@@ -674,9 +689,28 @@ hxm_status plan_gemm_w8(int32_t op, bool sw, int64_t M, int64_t N, int64_t n_out
     p->threads = e->threads;
     p->tiles = ((M + e->cfg.bm - 1) / e->cfg.bm) * ((N + e->cfg.bn - 1) / e->cfg.bn);
     p->lds_bytes = kernel_lds_bytes(*e, true, false);
-    if (!grid_fits(p->tiles, e->threads)) {
+    int64_t groups = p->tiles;
+    if (c.split_k == HXM_STREAM_K) {
+      // Stream-K when the tiles leave a partial round; whole rounds run as
+      // split_k = 1.  The plan records the mode, the partial-tile slots (as
+      // k_slices: the most workgroups one tile is cut over) and the buffer.
+      StreamKLayout sk;
+      const int64_t KT = (K * 2 + e->cfg.bk - 1) / e->cfg.bk;
+      if (K > 0 && stream_k_layout(p->tiles, KT, device_cu_count(), &sk)) {
+        p->config.split_k = HXM_STREAM_K;
+        p->k_slices = sk.maxseg;
+        p->workspace_bytes = stream_k_bytes(*e, sk);
+        groups = sk.dp + sk.groups;
+      }
+    }
+    if (p->workspace_bytes > kSplitKPlaneBytesMax) {
+      snprintf(why, sizeof(why),
+               "stream-K needs %lld bytes of fp32 partial tiles, above the %lld-byte limit",
+               (long long)p->workspace_bytes, (long long)kSplitKPlaneBytesMax);
+      st = refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_WORKSPACE_BUDGET, why);
+    } else if (!grid_fits(groups, e->threads)) {
       snprintf(why, sizeof(why), "%lld workgroups of %d threads exceed the launch limit",
-               (long long)p->tiles, e->threads);
+               (long long)groups, e->threads);
       st = refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_TILE_ALIGNMENT, why);
     } else {
       const bool full = M % 32 == 0 && n_out % 32 == 0 && K % 32 == 0;
@@ -723,8 +757,35 @@ hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const in
   g.vec_store = (reinterpret_cast<uintptr_t>(C) % 8 == 0) && ((ldc * 2) % 8 == 0);
   g.vec8_store = (reinterpret_cast<uintptr_t>(C) % 16 == 0) && ((ldc * 2) % 16 == 0);
   const int wi = static_cast<int>(e - kW8Kernels);
-  hipLaunchKernelGGL(part_fn(kW8Parts, wi, sw ? 1 : epi == kEpiW8Res ? 2 : 0),
-                     dim3(static_cast<unsigned>(plan.tiles)),
+  int64_t groups = plan.tiles;
+  if (plan.config.split_k == HXM_STREAM_K) {
+    StreamKLayout sk;
+    const int64_t KT = (K * 2 + e->cfg.bk - 1) / e->cfg.bk;
+    if (!stream_k_layout(plan.tiles, KT, device_cu_count(), &sk))
+      return fail(HXM_HIP_ERROR, "hip-error: stream-K layout changed between plan and launch");
+    void* ws = nullptr;
+    bool grown = false;
+    if ((st = stream_workspace(stream, static_cast<size_t>(stream_k_bytes(*e, sk)), &ws,
+                               kWsStreamK, &grown)) != HXM_OK)
+      return st;
+    // A new buffer's counters start at zero; every launch leaves them there
+    // (the last workgroup at a tile resets its counter).  Growth is refused
+    // under graph capture, so this fill is never captured.
+    if (grown) HXM_HIP_TRY(hipMemsetAsync(ws, 0, static_cast<size_t>(stream_k_counter_bytes(sk)),
+                                          stream));
+    g.sk_first = sk.dp;
+    g.sk_groups = sk.groups;
+    g.sk_tiles = sk.tiles;
+    g.sk_iters = sk.iters;
+    g.sk_maxseg = sk.maxseg;
+    g.sk_xcd = sk.xcd;
+    g.sk_count = static_cast<uint32_t*>(ws);
+    g.sk_part = reinterpret_cast<float*>(static_cast<char*>(ws) + stream_k_counter_bytes(sk));
+    groups = sk.dp + sk.groups;
+  }
+  const int fe = (sw ? 1 : epi == kEpiW8Res ? 2 : 0) +
+                 (plan.config.split_k == HXM_STREAM_K ? 3 : 0);
+  hipLaunchKernelGGL(part_fn(kW8Parts, wi, fe), dim3(static_cast<unsigned>(groups)),
                      dim3(e->threads), 0, stream, g);
   if ((st = check_launch("w8a16 gemm kernel")) != HXM_OK) return st;
   return ok();

@@ -117,7 +117,21 @@ struct GemmArgs {
   int split = 1;
   int kslice_bytes = 0;
   int64_t plane_elems = 0;
+  // Stream-K (the int8-weight kernels): workgroups [sk_first, sk_first +
+  // sk_groups) of the launch each take sk_iters consecutive K stages of the
+  // stream over the tiles the data-parallel workgroups [0, sk_first) leave
+  // (sk_tiles of them); a tile whose stages span several workgroups is
+  // finished by the last to arrive (below).  sk_groups = 0: none.
+  int sk_first = 0, sk_groups = 0, sk_tiles = 0, sk_iters = 0, sk_maxseg = 0;
+  int sk_xcd = 0;            // 1: each XCD's workgroups stream that XCD's own tiles
+  float* sk_part = nullptr;  // fp32 partial tiles, sk_tiles * sk_maxseg slots
+  uint32_t* sk_count = nullptr;  // one arrival counter per stream-K tile, left at 0
 };
+
+// Cache-policy bit of the buffer intrinsics' aux operand: sc1, coherent at
+// device scope across the XCDs' separate L2s (stores write through, loads do
+// not hit a line another XCD may have changed).
+constexpr int kAuxSc1 = 16;
 
 template <typename T>
 struct Mfma;
@@ -275,8 +289,8 @@ __device__ __forceinline__ v4i32 lds_frag(const uint8_t* lds, int row, int chunk
   return *reinterpret_cast<const v4i32*>(lds + row * BKB + ((chunk ^ swz<BKB>(row)) << 4));
 }
 
-template <typename T, int BM, int BN, int BKB, int STAGES, int WM, int WN, int EPI>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
+template <typename T, int BM, int BN, int BKB, int STAGES, int WM, int WN, int EPI, int SK = 0>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g0) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;  // wave sub-tile
   constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 blocks per wave
@@ -301,6 +315,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   // NF-2 and NF-1, which must not come before the read.
   static_assert(!BQ || NF >= 4, "int8 B needs at least 4 MFMA slots per k-step");
   static_assert(EPI != kEpiSwiglu || TN == 128, "SwiGLU image interleaves 64-channel blocks");
+  static_assert(!SK || BQ, "stream-K is compiled for the int8-weight kernels");
   // Epilogue scales in LDS: rows [0, QR*64), columns [QR*64, (QR+QC)*64) floats.
   constexpr int QR = EPI == kEpiDequant ? (BM + 63) / 64 : 0;
   constexpr int QC = EPI == kEpiDequant || BQ ? (BN + 63) / 64 : 0;
@@ -315,34 +330,98 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     return u == 0 ? s0 : u == 1 ? s1 : u == 2 ? s2 : s3;
   };
 
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform
-  const int wm = wave / WN, wn = wave % WN;
-
-  if (g.split > 1) {  // uniform: this workgroup's K slice and C plane
+  if (g0.split > 1) {  // uniform: this workgroup's K slice and C plane
     const int z = blockIdx.y;
-    const int kb0 = z * g.kslice_bytes;  // a multiple of BKB (host)
-    g.A += kb0;
-    g.B += BQ ? kb0 / 2 : kb0;
-    g.K_bytes = min(g.kslice_bytes, g.K_bytes - kb0);
-    g.C = static_cast<char*>(g.C) +
-          static_cast<int64_t>(z) * g.plane_elems * (g.out_dtype == HXM_I32 || g.out_dtype == HXM_F32 ? 4 : 2);
+    const int kb0 = z * g0.kslice_bytes;  // a multiple of BKB (host)
+    g0.A += kb0;
+    g0.B += BQ ? kb0 / 2 : kb0;
+    g0.K_bytes = min(g0.kslice_bytes, g0.K_bytes - kb0);
+    g0.C = static_cast<char*>(g0.C) +
+           static_cast<int64_t>(z) * g0.plane_elems * (g0.out_dtype == HXM_I32 || g0.out_dtype == HXM_F32 ? 4 : 2);
   }
 
   // ---- XCD-aware tile order ----
-  const int tiles_m = (g.M + BM - 1) / BM;
-  const int tiles_n = (g.N + BN - 1) / BN;
+  // Workgroups are dispatched round-robin over the 8 XCDs, so ordinal b is
+  // remapped to position b >> 3 of XCD b & 7's window of ntiles / 8 tiles,
+  // and each window is walked in groups of g.group_m tile-rows.
+  const int tiles_m = (g0.M + BM - 1) / BM;
+  const int tiles_n = (g0.N + BN - 1) / BN;
   const int ntiles = tiles_m * tiles_n;
-  int t = blockIdx.x;
-  if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
-  const int gm = g.group_m;
-  const int per_group = gm * tiles_n;
-  const int group = t / per_group;
-  const int first_m = group * gm;
-  const int gsize = min(tiles_m - first_m, gm);
-  const int tm = first_m + (t % per_group) % gsize;
-  const int tn = (t % per_group) / gsize;
-  const int m0 = tm * BM, n0 = tn * BN;
+  auto walk = [&](int b) { return (ntiles & 7) == 0 ? (b & 7) * (ntiles >> 3) + (b >> 3) : b; };
+  auto tile_origin = [&](int t, int& m0, int& n0) {
+    const int gm = g0.group_m;
+    const int per_group = gm * tiles_n;
+    const int group = t / per_group;
+    const int first_m = group * gm;
+    const int gsize = min(tiles_m - first_m, gm);
+    m0 = (first_m + (t % per_group) % gsize) * BM;
+    n0 = ((t % per_group) / gsize) * BN;
+  };
+
+  // The tile body runs once per tile, or (stream-K) once per segment: K
+  // stages [k0, k1) of one tile, with A, B and K_bytes of the arguments
+  // moved to cover the segment.  After the main loop a whole tile
+  // goes to the epilogue; a segment of a tile spread over several
+  // workgroups goes through the partial-tile exchange, which leaves the last
+  // workgroup to arrive with the whole tile.  Without stream-K the loop
+  // condition is constant false: one pass, the body as straight-line code.
+  __shared__ int sk_last;
+  const int KT_all = (g0.K_bytes + BKB - 1) / BKB;
+  // Stream-K: workgroups [0, sk_first) take one whole tile each, as the
+  // plain kernel; the sk_groups after them each take sk_iters consecutive K
+  // stages of the stream of the remaining tiles (per XCD, the stream of that
+  // XCD's own window when sk_xcd: its tiles share A and B panels in that
+  // XCD's L2), segment by segment.
+  const bool whole = !SK || static_cast<int>(blockIdx.x) < g0.sk_first;
+  const int sk_b = blockIdx.x - g0.sk_first;
+  const int sk_x = SK && g0.sk_xcd ? sk_b & 7 : 0;
+  const int sk_w = SK && g0.sk_xcd ? sk_b >> 3 : sk_b;                      // index in the stream
+  const int sk_tn = SK && g0.sk_xcd ? g0.sk_tiles >> 3 : g0.sk_tiles;       // tiles in the stream
+  int64_t it = whole ? 0 : static_cast<int64_t>(sk_w) * g0.sk_iters;
+  const int64_t it_end =
+      whole ? KT_all
+            : min(static_cast<int64_t>(sk_tn) * KT_all, static_cast<int64_t>(sk_w + 1) * g0.sk_iters);
+  if (SK && it >= it_end) return;  // a stream-K workgroup with no stages left
+  const uint8_t* const sk_A = g0.A;
+  const uint8_t* const sk_B = g0.B;
+  const int sk_K = g0.K_bytes;
+  do {
+    int m0, n0, sk_slot = -1, sk_seg = 0, sk_nseg = 1;
+    if constexpr (SK) {
+      const int st = whole ? 0 : static_cast<int>(it / KT_all);
+      const int k0 = static_cast<int>(it % KT_all);
+      const int k1 = static_cast<int>(min<int64_t>(KT_all, k0 + (it_end - it)));
+      if (!whole) {
+        const int64_t tfirst = static_cast<int64_t>(st) * KT_all;
+        const int seg0 = static_cast<int>(tfirst / g0.sk_iters);
+        sk_nseg = static_cast<int>((tfirst + KT_all - 1) / g0.sk_iters) - seg0 + 1;
+        sk_seg = sk_w - seg0;
+        sk_slot = sk_x * sk_tn + st;
+      }
+      // The tile's walk index: the workgroup's own, or position sk_first / 8
+      // + st of this XCD's window, or ordinal sk_first + st.
+      tile_origin(whole       ? walk(blockIdx.x)
+                  : g0.sk_xcd ? sk_x * (ntiles >> 3) + (g0.sk_first >> 3) + st
+                              : walk(g0.sk_first + st),
+                  m0, n0);
+      g0.A = sk_A + k0 * BKB;
+      g0.B = sk_B + k0 * (BKB / 2);
+      g0.K_bytes = min(sk_K, k1 * BKB) - k0 * BKB;
+      it += k1 - k0;
+      wait_and_barrier<0>();  // the previous segment is done with the LDS
+    } else {
+      tile_origin(walk(blockIdx.x), m0, n0);
+    }
+    const GemmArgs& g = g0;
+    // The lane's indices.  In the stream-K loop they come from an opaque
+    // copy of the thread id made in each pass, so the compiler recomputes
+    // what depends on them per tile instead of hoisting it out of the loop
+    // and holding it in registers through the main loop.
+    int tid = threadIdx.x;
+    if constexpr (SK) asm volatile("" : "+v"(tid));
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
+    const int wm = wave / WN, wn = wave % WN;
 
   const v4i32 ra = operand_rsrc(g.A, g.lda_bytes, m0, g.M, g.K_bytes);
   const v4i32 rb = operand_rsrc(g.B, g.ldb_bytes, n0, g.N, BQ ? g.K_bytes / 2 : g.K_bytes);
@@ -577,6 +656,96 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
       main_loop(std::true_type{});
   }
 
+  // ---- stream-K: partial tiles ----
+  // Every segment of a shared tile stores its fp32 accumulators (each lane's
+  // registers, 16 bytes a store, device-coherent) in its slot, then counts
+  // its arrival; the workgroup that arrives last adds the slots in segment
+  // order -- a fixed order, so the result does not depend on which
+  // workgroup that is -- resets the counter for the next launch and runs the
+  // epilogue.  Nobody waits for anybody: a workgroup that is not last is
+  // done.
+  if constexpr (SK) {
+    if (sk_slot >= 0 && sk_nseg > 1) {
+      constexpr int kWaveFloats = FM * FN * 16 * 64;
+      wait_and_barrier<0>();  // the main loop's last (past-K) loads have landed
+      const int64_t slot_bytes = static_cast<int64_t>(NW) * kWaveFloats * 4;
+      const uint8_t* part0 = reinterpret_cast<const uint8_t*>(g.sk_part) +
+                             static_cast<int64_t>(sk_slot) * g.sk_maxseg * slot_bytes;
+      auto slot_rsrc = [&](int seg) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(part0 + seg * slot_bytes),
+                                                 static_cast<short>(0),
+                                                 static_cast<int>(slot_bytes), 0x00020000);
+      };
+      const uint32_t wave_off = static_cast<uint32_t>(wave) * kWaveFloats * 4 + lane * 16;
+      {
+        const __amdgpu_buffer_rsrc_t mine = slot_rsrc(sk_seg);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              v4f32 v;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float a = acc[i][j][q * 4 + e];  // copy the element out first
+                v[e] = a;
+              }
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  __builtin_bit_cast(v4u32_t, v), mine,
+                  wave_off + static_cast<uint32_t>(((i * FN + j) * 4 + q) * 1024), 0, kAuxSc1);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+      }
+      // Every wave's stores complete before the workgroup's one arrival.
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      if (threadIdx.x == 0) {
+        const uint32_t before = __hip_atomic_fetch_add(g.sk_count + sk_slot, 1u, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
+        const int last = before == static_cast<uint32_t>(sk_nseg - 1);
+        if (last)
+          __hip_atomic_store(g.sk_count + sk_slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sk_last = last;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (!sk_last) continue;
+      // The whole tile: every slot, this segment's own included (its stores
+      // completed above), added in segment order, ((p0 + p1) + p2) ..., and
+      // written over the accumulators, which are not read again.  One row
+      // of FN blocks of one slot is loaded per round trip (every load of the
+      // row in flight at once): a block at a time, each a device-coherent
+      // round trip, cost 21 us on the FFN's gate/up GEMM.
+      auto slot_row = [&](int sg, int i, acc_t (&v)[FN]) {
+        const __amdgpu_buffer_rsrc_t r = slot_rsrc(sg);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const v4f32 x = __builtin_bit_cast(
+                v4f32, __builtin_amdgcn_raw_buffer_load_b128(
+                           r, wave_off + static_cast<uint32_t>(((i * FN + j) * 4 + q) * 1024), 0,
+                           kAuxSc1));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[j][q * 4 + e] = x[e];
+          }
+      };
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        acc_t t[FN];
+        slot_row(0, i, t);
+        for (int sg = 1; sg < sk_nseg; ++sg) {
+          acc_t v[FN];
+          slot_row(sg, i, v);
+#pragma unroll
+          for (int j = 0; j < FN; ++j) t[j] += v[j];
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = t[j];
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+
   // ---- epilogue ----
   // Lane l holds, for block (i, j) and register group q = v/4, row
   // m = i*32 + l%32 of the wave tile and the four consecutive columns
@@ -759,7 +928,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         pipeline(std::false_type{});
       else
         pipeline(std::true_type{});
-      return;
+      continue;
     }
   }
   // SwiGLU (full tiles, or edge tiles with n_out % 8 == 0): the same
@@ -847,7 +1016,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         pipeline(std::false_type{});
       else
         pipeline(std::true_type{});
-      return;
+      continue;
     }
   }
   if constexpr (EPI == kEpiI32 || EPI == kEpiFloat) {
@@ -913,7 +1082,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         plain(std::false_type{});
       else
         plain(std::true_type{});
-      return;
+      continue;
     }
   }
 
@@ -1121,6 +1290,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
       }
     }
   }
+  } while (SK && it < it_end);
 }
 
 typedef void (*gemm_fn)(GemmArgs);
@@ -1155,7 +1325,8 @@ constexpr int config_index(const ConfigKey (&keys)[N], int bm, int bn, int bkb, 
 #define HXM_DECLARE_PART_TABLES(P)            \
   extern const gemm_fn kI8Fns_p##P[][2];  /* {kEpiI32, kEpiDequant} */ \
   extern const gemm_fn kF16Fns_p##P[][2]; /* {f16, bf16} operands, kEpiFloat */ \
-  extern const gemm_fn kW8Fns_p##P[][3];  /* {kEpiW8, kEpiSwiglu (null unless TN == 128), kEpiW8Res} */
+  extern const gemm_fn kW8Fns_p##P[][6];  /* {kEpiW8, kEpiSwiglu (null unless TN == 128), kEpiW8Res}, \
+                                              then the same three in stream-K form */
 HXM_DECLARE_PART_TABLES(0)
 HXM_DECLARE_PART_TABLES(1)
 HXM_DECLARE_PART_TABLES(2)

@@ -52,6 +52,42 @@ inline int32_t k_slices(int64_t k_bytes, int64_t stage_bytes, int32_t split) {
   return static_cast<int32_t>(ceil_div(stages, per));
 }
 
+// Stream-K layout of an int8-weight GEMM launch of `ntiles` tiles of KT K
+// stages each on `cus` CUs (one workgroup per CU): the first dp tiles, whole
+// rounds, run one per workgroup; the rest (tiles = ntiles mod cus) are cut
+// into one stream of tiles * KT stages, and `groups` (= cus) workgroups take
+// `iters` consecutive stages each, so every CU does the same share of the
+// last round.  With xcd, each XCD's cus / 8 workgroups stream only that
+// XCD's tiles/8 tiles (its own window of the tile walk, whose A and B panels
+// its L2 holds); it needs ntiles, dp and cus to be multiples of 8.  maxseg:
+// the most workgroups one tile's stages are spread over (partial-tile slots
+// per tile).  False when nothing is left for a stream (whole rounds) or an
+// argument is out of range.
+struct StreamKLayout {
+  int32_t dp, groups, tiles, iters, maxseg, xcd;
+};
+inline bool stream_k_layout(int64_t ntiles, int64_t KT, int64_t cus, StreamKLayout* out) {
+  if (!out || ntiles <= 0 || KT <= 0 || cus <= 0 || ntiles > INT32_MAX / 2 ||
+      KT > INT32_MAX / 2 || cus > 65536)
+    return false;
+  const int64_t S = ntiles % cus;
+  if (S == 0) return false;
+  const int64_t dp = ntiles - S;
+  const bool xcd = ntiles % 8 == 0 && dp % 8 == 0 && cus % 8 == 0;
+  const int64_t streams = xcd ? 8 : 1;
+  const int64_t tiles = S / streams, groups = cus / streams;
+  const int64_t iters = ceil_div(tiles * KT, groups);
+  int64_t maxseg = 1;
+  for (int64_t t = 0; t < tiles; ++t) {
+    const int64_t nseg = (t * KT + KT - 1) / iters - (t * KT) / iters + 1;
+    if (nseg > maxseg) maxseg = nseg;
+  }
+  *out = StreamKLayout{static_cast<int32_t>(dp), static_cast<int32_t>(cus),
+                       static_cast<int32_t>(S), static_cast<int32_t>(iters),
+                       static_cast<int32_t>(maxseg), xcd ? 1 : 0};
+  return true;
+}
+
 // One entry of the tuning-cache file: "op M N K bm bn bk waves_m waves_n
 // stages split_k reps".  Every field is read as 64-bit and range-checked
 // before it narrows, so an out-of-range value cannot wrap onto a compiled

@@ -54,11 +54,16 @@ hxm_status require_device(int* device_out);
 // one buffer per stream never races with itself.  Slot 0 holds per-call
 // operand packs and the tuner's reference output; slot 1 the split-K
 // partial planes, so the two never overwrite or reallocate each other.
-constexpr int kWsMain = 0, kWsSplitK = 1;
+constexpr int kWsMain = 0, kWsSplitK = 1, kWsStreamK = 2;
 // Largest split-K partial-plane buffer (S * M * N int32) a call may ask for;
 // the buffer stays allocated until hxm_release_cache().
 constexpr int64_t kSplitKPlaneBytesMax = int64_t(256) << 20;
-hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out, int slot = kWsMain);
+// Slot 2 holds the W8A16 stream-K partial tiles and arrival counters.
+// *grown (when given) says whether the buffer was (re)allocated by this call.
+hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out, int slot = kWsMain,
+                            bool* grown = nullptr);
+// CUs of the current device (cached per device; 0 when it cannot be read).
+int device_cu_count();
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -80,10 +80,27 @@ hxm_status require_device(int* device_out) {
   return HXM_OK;
 }
 
-hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out, int slot) {
+int device_cu_count() {
+  static std::mutex mu;
+  static std::vector<int> cus;
   int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lk(mu);
+  if (static_cast<int>(cus.size()) <= dev) cus.resize(dev + 1, -1);
+  if (cus[dev] < 0) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess
+                   ? n
+                   : 0;
+  }
+  return cus[dev];
+}
+
+hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out, int slot, bool* grown) {
+  int dev = 0;
+  if (grown) *grown = false;
   HXM_HIP_TRY(hipGetDevice(&dev));
-  if (slot != kWsMain && slot != kWsSplitK)
+  if (slot != kWsMain && slot != kWsSplitK && slot != kWsStreamK)
     return fail(HXM_INVALID_ARG, "invalid-argument: workspace slot %d", slot);
   const WsKey key(dev, reinterpret_cast<uintptr_t>(stream), slot);
   std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -118,6 +135,7 @@ hxm_status stream_workspace(hipStream_t stream, size_t bytes, void** out, int sl
                   grow);
     }
     w.bytes = grow;
+    if (grown) *grown = true;
   }
   *out = w.ptr;
   return HXM_OK;

@@ -39,6 +39,7 @@ hxm_gemm_config default_config(int64_t M, int64_t N, int32_t dt);
 int num_w8_kernels();
 hxm_gemm_config w8_kernel_config(int i);
 bool w8_kernel_has_swiglu(int i);
+bool w8_kernel_has_stream_k(int i);
 hxm_gemm_config default_w8_config(int64_t M, int64_t N, bool swiglu);
 hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const int8_t* W,
                        int64_t ldw, const float* scale, void* C, int64_t ldc, int64_t M,
@@ -409,7 +410,11 @@ hxm_status tune_core(const TuneSpec& sp, int32_t reps, hxm_gemm_config* best, ch
     if (measure(cands[i], M, N, K, &samples) != HXM_OK) continue;  // scores inf
     if (have_ref) {
       HXM_HIP_TRY(hipMemsetAsync(bad, 0, sizeof(unsigned), s));
-      if (is_small_gemm_config(cands[i]) != is_small_gemm_config(control))
+      // The direct-load small-output kernel and the stream-K tiles (fp32
+      // partial tiles added across workgroups) sum in another order than the
+      // staged one-workgroup tiles: checked within the float tolerance.
+      if (is_small_gemm_config(cands[i]) != is_small_gemm_config(control) ||
+          (cands[i].split_k == HXM_STREAM_K) != (control.split_k == HXM_STREAM_K))
         count_far_kernel<<<1024, 256, 0, s>>>(static_cast<const uint32_t*>(C),
                                               (ldc * out_eb) / 4, ref, M, row_words,
                                               op == HXM_BF16, bad);
@@ -923,8 +928,20 @@ hxm_status hxm_tune_w8a16(int32_t op, const void* x, int64_t ldx, const int8_t* 
   TuneSpec sp;
   sp.op = op;
   sp.M = M, sp.N = N, sp.K = K;
-  for (int i = 0; i < num_w8_kernels(); ++i)
-    if (!sw || w8_kernel_has_swiglu(i)) sp.cands.push_back(w8_kernel_config(i));
+  // Every compiled tile, and its stream-K form where its tiles leave a
+  // partial round on this device.
+  const int cus = device_cu_count();
+  for (int i = 0; i < num_w8_kernels(); ++i) {
+    if (sw && !w8_kernel_has_swiglu(i)) continue;
+    hxm_gemm_config c = w8_kernel_config(i);
+    sp.cands.push_back(c);
+    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((rows + c.bn - 1) / c.bn);
+    StreamKLayout sk;
+    if (w8_kernel_has_stream_k(i) && stream_k_layout(tiles, (K + c.bk - 1) / c.bk, cus, &sk)) {
+      c.split_k = HXM_STREAM_K;
+      sp.cands.push_back(c);
+    }
+  }
   sort_configs(&sp.cands);
   sp.control = default_w8_config(M, rows, sw);
   sp.canary = sp.cands.front();  // the smallest compiled tile on a 32-row slice

@@ -6,10 +6,11 @@ softmax, rms_norm, layer_norm, prepack_weight, tune_gemm); ``hxm.search``
 mirrors qcom_hexagon_backend/backend/hmx_search.py.  Importing this package
 loads libhxm.so and fails if it has not been built.
 """
-from ._lib import (B_KN, B_NK, BF16, F16, F32, I8, I32, LIB_PATH, W_NK, W_PACKED, GemmConfig,
-                   HxmError, check, last_error, lib, status_string)
+from ._lib import (B_KN, B_NK, BF16, F16, F32, I8, I32, LIB_PATH, STREAM_K, W_NK, W_PACKED,
+                   GemmConfig, HxmError, check, last_error, lib, status_string)
 
-__all__ = ["B_KN", "B_NK", "W_NK", "W_PACKED", "BF16", "F16", "F32", "I8", "I32", "LIB_PATH", "GemmConfig",
+__all__ = ["B_KN", "B_NK", "W_NK", "W_PACKED", "BF16", "F16", "F32", "I8", "I32", "LIB_PATH",
+           "STREAM_K", "GemmConfig",
            "HxmError", "check", "last_error", "lib", "status_string", "version"]
 
 

@@ -23,6 +23,7 @@ F16, BF16, F32, I8, I32 = 1, 2, 3, 4, 5
 B_KN, B_NK = 0, 1
 W_NK, W_PACKED = 0, 1
 OP_W8A16, OP_W8A16_SWIGLU = 16, 17
+STREAM_K = 1024  # HXM_STREAM_K: split_k of a W8A16 config in stream-K form
 IMAGE_GEMM, IMAGE_W8A16 = 0, 1
 
 

@@ -87,8 +87,22 @@ typedef struct hxm_gemm_config {
                                S * M * N * 4 bytes, live in a library-owned
                                per-stream buffer kept until hxm_release_cache();
                                above 256 MiB the call is refused
-                               ("workspace-budget") */
+                               ("workspace-budget").  HXM_STREAM_K: the W8A16
+                               GEMMs' stream-K mode (below) */
 } hxm_gemm_config;
+
+/* split_k of a W8A16 GEMM config (hxm_gemm_w8a16, _swiglu, _residual): when
+ * the tile count is not a multiple of the CU count, the whole rounds run one
+ * tile per workgroup and the remaining tiles' K stages are shared evenly by
+ * one persistent workgroup per CU in the same launch, so the last round
+ * keeps every CU busy.  A tile cut between workgroups is summed from fp32
+ * partial tiles in a fixed order (deterministic, but not bit-identical to
+ * the one-workgroup tile: within the float tolerance).  Its partial tiles
+ * and arrival counters live in a library-owned per-stream buffer (256 KiB
+ * per partial of a 256x256 tile) kept until hxm_release_cache(); above
+ * 256 MiB the call is refused ("workspace-budget").  With whole rounds the
+ * call runs as split_k = 1. */
+#define HXM_STREAM_K 1024
 
 /* ---- status / library ------------------------------------------------- */
 

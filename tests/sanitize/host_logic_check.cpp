@@ -3,7 +3,9 @@
 // tests/test_host_sanitize.py.  Every function is driven with boundary values
 // and a seeded random sweep and compared with a restatement in 128-bit
 // integers; the tuning-cache entry parser is also fed malformed and random
-// lines.  Prints "host_logic ok" and exits 0 when every check holds.
+// lines; stream-K layouts are walked segment by segment as the kernel walks
+// them.  Prints "host_logic ok" and exits 0 when every check holds.
+#include <algorithm>
 #include <climits>
 #include <cstring>
 #include <random>
@@ -149,6 +151,65 @@ int main() {
     std::fprintf(stderr, "%d failure(s)\n", failures);
     return 1;
   }
+  // Stream-K layouts: every (tile, stage) of the launch is computed by
+  // exactly one workgroup, with the segment walk the kernel runs
+  // (gemm_kernel.h, the SK loop), each segment's index below its tile's
+  // segment count, which is at most maxseg, every partial-tile slot index in
+  // range, and the data-parallel tiles the whole rounds.
+  for (int it = 0; it < 3000; ++it) {
+    const int64_t cus = (it % 3 == 0) ? 256 : 1 + static_cast<int64_t>(rng() % 300);
+    const int64_t ntiles = 1 + static_cast<int64_t>(rng() % (it % 5 == 0 ? 2000 : 700));
+    const int64_t KT = 1 + static_cast<int64_t>(rng() % (it % 7 == 0 ? 700 : 70));
+    hxm::StreamKLayout L;
+    const bool ok = hxm::stream_k_layout(ntiles, KT, cus, &L);
+    CHECK(ok == (ntiles % cus != 0), "stream_k_layout(%lld,%lld,%lld) -> %d",
+          (long long)ntiles, (long long)KT, (long long)cus, ok);
+    if (!ok) continue;
+    CHECK(L.dp + L.tiles == ntiles && L.dp % cus == 0 && L.tiles < cus && L.groups == cus,
+          "stream-K split of %lld tiles", (long long)ntiles);
+    CHECK(!L.xcd || (ntiles % 8 == 0 && L.dp % 8 == 0 && cus % 8 == 0), "xcd streams");
+    const int64_t streams = L.xcd ? 8 : 1;
+    const int64_t per = L.tiles / streams, gper = cus / streams;
+    CHECK(L.iters >= 1 && per * streams == L.tiles && gper * L.iters >= per * KT,
+          "stream coverage");
+    std::vector<int> hits(static_cast<size_t>(L.tiles * KT), 0);
+    std::vector<int> segs(static_cast<size_t>(L.tiles), 0);
+    for (int64_t b = 0; b < cus; ++b) {             // the stream-K workgroups
+      const int64_t x = L.xcd ? b & 7 : 0, w = L.xcd ? b >> 3 : b;
+      int64_t i = w * L.iters;
+      const int64_t end = std::min<int64_t>(per * KT, (w + 1) * L.iters);
+      while (i < end) {
+        const int64_t st = i / KT, k0 = i % KT, k1 = std::min<int64_t>(KT, k0 + (end - i));
+        const int64_t tfirst = st * KT, seg0 = tfirst / L.iters;
+        const int64_t nseg = (tfirst + KT - 1) / L.iters - seg0 + 1, seg = w - seg0;
+        const int64_t slot = x * per + st;
+        CHECK(seg >= 0 && seg < nseg && nseg <= L.maxseg && slot >= 0 && slot < L.tiles,
+              "segment %lld of %lld (maxseg %d), slot %lld", (long long)seg, (long long)nseg,
+              L.maxseg, (long long)slot);
+        if (slot < 0 || slot >= L.tiles) break;
+        for (int64_t k = k0; k < k1; ++k) ++hits[static_cast<size_t>(slot * KT + k)];
+        ++segs[static_cast<size_t>(slot)];
+        CHECK(k1 > k0, "empty segment");
+        i += k1 - k0;
+      }
+    }
+    for (size_t q = 0; q < hits.size(); ++q)
+      CHECK(hits[q] == 1, "stage %zu computed %d times (ntiles %lld KT %lld cus %lld)", q, hits[q],
+            (long long)ntiles, (long long)KT, (long long)cus);
+    int64_t most = 0;
+    for (int v : segs) most = std::max<int64_t>(most, v);
+    CHECK(most == L.maxseg, "maxseg %d, most segments %lld", L.maxseg, (long long)most);
+  }
+  hxm::StreamKLayout L0;
+  CHECK(!hxm::stream_k_layout(0, 4, 256, &L0) && !hxm::stream_k_layout(10, 0, 256, &L0) &&
+            !hxm::stream_k_layout(10, 4, 0, &L0) && !hxm::stream_k_layout(512, 4, 256, &L0) &&
+            !hxm::stream_k_layout(10, 4, 256, nullptr) &&
+            !hxm::stream_k_layout(INT64_MAX, 4, 256, &L0),
+        "stream_k_layout refusals");
+  CHECK(hxm::stream_k_layout(688, 64, 256, &L0) && L0.dp == 512 && L0.tiles == 176 &&
+            L0.xcd == 1 && L0.iters == 44 && L0.maxseg == 3,
+        "the benchmark's gate/up layout");
+
   std::printf("host_logic ok\n");
   return 0;
 }

@@ -1,6 +1,8 @@
 """libhxm's host-only arithmetic under AddressSanitizer and
 UndefinedBehaviorSanitizer on the CPU: the guards that keep 32-bit offsets
-and launch grids in range, the K split and the tuning-cache entry parser
+and launch grids in range, the K split, the stream-K layout (every stage of
+every tile computed once by the segment walk the kernel runs) and the
+tuning-cache entry parser
 (hexagon-mlir_amd/csrc/host_logic.h, the code the library itself runs),
 driven by tests/sanitize/host_logic_check.cpp with boundary values, a seeded
 random sweep against 128-bit restatements, and malformed cache lines."""

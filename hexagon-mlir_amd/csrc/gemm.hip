@@ -115,7 +115,8 @@ static gemm_fn part_fn(const gemm_fn (*const parts[kGemmParts])[E], int i, int e
 }
 static const gemm_fn (*const kI8Parts[kGemmParts])[2] = {kI8Fns_p0, kI8Fns_p1, kI8Fns_p2};
 static const gemm_fn (*const kF16Parts[kGemmParts])[2] = {kF16Fns_p0, kF16Fns_p1, kF16Fns_p2};
-static const gemm_fn (*const kW8Parts[kGemmParts])[6] = {kW8Fns_p0, kW8Fns_p1, kW8Fns_p2};
+static const gemm_fn (*const kW8Parts[kGemmParts])[3] = {kW8Fns_p0, kW8Fns_p1, kW8Fns_p2};
+static const gemm_fn* const kW8SkParts[kGemmParts] = {kW8SkFns_p0, kW8SkFns_p1, kW8SkFns_p2};
 
 static int elem_bytes(int32_t dt) { return dt == HXM_I8 ? 1 : 2; }
 
@@ -590,8 +591,10 @@ hxm_gemm_config w8_kernel_config(int i) {
   return c;
 }
 bool w8_kernel_has_swiglu(int i) { return part_fn(kW8Parts, i, 1) != nullptr; }
-// Entry i has a stream-K form (split_k = HXM_STREAM_K).
-bool w8_kernel_has_stream_k(int i) { return part_fn(kW8Parts, i, 3) != nullptr; }
+// Entry i has a stream-K form (split_k = HXM_STREAM_K): entry 0, compiled
+// in gemm_w8sk.hip, part e holding epilogue e (kEpiW8, kEpiSwiglu, kEpiW8Res).
+bool w8_kernel_has_stream_k(int i) { return i == 0; }
+static gemm_fn w8_stream_k_fn(int e) { return kW8SkParts[e][e]; }
 
 static const KernelEntry* find_w8_kernel(const hxm_gemm_config& c, bool swiglu) {
   for (int i = 0; i < kNumW8Kernels; ++i) {
@@ -783,9 +786,10 @@ hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const in
     g.sk_part = reinterpret_cast<float*>(static_cast<char*>(ws) + stream_k_counter_bytes(sk));
     groups = sk.dp + sk.groups;
   }
-  const int fe = (sw ? 1 : epi == kEpiW8Res ? 2 : 0) +
-                 (plan.config.split_k == HXM_STREAM_K ? 3 : 0);
-  hipLaunchKernelGGL(part_fn(kW8Parts, wi, fe), dim3(static_cast<unsigned>(groups)),
+  const int fe = sw ? 1 : epi == kEpiW8Res ? 2 : 0;
+  hipLaunchKernelGGL(plan.config.split_k == HXM_STREAM_K ? w8_stream_k_fn(fe)
+                                                          : part_fn(kW8Parts, wi, fe),
+                     dim3(static_cast<unsigned>(groups)),
                      dim3(e->threads), 0, stream, g);
   if ((st = check_launch("w8a16 gemm kernel")) != HXM_OK) return st;
   return ok();

@@ -1325,8 +1325,8 @@ constexpr int config_index(const ConfigKey (&keys)[N], int bm, int bn, int bkb, 
 #define HXM_DECLARE_PART_TABLES(P)            \
   extern const gemm_fn kI8Fns_p##P[][2];  /* {kEpiI32, kEpiDequant} */ \
   extern const gemm_fn kF16Fns_p##P[][2]; /* {f16, bf16} operands, kEpiFloat */ \
-  extern const gemm_fn kW8Fns_p##P[][6];  /* {kEpiW8, kEpiSwiglu (null unless TN == 128), kEpiW8Res}, \
-                                              then the same three in stream-K form */
+  extern const gemm_fn kW8Fns_p##P[][3];  /* {kEpiW8, kEpiSwiglu (null unless TN == 128), kEpiW8Res} */ \
+  extern const gemm_fn kW8SkFns_p##P[3];  /* stream-K form of entry 0: part p holds epilogue p */
 HXM_DECLARE_PART_TABLES(0)
 HXM_DECLARE_PART_TABLES(1)
 HXM_DECLARE_PART_TABLES(2)

@@ -617,7 +617,15 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g0) {
               read(R, cb ^ 1, nxt, std::integral_constant<int, 0>{});
           }
         });
-        constexpr int i = BQ ? sl % FM : sl / FN, j = BQ ? sl / FM : sl % FN;
+        // A snake over the wave's blocks: rows (columns, for an int8 B) in
+        // turn, every other one walked backwards, so each MFMA shares one
+        // operand with the one before it.  Operand changes cost power: an
+        // MFMA-only loop on random operands ran 0.7% faster in this order
+        // than in the plain row order (int8 and f16 alike).  Every fragment
+        // is still first needed at the slot the plain order gives it.
+        constexpr int i0 = BQ ? sl % FM : sl / FN, j0 = BQ ? sl / FM : sl % FN;
+        constexpr int i = BQ && (j0 & 1) ? FM - 1 - i0 : i0;
+        constexpr int j = !BQ && (i0 & 1) ? FN - 1 - j0 : j0;
         acc[i][j] = Mfma<T>::run(bf[cb][j], af[cb][i], acc[i][j]);
         cvt_slot(KSI, SI);
         __builtin_amdgcn_sched_barrier(0);

@@ -80,9 +80,10 @@ __global__ __launch_bounds__(kProbeThreads) void stream_read_kernel(
 // (16 bytes per lane each) from the operand bytes -- wave w reads A bytes
 // [8 KiB * w, +8 KiB) and the same window of B, wrapped at the buffers' ends
 // -- and then runs `steps` rounds of 2 x 16 MFMAs over a 4 x 4 grid of 32x32
-// accumulator blocks, the sets alternating, so every instruction sees other
-// data than the one before (the operand toggling, and so the power, of a
-// GEMM's k-steps).  MODE: 0 int8 x int8 (v_mfma_i32_32x32x32_i8), 1 f16,
+// accumulator blocks, the sets alternating and the blocks in the GEMM
+// kernels' snake order, so every instruction shares one operand with the one
+// before it and no more (the operand toggling, and so the power, of a GEMM's
+// k-steps).  MODE: 0 int8 x int8 (v_mfma_i32_32x32x32_i8), 1 f16,
 // 2 bf16 (v_mfma_f32_32x32x16_*), 3 f16 x int8 (B bytes converted exactly to
 // f16 once, as the W8A16 kernels convert theirs).  Every accumulator is
 // folded into one word per lane, stored only when it equals `never`, so the
@@ -118,7 +119,8 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(const uint8_t* __restri
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int jj = 0; jj < 4; ++jj) {
+          const int j = (i & 1) ? 3 - jj : jj;  // the GEMM kernels' snake order
           if constexpr (MODE == 0)
             acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[s][j], fa[s][i], acc[i][j], 0, 0, 0);
           else if constexpr (MODE == 2)

@@ -646,14 +646,16 @@ __global__ __launch_bounds__(256) void swiglu_pack_kernel(
     out_scale[r] = ch < I ? (up ? su : sg)[ch] : 0.0f;
 }
 
-// Stream-K buffer of a W8A16 launch: the arrival counters (one per
-// stream-K tile, padded to 256 bytes) and then sk.tiles * sk.maxseg fp32
-// partial tiles of BM x BN.
-static int64_t stream_k_counter_bytes(const StreamKLayout& sk) {
-  return (static_cast<int64_t>(sk.tiles) * 4 + 255) / 256 * 256;
-}
+// Stream-K buffer of a W8A16 launch: a block of arrival counters, one per
+// stream-K tile (a launch has fewer stream-K tiles than the device has CUs),
+// then sk.tiles * sk.maxseg fp32 partial tiles of BM x BN.  The counter
+// block has the same place and size for every shape: it is zeroed whenever
+// the buffer is allocated, and every launch leaves the counters it used at
+// zero, so a later shape with more stream-K tiles never finds a counter in
+// bytes that an earlier shape used for partial tiles.
+constexpr int64_t kStreamKCounterBytes = 4096;
 static int64_t stream_k_bytes(const KernelEntry& e, const StreamKLayout& sk) {
-  return stream_k_counter_bytes(sk) +
+  return kStreamKCounterBytes +
          static_cast<int64_t>(sk.tiles) * sk.maxseg * e.cfg.bm * e.cfg.bn * 4;
 }
 
@@ -692,7 +694,7 @@ hxm_status plan_gemm_w8(int32_t op, bool sw, int64_t M, int64_t N, int64_t n_out
     p->threads = e->threads;
     p->tiles = ((M + e->cfg.bm - 1) / e->cfg.bm) * ((N + e->cfg.bn - 1) / e->cfg.bn);
     p->lds_bytes = kernel_lds_bytes(*e, true, false);
-    int64_t groups = p->tiles;
+    int64_t groups = p->tiles, sk_tiles = 0;
     if (c.split_k == HXM_STREAM_K) {
       // Stream-K when the tiles leave a partial round; whole rounds run as
       // split_k = 1.  The plan records the mode, the partial-tile slots (as
@@ -704,12 +706,17 @@ hxm_status plan_gemm_w8(int32_t op, bool sw, int64_t M, int64_t N, int64_t n_out
         p->k_slices = sk.maxseg;
         p->workspace_bytes = stream_k_bytes(*e, sk);
         groups = sk.dp + sk.groups;
+        sk_tiles = sk.tiles;
       }
     }
     if (p->workspace_bytes > kSplitKPlaneBytesMax) {
       snprintf(why, sizeof(why),
                "stream-K needs %lld bytes of fp32 partial tiles, above the %lld-byte limit",
                (long long)p->workspace_bytes, (long long)kSplitKPlaneBytesMax);
+      st = refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_WORKSPACE_BUDGET, why);
+    } else if (sk_tiles > kStreamKCounterBytes / 4) {
+      snprintf(why, sizeof(why), "stream-K with %lld partial-round tiles needs more than %lld "
+               "arrival counters", (long long)sk_tiles, (long long)(kStreamKCounterBytes / 4));
       st = refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_WORKSPACE_BUDGET, why);
     } else if (!grid_fits(groups, e->threads)) {
       snprintf(why, sizeof(why), "%lld workgroups of %d threads exceed the launch limit",
@@ -771,11 +778,10 @@ hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const in
     if ((st = stream_workspace(stream, static_cast<size_t>(stream_k_bytes(*e, sk)), &ws,
                                kWsStreamK, &grown)) != HXM_OK)
       return st;
-    // A new buffer's counters start at zero; every launch leaves them there
-    // (the last workgroup at a tile resets its counter).  Growth is refused
-    // under graph capture, so this fill is never captured.
-    if (grown) HXM_HIP_TRY(hipMemsetAsync(ws, 0, static_cast<size_t>(stream_k_counter_bytes(sk)),
-                                          stream));
+    // A new buffer's counter block starts at zero; every launch leaves it
+    // there (the last workgroup at a tile resets its counter).  Growth is
+    // refused under graph capture, so this fill is never captured.
+    if (grown) HXM_HIP_TRY(hipMemsetAsync(ws, 0, static_cast<size_t>(kStreamKCounterBytes), stream));
     g.sk_first = sk.dp;
     g.sk_groups = sk.groups;
     g.sk_tiles = sk.tiles;
@@ -783,7 +789,7 @@ hxm_status run_gemm_w8(int epi, int32_t op, const void* x, int64_t ldx, const in
     g.sk_maxseg = sk.maxseg;
     g.sk_xcd = sk.xcd;
     g.sk_count = static_cast<uint32_t*>(ws);
-    g.sk_part = reinterpret_cast<float*>(static_cast<char*>(ws) + stream_k_counter_bytes(sk));
+    g.sk_part = reinterpret_cast<float*>(static_cast<char*>(ws) + kStreamKCounterBytes);
     groups = sk.dp + sk.groups;
   }
   const int fe = sw ? 1 : epi == kEpiW8Res ? 2 : 0;

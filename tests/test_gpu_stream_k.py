@@ -11,7 +11,8 @@ the arrival counters are left at zero for the next launch); the three
 epilogues (per-channel scale, SwiGLU, residual); streams per XCD and the
 global stream; K that ends inside a stage; ragged tiles; shapes with fewer
 tiles than CUs (every tile cut) and the benchmark's partial third round; the
-plan record; and replays of a captured HIP graph."""
+plan record; a shape with more arrival counters reusing the buffer an
+earlier shape sized; and replays of a captured HIP graph."""
 import numpy as np
 import pytest
 import torch
@@ -116,6 +117,37 @@ def test_stream_k_swiglu(dev, M, I, K):
     ref = orc.swiglu_gateup(bits(x)[rows], Wg.numpy(), Wu.numpy(), sg.numpy(), su.numpy())
     np.testing.assert_allclose(f32(bits(h_sk)[rows]), f32(ref), **TOL)
     assert torch.equal(ops.gemm_w8a16_swiglu(xd, Wgu, sgu, I, config=tile + (SK,)), h_sk)
+
+
+def test_stream_k_counters_zero_across_shapes(dev):
+    """A stream's stream-K buffer is reused by every shape that fits it.  The
+    first shape (256x8448x256: 33 partial-round tiles cut in up to 4
+    segments, a 34.6 MB buffer) sizes the buffer; the second (1280x3328x256:
+    65 tiles of up to 2 segments, 34.1 MB) fits in it and has more arrival
+    counters than the first.  Its counters must still start at zero, not
+    in bytes the first shape used for partial tiles: every tile of the
+    second call is written and equals the one-workgroup tiles' result."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus != 256:
+        pytest.skip(f"the shape pair is chosen for 256 CUs (this device has {cus})")
+    tile = (256, 256, 64, 2, 2, 3)
+    stream = torch.cuda.Stream()
+    assert hxm.lib.hxm_release_cache() == 0  # no stream-K buffer yet
+    outs = []
+    for (M, N, K, seed) in [(256, 8448, 256, 11), (1280, 3328, 256, 12)]:
+        print(f"stream-K counters M={M} N={N} K={K}", flush=True)
+        x, W, s = w8_operands(M, N, K, seed)
+        xd, Wd, sd = x.to(dev), W.to(dev), s.to(dev)
+        y = torch.full((M, N), -7.0, dtype=torch.float16, device=dev)
+        with torch.cuda.stream(stream):
+            ops.gemm_w8a16(xd, Wd, sd, out=y, config=tile + (SK,))
+            p = ops.last_plan()
+        torch.cuda.synchronize()
+        assert p["config"][6] == SK
+        outs.append((p["workspace_bytes"], p["k_slices"]))
+        want = ops.gemm_w8a16(xd, Wd, sd, config=tile + (1,))
+        np.testing.assert_allclose(y.float().cpu().numpy(), want.float().cpu().numpy(), **TOL)
+    assert outs[1][0] <= outs[0][0] and (outs[0][1], outs[1][1]) == (4, 2), outs
 
 
 def test_stream_k_refused_where_not_compiled(dev):

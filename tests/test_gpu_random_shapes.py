@@ -7,6 +7,9 @@ the same cases and a failure names its case.
   columns past N must stay untouched);
 * f16 / bf16 matmul, W8A16 GEMM, GEMV (packed and plain) and the fused
   SwiGLU gate/up GEMM within rtol 1e-2 / atol 1e-3;
+* the stream-K form of the W8A16 GEMMs on random shapes, epilogues and
+  output strides, one stream's buffer reused across them: within the same
+  tolerance of the one-workgroup tiles and of the oracle, deterministic;
 * softmax / RMSNorm / LayerNorm on f16, bf16 and f32 rows of every kernel
   shape (register, split, unaligned, streaming) with offset, large, tiny and
   N(0,1) values; f32 rows are held to rtol 1e-4 / atol 1e-5.
@@ -165,3 +168,69 @@ def test_random_rows_with_value_patterns(dev):
         y = ops.layer_norm(x.to(dev), (cols,), w.to(dev), b.to(dev), eps=1e-5)
         np.testing.assert_allclose(y.float().cpu().numpy(), orc.to_f32(ry, name), **tol,
                                    err_msg=case + " layernorm")
+
+
+def test_random_stream_k_w8a16(dev):
+    """The stream-K form (split_k = HXM_STREAM_K) of the gate/up tile on
+    random shapes, epilogues and output strides, all on one stream so its
+    stream-K buffer is reused by shapes of every size: within the float
+    tolerance of the one-workgroup tiles and of the oracle (sampled rows),
+    bit-identical on a repeated call, and nothing written past N."""
+    rng = random.Random(777)
+    tile = (256, 256, 64, 2, 2, 3, hxm.STREAM_K)
+    plain = tile[:6] + (1,)
+    stream = torch.cuda.Stream()
+    streamed = 0
+    for it in range(16):
+        M, N = rng.randint(1, 1500), rng.randint(1, 6000)
+        K = 16 * rng.randint(1, 200)
+        epi = rng.choice(["w8", "residual", "swiglu"])
+        pad = rng.choice([0, 8, 64])
+        case = f"case {it}: {M}x{N}x{K} {epi} ldc+{pad}"
+        print(case, flush=True)
+        g = torch.Generator().manual_seed(7000 + it)
+        x = torch.randn(M, K, generator=g).half()
+        xd = x.to(dev)
+        rows = np.unique(np.linspace(0, M - 1, 8).astype(int))
+        with torch.cuda.stream(stream):
+            if epi == "swiglu":
+                I = N
+                Wg = torch.randint(-127, 128, (I, K), generator=g, dtype=torch.int8)
+                Wu = torch.randint(-127, 128, (I, K), generator=g, dtype=torch.int8)
+                sg = torch.rand(I, generator=g) * 0.004 + 0.001
+                su = torch.rand(I, generator=g) * 0.004 + 0.001
+                Wgu, sgu = ops.swiglu_pack(Wg.to(dev), Wu.to(dev), sg.to(dev), su.to(dev))
+                buf = torch.full((M, I + pad), -7.0, dtype=torch.float16, device=dev)
+                run = lambda cfg, o: ops.gemm_w8a16_swiglu(xd, Wgu, sgu, I, out=o, config=cfg)
+                ref = orc.swiglu_gateup(bits(x)[rows], Wg.numpy(), Wu.numpy(), sg.numpy(),
+                                        su.numpy())
+            else:
+                W = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+                s = (torch.rand(N, generator=g) * 0.019 + 0.001).half().float()
+                Wd, sd = W.to(dev), s.to(dev)
+                buf = torch.full((M, N + pad), -7.0, dtype=torch.float16, device=dev)
+                if epi == "residual":
+                    r = torch.randn(M, N, generator=g).half()
+                    rd = r.to(dev)
+                    run = lambda cfg, o: ops.gemm_w8a16(xd, Wd, sd, out=o, residual=rd, config=cfg)
+                    ref = orc.gemm_w8a16_residual(bits(x)[rows], W.numpy(), s.numpy(),
+                                                  bits(r)[rows])
+                else:
+                    run = lambda cfg, o: ops.gemm_w8a16(xd, Wd, sd, out=o, config=cfg)
+                    ref = orc.gemm_w8a16(bits(x)[rows], W.numpy(), s.numpy())
+            n_out = buf.shape[1] - pad
+            run(tile, buf[:, :n_out])
+            streamed += ops.last_plan()["config"][6] == hxm.STREAM_K
+            want = torch.empty(M, n_out, dtype=torch.float16, device=dev)
+            run(plain, want)
+            again = torch.empty(M, n_out, dtype=torch.float16, device=dev)
+            run(tile, again)
+        torch.cuda.synchronize()
+        got = buf[:, :n_out]
+        np.testing.assert_allclose(got.float().cpu().numpy(), want.float().cpu().numpy(), **TOL,
+                                   err_msg=case + " vs one-workgroup tiles")
+        np.testing.assert_allclose(orc.f16_bits_to_f32(bits(got)[rows]), orc.f16_bits_to_f32(ref),
+                                   **TOL, err_msg=case + " vs oracle")
+        assert torch.equal(again, got), case + " repeat"
+        assert bool((buf[:, n_out:] == -7.0).all()), case + " wrote past N"
+    assert streamed >= 12, f"only {streamed} of 16 cases ran the stream-K form"

@@ -190,6 +190,12 @@ hxm_status hxm_resident_weight(const void* src, int64_t ld, int64_t rows, int64_
     } else {
       st = hxm_prepack_weight(src, ld, img.ptr, rows, rows, cols, src_dtype, stream);
     }
+    // The image is built before it enters the cache: a hit on another
+    // thread's stream may read it at once, with nothing ordering that read
+    // after this stream's pack kernel.
+    hipError_t e = hipSuccess;
+    if (st == HXM_OK && (e = hipStreamSynchronize(s)) != hipSuccess)
+      st = fail(HXM_HIP_ERROR, "hip-error: resident image build: %s", hipGetErrorString(e));
     if (st != HXM_OK) {
       (void)hipFree(img.ptr);
       return st;

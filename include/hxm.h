@@ -26,6 +26,15 @@
  *     capture grows it (it is kept until hxm_release_cache).
  *   - numerics: fp16/bf16 products accumulate in fp32 and are rounded once
  *     to the output dtype; int8 products accumulate exactly in int32.
+ *   - host threads: entries may run at the same time on several host
+ *     threads when each uses its own stream (workspaces are per stream; the
+ *     device table, the tuning cache and the resident images are locked).
+ *     Calls on one stream must not overlap in time: a call may launch
+ *     several kernels that share that stream's workspace, and another
+ *     thread's launches in between would reuse it.  hxm_release_cache must
+ *     not overlap any other call on its device (it frees buffers another
+ *     call may have been handed), and hxm_gemm_i8_noalloc calls share one
+ *     scratch array per device.
  *
  * Reference interfaces replaced (paths relative to the reference root):
  *   the compiled Triton kernel symbol launched by
@@ -327,7 +336,9 @@ typedef enum hxm_image_kind {
  * cols) != NULL are the caller's contract: a mismatch is refused
  * ("unsupported-dtype" / "invalid-argument") before anything is packed.
  * *image_dtype receives the image dtype.  Synchronises `stream` once (the
- * hash is read back).  Images stay valid until hxm_release_cache(). */
+ * hash is read back), and once more when it builds a new image, so an
+ * image is complete before any thread or stream can be handed it.  Images
+ * stay valid until hxm_release_cache(). */
 hxm_status hxm_resident_weight(const void* src, int64_t ld, int64_t rows,
                                int64_t cols, int32_t src_dtype,
                                int32_t expect_dtype, const int64_t* expect_shape,

@@ -173,14 +173,6 @@ hxm_status build_id(uint64_t* out) {
   return HXM_OK;
 }
 
-int device_cus() {
-  int dev = 0;
-  hipDeviceProp_t prop;
-  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
-    return 0;
-  return prop.multiProcessorCount;
-}
-
 bool same_config(const hxm_gemm_config& a, const hxm_gemm_config& b) {
   return a.bm == b.bm && a.bn == b.bn && a.bk == b.bk && a.waves_m == b.waves_m &&
          a.waves_n == b.waves_n && a.stages == b.stages && a.split_k == b.split_k;
@@ -728,7 +720,7 @@ hxm_status hxm_tune_cache_save(const char* path) {
   uint64_t bid = 0;
   hxm_status st = build_id(&bid);
   if (st != HXM_OK) return st;
-  const int cus = device_cus();
+  const int cus = device_cu_count();
   const std::string tmp = std::string(path) + ".tmp";
   FILE* f = std::fopen(tmp.c_str(), "w");
   if (!f) return fail(HXM_INVALID_ARG, "invalid-argument: cannot write %s", tmp.c_str());
@@ -786,7 +778,7 @@ hxm_status hxm_tune_cache_load(const char* path, int32_t* loaded) {
     std::fclose(f);
     return st;
   }
-  const int cus = device_cus();
+  const int cus = device_cu_count();
   if (fcus != cus) {
     std::fclose(f);
     return fail(HXM_INVALID_ARG,
@@ -862,7 +854,7 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
     // one stage per slice).  The best split is shape-dependent (measured,
     // 256x256 tile: 512x512x16384 best at 16, 1024x1024x4096 at 4).
     const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
-    const int cus = device_cus();
+    const int cus = device_cu_count();
     if (op == HXM_I8 && cus > 0 && tiles * 2 <= cus) {
       for (int32_t s = 2; s <= 16 && tiles * s <= 2 * cus && (K + c.bk - 1) / c.bk >= s &&
                           s * M * N * 4 <= kSplitKPlaneBytesMax;

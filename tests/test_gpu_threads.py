@@ -70,7 +70,9 @@ def test_threads_on_own_streams_match_single_thread(dev):
 
     print("4 threads x 3 reps", flush=True)
     hxm.lib.hxm_release_cache()                     # workspaces grow while threads run
-    threads = [threading.Thread(target=worker, args=(t,)) for t in range(4)]
+    # Daemon threads: a worker stuck in a call fails the test below without
+    # keeping the test process alive after it.
+    threads = [threading.Thread(target=worker, args=(t,), daemon=True) for t in range(4)]
     for th in threads:
         th.start()
     for th in threads:

@@ -139,6 +139,35 @@ def test_gemm_i8_accumulate_and_strides(dev):
     assert np.array_equal(got[:, N:], C0[:, N:].numpy()), "wrote outside the output view"
 
 
+def test_gemm_i8_int32_is_modular(dev):
+    """int32 results wrap in two's complement, as the oracle's int8
+    linalg.matmul does: C += A.B past 2^31 in the epilogue (both B layouts)
+    and in the split-K reduce, and the MFMA's own int32 accumulator past 2^31
+    (K = 131088 products of -128 * -128 = 16384 sum to 2^31 + 262144), alone
+    and split in two (each plane below 2^31, the sum wrapping in the reduce)."""
+    A = torch.full((64, 1024), 127, dtype=torch.int8)
+    B = torch.full((1024, 64), 127, dtype=torch.int8)
+    C0 = torch.full((64, 64), 2 ** 31 - 1000000, dtype=torch.int64).to(torch.int32)
+    ref = orc.gemm_i8(A.numpy(), B.numpy(), C=C0.numpy(), accumulate=True)
+    assert (ref < 0).all()                      # the sum did wrap
+    Ad, Bd = A.to(dev), B.to(dev)
+    for lay, Bl in (("kn", Bd), ("nk", ops.prepack_weight(Bd))):
+        for cfg in (None, hxm.GemmConfig(64, 64, 128, 2, 2, 2, 4)):
+            C = C0.to(dev)
+            ops.gemm_i8(Ad, Bl, out=C, b_layout=lay, accumulate=True, config=cfg)
+            assert np.array_equal(C.cpu().numpy(), ref), f"{lay} {cfg}"
+    K = 131088
+    print(f"int8 accumulator wrap, K={K}", flush=True)
+    A = torch.full((32, K), -128, dtype=torch.int8)
+    B = torch.full((K, 32), -128, dtype=torch.int8)
+    ref = orc.gemm_i8(A.numpy(), B.numpy())
+    assert (ref == K * 16384 - 2 ** 32).all()
+    Ad, Bp = A.to(dev), ops.prepack_weight(B.to(dev))
+    for cfg in (None, hxm.GemmConfig(32, 32, 128, 1, 1, 2, 2)):
+        got = ops.gemm_i8(Ad, Bp, b_layout="nk", config=cfg)
+        assert np.array_equal(got.cpu().numpy(), ref), f"K={K} {cfg}"
+
+
 def test_gemm_i8_4096_cube(dev):
     """The int8 4096^3 benchmark shape: int32 exact and the dequant epilogue."""
     n = 4096

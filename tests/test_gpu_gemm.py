@@ -168,6 +168,30 @@ def test_gemm_i8_int32_is_modular(dev):
         assert np.array_equal(got.cpu().numpy(), ref), f"K={K} {cfg}"
 
 
+def test_matmul_f16_overflow_and_subnormal_outputs(dev):
+    """The fp32 -> f16 rounding at the edges of f16: sums past 65504 round to
+    +-inf, and sums below the smallest normal (2^-14) come out as the
+    subnormal the oracle's RNE conversion gives, bit for bit (every product
+    and partial sum here is exact in fp32)."""
+    M, N, K = 64, 64, 256                               # K <= 256: the small kernel too
+    A = torch.full((M, K), 16.0).half()                 # 256 * 256 = 65536 -> +inf
+    B = torch.full((K, N), 16.0).half()
+    B[:, 1] = -16.0                                      # -> -inf
+    tiny = torch.full((M, K), 2.0 ** -12).half()
+    Bt = torch.full((K, N), 2.0 ** -12).half()           # 256 * 2^-24 = 2^-16
+    Bt[:, 1] = 2.0 ** -15                                # 2^-19 = 32 subnormal ulps
+    Bt[:, 2] = 3 * 2.0 ** -20                            # exactly 3 ulps
+    Bt[:, 3] = 3 * 2.0 ** -21                            # 1.5 ulps: the tie rounds to 2
+    for a, b in ((A, B), (tiny, Bt)):
+        ref = orc.matmul(bits(a), bits(b))
+        for cfg in (None, (256, 256, 64, 2, 2, 2, 1), (16, 16, 32, 1, 1, 0, 1)):
+            got = ops.matmul(a.to(dev), b.to(dev), config=cfg)
+            assert np.array_equal(bits(got), ref), cfg
+    assert np.isinf(orc.f16_bits_to_f32(orc.matmul(bits(A), bits(B)))).all()
+    sub = orc.matmul(bits(tiny), bits(Bt))
+    assert (sub[:, :4] == [256, 32, 3, 2]).all()         # f16 bit patterns of the subnormals
+
+
 def test_gemm_i8_4096_cube(dev):
     """The int8 4096^3 benchmark shape: int32 exact and the dequant epilogue."""
     n = 4096

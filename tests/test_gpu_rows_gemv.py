@@ -253,3 +253,22 @@ def test_gemv_golden_and_exact_small_ints(dev, golden, packed):
     for m in (1, 4):
         y = ops.gemv_w8a16(x[:m].to(dev), Wd, torch.ones(2).half().to(dev)).cpu()
         assert torch.equal(y.float(), W[:, :m].t().float())
+
+
+def test_gemv_kernels_agree_bit_for_bit(dev):
+    """Every GEMV kernel sums a row's products in one grouping: wave w of the
+    8 takes the slabs w, w + 8, ..., two MFMAs per slab in K order, and the
+    waves' partials are added in wave order.  So row 0 comes out the same
+    bits from the one-chunk kernel (M = 1, packed and plain weights) and the
+    pipelined kernels (M = 4 with one channel group per workgroup, M = 16
+    with three), at the benchmark's N = 11008, K = 4096."""
+    g = torch.Generator().manual_seed(17)
+    N, K = 11008, 4096
+    W = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+    sc = (torch.rand(N, generator=g) * 0.019 + 0.001).half().to(dev)
+    x = torch.randn(16, K, generator=g).half().to(dev)
+    Wp = ops.prepack_w8a16(W)
+    y1 = ops.gemv_w8a16(x[:1], Wp, sc)
+    assert torch.equal(ops.gemv_w8a16(x[:1], W, sc), y1)           # plain layout
+    for M in (4, 16):
+        assert torch.equal(ops.gemv_w8a16(x[:M], Wp, sc)[:1], y1), f"M={M}"

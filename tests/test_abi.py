@@ -126,6 +126,12 @@ def _span_refusals():
             assert st == _lib.HXM_NO_DEVICE
 
 
+@pytest.mark.skipif("_gpu_present()", reason="a GPU box counts its gfx950 devices; "
+                    "test_gpu_ops_contract.py covers it there")
+def test_device_count_is_zero_without_a_gpu():
+    assert hxm.lib.hxm_device_count() == 0
+
+
 @pytest.mark.skipif("_gpu_present()", reason="stand-in addresses are for machines without a GPU; "
                     "test_refusals_with_device_buffers covers a GPU box")
 def test_refusals_happen_before_launch():

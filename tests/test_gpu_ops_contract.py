@@ -91,3 +91,9 @@ def test_gemv_column_split_writes_through_ldy(dev, M, packed):
         ops.gemv_w8a16(xd, Wr, scd[r * n:(r + 1) * n], out=y[:, r * n:(r + 1) * n], N=n)
     ref = orc.f16_bits_to_f32(orc.gemv_w8a16(bits(x), W.numpy(), bits(sc)))
     np.testing.assert_allclose(y.float().cpu().numpy(), ref, rtol=1e-2, atol=1e-3)
+
+
+def test_device_count_sees_the_gfx950(dev):
+    """hxm_device_count counts the visible gfx950 devices: the box's MI355X."""
+    import hxm
+    assert hxm.lib.hxm_device_count() == torch.cuda.device_count() >= 1

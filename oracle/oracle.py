@@ -348,9 +348,10 @@ def rmsnorm_rows(x, gamma=None, eps: float = 1e-6, dtype="f16",
     return y
 
 
-def layernorm_rows(x, gamma=None, beta=None, eps: float = 1e-5, dtype="f32",
+def layernorm_rows(x, gamma=None, beta=None, eps: float = 1e-5, dtype="f16",
                    threads: int = 0):
-    """Returns (y, mean, rstd) with mean/rstd fp32."""
+    """Returns (y, mean, rstd) with mean/rstd fp32.  dtype defaults to f16
+    (x as uint16 bit patterns), as for softmax_rows and rmsnorm_rows."""
     x, dt, y = _rows_io(x, dtype)
     rows, cols = x.shape
     g = None if gamma is None else np.ascontiguousarray(gamma, dtype=x.dtype)

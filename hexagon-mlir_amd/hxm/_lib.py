@@ -193,12 +193,38 @@ def _load():
             f"libhxm.so not found at {LIB_PATH}: build it first "
             "(python -c 'import __graft_entry__ as g; g.build()' or make -C "
             "hexagon-mlir_amd/csrc)")
-    lib = ctypes.CDLL(LIB_PATH)
+    cdll = ctypes.CDLL(LIB_PATH)
     for name, (res, args) in SIGNATURES.items():
-        fn = getattr(lib, name)
+        fn = getattr(cdll, name)
         fn.restype = res
         fn.argtypes = args
-    return lib
+    return _Lib(cdll)
+
+
+class _Entry:
+    """One entry of the C ABI with its argument count checked.  ctypes
+    rejects too few arguments but passes surplus ones on as if the function
+    were variadic: a call with one argument too many would hand the library
+    every pointer after it shifted by one, so the count is checked first."""
+
+    __slots__ = ("_fn", "_n", "__name__")
+
+    def __init__(self, fn, name):
+        self._fn, self._n, self.__name__ = fn, len(fn.argtypes), name
+
+    def __call__(self, *args):
+        if len(args) != self._n:
+            raise TypeError(f"{self.__name__} takes {self._n} arguments ({len(args)} given)")
+        return self._fn(*args)
+
+
+class _Lib:
+    """libhxm.so with every entry of SIGNATURES bound as an _Entry."""
+
+    def __init__(self, cdll):
+        self._cdll = cdll
+        for name in SIGNATURES:
+            setattr(self, name, _Entry(getattr(cdll, name), name))
 
 
 lib = _load()

@@ -35,6 +35,19 @@ def test_library_exports_every_declared_symbol():
         assert getattr(hxm.lib, s) is not None
 
 
+def test_binding_checks_the_argument_count():
+    """ctypes would pass a surplus argument on, shifting every pointer after
+    it; the binding refuses the call before it reaches the library."""
+    import pytest as _pytest
+    for name, (_, args) in _lib.SIGNATURES.items():
+        fn = getattr(hxm.lib, name)
+        with _pytest.raises(TypeError, match="takes"):
+            fn(*([None] * (len(args) + 1)))
+        if args:
+            with _pytest.raises(TypeError):
+                fn(*([None] * (len(args) - 1)))
+
+
 def test_status_strings_and_version():
     assert hxm.status_string(0) == "ok"
     assert hxm.status_string(3) == "unsupported-shape"

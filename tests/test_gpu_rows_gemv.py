@@ -96,6 +96,34 @@ def test_layernorm_constant_rows_give_beta(dev, rows, cols, name):
     np.testing.assert_allclose(rstd.cpu().numpy(), np.full(rows, want, np.float32), rtol=1e-6)
 
 
+@pytest.mark.parametrize("rows,cols", [(62, 8384), (68, 1293), (40, 300), (4, 4096)])
+def test_layernorm_f32_error_follows_the_conditioning(dev, rows, cols):
+    """f32 rows far from zero mean (x = 3 + 0.01 z, |mean| / sigma = 300): any
+    LayerNorm that holds the mean in fp32 shifts every x - mean by the mean's
+    rounding, a few ulp(|mean|), and rstd = 1/sigma scales that shift into y.
+    So y is held to 4 eps32 |mean| rstd max|gamma| on top of the 1e-5 that
+    well-conditioned rows meet, and to no worse than three times a float32
+    two-pass LayerNorm of the same rows (numpy, float32 throughout)."""
+    print(f"layernorm f32 conditioning {rows}x{cols}", flush=True)
+    g = torch.Generator().manual_seed(rows * cols)
+    x = torch.randn(rows, cols, generator=g) * 0.01 + 3.0
+    w = 1 + 0.1 * torch.randn(cols, generator=g)
+    b = 0.1 * torch.randn(cols, generator=g)
+    got = ops.layer_norm(x.to(dev), (cols,), w.to(dev), b.to(dev), eps=1e-5).cpu().numpy()
+    ry, rm, rr = orc.layernorm_rows(x.numpy(), w.numpy(), b.numpy(), 1e-5, "f32")
+    eps32 = float(np.finfo(np.float32).eps)
+    shift = 4 * eps32 * np.abs(rm) * rr * float(w.abs().max())
+    err = np.abs(got - ry)
+    assert (err <= 1e-5 + 1e-5 * np.abs(ry) + shift[:, None]).all()
+    xn = x.numpy()
+    m = xn.sum(axis=1, dtype=np.float32) / np.float32(cols)
+    c = xn - m[:, None]
+    r = np.float32(1) / np.sqrt((c * c).sum(axis=1, dtype=np.float32) / np.float32(cols)
+                                + np.float32(1e-5))
+    np32 = (c * r[:, None]) * w.numpy() + b.numpy()
+    assert err.max() <= 3 * np.abs(np32 - ry).max() + 2e-6
+
+
 def test_rows_golden(dev, golden):
     g = golden("rows")
     xs = torch.from_numpy(g["softmax_x_bits"].view(np.float16)).to(dev)

@@ -416,11 +416,14 @@ hxm_status plan_gemm(int32_t op, int32_t table, int epi, int32_t b_layout, int64
     p->workspace_bytes =
         extra_ws + (b_layout == HXM_B_KN && K > 0 ? N * kn_image_ld(K, eb) * eb : 0);
     p->k_slices = k_slices(K * eb, e->cfg.bk, split);
-    if (p->k_slices > 1) p->workspace_bytes += p->k_slices * M * N * 4;
-    if (p->k_slices > 1 && p->k_slices * M * N * 4 > kSplitKPlaneBytesMax) {
+    const bool planes_fit =
+        p->k_slices <= 1 || split_planes_fit(p->k_slices, M, N, kSplitKPlaneBytesMax);
+    if (p->k_slices > 1 && planes_fit) p->workspace_bytes += p->k_slices * M * N * 4;
+    if (!planes_fit) {
       snprintf(why, sizeof(why),
-               "split_k=%d needs %lld bytes of int32 partial planes, above the %lld-byte limit",
-               p->k_slices, (long long)(p->k_slices * M * N * 4),
+               "split_k=%d needs %d int32 partial planes of %lld x %lld, above the %lld-byte "
+               "limit",
+               p->k_slices, p->k_slices, (long long)M, (long long)N,
                (long long)kSplitKPlaneBytesMax);
       st = refuse(p, HXM_UNSUPPORTED_SHAPE, HXM_REASON_WORKSPACE_BUDGET, why);
     } else if (!grid_fits(p->tiles, e->threads, p->k_slices)) {
@@ -437,9 +440,6 @@ hxm_status plan_gemm(int32_t op, int32_t table, int epi, int32_t b_layout, int64
   if (entry) *entry = st == HXM_OK ? e : nullptr;
   return st;
 }
-
-namespace {
-}  // namespace
 
 // Shared by the entry points and the tuner.  planes / planes_cap: where a
 // K split keeps its int32 partial planes; nullptr takes the stream's

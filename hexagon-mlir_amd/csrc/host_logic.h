@@ -52,6 +52,17 @@ inline int32_t k_slices(int64_t k_bytes, int64_t stage_bytes, int32_t split) {
   return static_cast<int32_t>(ceil_div(stages, per));
 }
 
+// Whether `slices` int32 partial planes of [M, N] fit in max_bytes,
+// slices * M * N * 4 <= max_bytes, decided without forming the product:
+// extents_fit admits M and N up to 2^30 each, so with 16 slices the product
+// would pass 2^63.  For positive integers a * b <= c exactly when
+// a <= floor(c / b), and nested floor divisions equal one.
+inline bool split_planes_fit(int64_t slices, int64_t M, int64_t N, int64_t max_bytes) {
+  if (slices < 1 || M < 0 || N < 0 || max_bytes < 0) return false;
+  if (M == 0 || N == 0) return true;
+  return M <= max_bytes / 4 / slices / N;
+}
+
 // Stream-K layout of an int8-weight GEMM launch of `ntiles` tiles of KT K
 // stages each on `cus` CUs (one workgroup per CU): the first dp tiles, whole
 // rounds, run one per workgroup; the rest (tiles = ntiles mod cus) are cut

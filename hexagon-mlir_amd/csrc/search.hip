@@ -857,7 +857,7 @@ hxm_status hxm_tune_gemm(int32_t op, const void* A, int64_t lda, const void* B,
     const int cus = device_cu_count();
     if (op == HXM_I8 && cus > 0 && tiles * 2 <= cus) {
       for (int32_t s = 2; s <= 16 && tiles * s <= 2 * cus && (K + c.bk - 1) / c.bk >= s &&
-                          s * M * N * 4 <= kSplitKPlaneBytesMax;
+                          split_planes_fit(s, M, N, kSplitKPlaneBytesMax);
            s *= 2) {
         hxm_gemm_config sc = c;
         sc.split_k = s;

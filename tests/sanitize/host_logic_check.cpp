@@ -92,6 +92,35 @@ int main() {
           (long long)sb, split, s);
   }
 
+  // Split-K plane budgets: slices * M * N * 4 <= max_bytes without forming
+  // the product, against the 128-bit product (extents up to 2^30 and beyond).
+  for (int it = 0; it < 200000; ++it) {
+    const int64_t sl = rng() % 2 ? 1 << (rng() % 5) : any64();
+    const int64_t M = rng() % 2 ? static_cast<int64_t>(rng() % (1LL << 31)) : any64();
+    const int64_t N = rng() % 2 ? static_cast<int64_t>(rng() % (1LL << 31)) : any64();
+    const int64_t mx = rng() % 2 ? int64_t(256) << 20 : any64();
+    // The product in steps, each checked against mx <= 2^63 before the next
+    // factor, so no step passes 2^127.
+    auto ref = [&]() {
+      if (sl < 1 || M < 0 || N < 0 || mx < 0) return false;
+      if (M == 0 || N == 0) return true;
+      i128 p = static_cast<i128>(sl) * M;
+      if (p > mx) return false;
+      p *= N;
+      if (p > mx) return false;
+      return p * 4 <= mx;
+    };
+    const bool want = ref();
+    CHECK(hxm::split_planes_fit(sl, M, N, mx) == want, "split_planes_fit(%lld, %lld, %lld, %lld)",
+          (long long)sl, (long long)M, (long long)N, (long long)mx);
+  }
+  CHECK(hxm::split_planes_fit(16, 512, 512, int64_t(256) << 20) &&
+            !hxm::split_planes_fit(8, 4096, 4096, int64_t(256) << 20) &&
+            hxm::split_planes_fit(16, 1024, 4096, int64_t(256) << 20) &&
+            !hxm::split_planes_fit(16, 1024, 4097, int64_t(256) << 20) &&
+            !hxm::split_planes_fit(16, 1073741823, 1073741823, int64_t(256) << 20),
+        "split_planes_fit known answers");
+
   // Tuning-cache entries: exact fields back, range checks at both edges.
   hxm::CacheEntry e;
   CHECK(hxm::parse_cache_entry("4 4096 4096 4096 256 256 128 2 2 2 1 10\n", &e) && e.op == 4 &&

@@ -82,6 +82,12 @@ def test_split_k_limits():
     assert ok["workspace_bytes"] == 16 * 512 * 512 * 4
     big = plan(4096, 4096, 4096, I8, config=base + (8,))           # 8 planes of 64 MiB
     assert big["plan"] == "refused" and big["reason"] == "workspace-budget"
+    # The largest extents the planner admits: 16 planes of (2^30 - 1)^2 int32
+    # would pass 2^63 bytes; the budget check must not form that product.
+    huge = plan(2 ** 30 - 1, 2 ** 30 - 1, 4096, I8, config=base + (16,))
+    assert huge["plan"] == "refused" and huge["reason"] == "workspace-budget"
+    edge = plan(1024, 4096, 4096, I8, config=base + (16,))          # exactly 256 MiB
+    assert edge["plan"] == "mfma-full" and edge["workspace_bytes"] == 16 * 1024 * 4096 * 4
     f16 = plan(512, 512, 512, F16, config=hxm.search.gemm_configs(hxm.F16)[0].as_tuple()[:6] + (2,))
     assert f16["reason"] == "no-kernel"
 

@@ -146,6 +146,23 @@ hxm_status hxm_resident_weight(const void* src, int64_t ld, int64_t rows, int64_
     return fail(HXM_UNSUPPORTED_SHAPE,
                 "tile-alignment: resident W8A16 image needs K and ldw multiples of 16 and "
                 "a 16-byte aligned source");
+  // The image must be one its pack accepts: refused here, before the hash
+  // reads every element of the weight and synchronises the stream.  Within
+  // these limits rows * cols * 4 and the packed bytes stay far below 2^63.
+  // The GEMM image (and the f32 one) is built by 32x32 tiles of 256 threads
+  // on a (cols/32, rows/32) grid; the W8A16 image has the GEMV's 32-bit
+  // extents and one 64-lane group per 1 KiB block.
+  if (gemm && !grid_fits((cols + 31) / 32, 256, (rows + 31) / 32))
+    return fail(HXM_UNSUPPORTED_SHAPE,
+                "tile-alignment: resident GEMM image of [%lld, %lld] is beyond the pack's "
+                "launch grid (K <= %lld)",
+                (long long)rows, (long long)cols, (long long)(int64_t(65535) * 32));
+  if (!gemm && (rows > INT32_MAX - 16 || cols > INT32_MAX - 64 ||
+                !grid_fits((hxm_w8a16_packed_bytes(rows, cols) / 1024 * 64 + 255) / 256, 256)))
+    return fail(HXM_UNSUPPORTED_SHAPE,
+                "tile-alignment: resident W8A16 image of [%lld, %lld] is beyond the pack's "
+                "extents",
+                (long long)rows, (long long)cols);
   int dev = 0;
   hxm_status st = require_device(&dev);
   if (st != HXM_OK) return st;

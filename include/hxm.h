@@ -334,7 +334,9 @@ typedef enum hxm_image_kind {
  * element and its position), so equal content at another address hits and a
  * one-element change misses.  expect_dtype >= 0 and expect_shape (rows,
  * cols) != NULL are the caller's contract: a mismatch is refused
- * ("unsupported-dtype" / "invalid-argument") before anything is packed.
+ * ("unsupported-dtype" / "invalid-argument") before anything is packed, and
+ * so are extents the image's pack would refuse ("tile-alignment"), before
+ * the weight is hashed.
  * *image_dtype receives the image dtype.  Synchronises `stream` once (the
  * hash is read back), and once more when it builds a new image, so an
  * image is complete before any thread or stream can be handed it.  Images

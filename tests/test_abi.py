@@ -137,6 +137,23 @@ def _span_refusals():
             assert st == _lib.HXM_UNSUPPORTED_SHAPE and "packed image" in hxm.last_error()
         else:
             assert st == _lib.HXM_NO_DEVICE
+    # Resident images the pack would refuse are refused before the weight is
+    # hashed: a GEMM image past the pack's grid (K > 65535 * 32), a W8A16
+    # image past the GEMV's 32-bit extents.  At the limit the call goes on
+    # to the device check.
+    img, img_dt = ctypes.c_void_p(), ctypes.c_int32()
+
+    def resident(rows, cols, kind):
+        return L.hxm_resident_weight(16, cols, rows, cols, hxm.I8, -1, None, kind,
+                                     ctypes.byref(img), ctypes.byref(img_dt), None)
+    assert resident(65535 * 32 + 16, 16, _lib.IMAGE_GEMM) == _lib.HXM_UNSUPPORTED_SHAPE
+    assert "launch grid" in hxm.last_error()
+    assert resident(65535 * 32, 16, _lib.IMAGE_GEMM) == _lib.HXM_NO_DEVICE
+    assert resident(2 ** 31 - 1, 16, _lib.IMAGE_W8A16) == _lib.HXM_UNSUPPORTED_SHAPE
+    assert "beyond the pack's extents" in hxm.last_error()
+    assert resident(16, 2 ** 31 - 64, _lib.IMAGE_W8A16) == _lib.HXM_UNSUPPORTED_SHAPE
+    assert resident(1 << 16, 1 << 16, _lib.IMAGE_W8A16) == _lib.HXM_NO_DEVICE  # a 4 GiB image
+    assert resident(1 << 20, 1 << 20, _lib.IMAGE_W8A16) == _lib.HXM_UNSUPPORTED_SHAPE  # 1 TiB
 
 
 @pytest.mark.skipif("_gpu_present()", reason="a GPU box counts its gfx950 devices; "

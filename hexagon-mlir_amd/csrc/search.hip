@@ -52,6 +52,7 @@ constexpr int kEpiW8Code = 3, kEpiSwigluCode = 4;  // gemm.hip's Epilogue values
 constexpr int64_t kTileEdge = 32;
 constexpr int64_t kMinRows = 4;
 constexpr int64_t kFrontendMaxBlockNumel = 1048576;
+constexpr int64_t kLadderExtentMax = int64_t(1) << 62;  // padded extent fits int64
 constexpr int64_t kCroutonElemBytes = 2;
 constexpr double kCvFactor = 3.0;
 constexpr double kMarginFloor = 0.15;
@@ -535,9 +536,14 @@ const char* hxm_reason_string(int32_t reason) {
 }
 
 int32_t hxm_tile_ladder(int64_t extent, int64_t* out, int32_t cap) {
+  // The padded extent of anything above 2^62 is 2^63, which no int64 holds.
+  if (extent > kLadderExtentMax) return -1;
   std::vector<int64_t> v;
   const int64_t top = std::max(kTileEdge, next_pow2(extent));
-  for (int64_t r = kTileEdge; r <= top; r *= 2) v.push_back(r);
+  for (int64_t r = kTileEdge;; r *= 2) {  // doubling stops at top <= 2^62
+    v.push_back(r);
+    if (r >= top) break;
+  }
   if (is_pow2(extent) && std::find(v.begin(), v.end(), extent) == v.end())
     v.push_back(extent);
   std::sort(v.begin(), v.end());
@@ -549,9 +555,10 @@ int32_t hxm_tile_ladder(int64_t extent, int64_t* out, int32_t cap) {
 // alignment, then the strict VTCM budget on crouton bytes.
 int32_t hxm_hmx_tile_verdict(int64_t bm, int64_t bn, int64_t bk, int64_t vtcm_budget) {
   if (!is_pow2(bm) || !is_pow2(bn) || !is_pow2(bk)) return HXM_REASON_FRONTEND_BLOCK_LIMIT;
-  if (bm * bk > kFrontendMaxBlockNumel || bk * bn > kFrontendMaxBlockNumel ||
-      bm * bn > kFrontendMaxBlockNumel)
-    return HXM_REASON_FRONTEND_BLOCK_LIMIT;
+  // a * b > limit as a > limit / b (positive integers): the products of
+  // powers of two up to 2^62 would pass 2^63.
+  const int64_t lim = kFrontendMaxBlockNumel;
+  if (bm > lim / bk || bk > lim / bn || bm > lim / bn) return HXM_REASON_FRONTEND_BLOCK_LIMIT;
   if (bm <= kMinRows) return HXM_REASON_MIN_ROWS;
   if (bm % kTileEdge || bn % kTileEdge || bk % kTileEdge) return HXM_REASON_TILE_ALIGNMENT;
   const int64_t crouton = (bm * bk + bk * bn + bm * bn) * kCroutonElemBytes;
@@ -1059,8 +1066,12 @@ int32_t hxm_predict_tile_time(int64_t M, int64_t N, int64_t K, const hxm_gemm_co
   // A K split runs S workgroups per tile on K/S each, and its int32 partial
   // planes are written and read back once (a second launch sums them).
   const int64_t S = cfg->split_k > 1 ? cfg->split_k : 1;
-  const int64_t tiles = (M / bm) * (N / bn) * S;
-  const int64_t per_cu = (tiles + model->cus - 1) / model->cus;
+  // M and N are the caller's and unbounded: a tile count past int64 has no
+  // cell (tm, tn >= 1 here, since M and N are positive multiples of the tile).
+  const int64_t tm = M / bm, tn = N / bn;
+  if (tm > INT64_MAX / tn / S) return done(HXM_ABSTAIN_NO_CELL);
+  const int64_t tiles = tm * tn * S;
+  const int64_t per_cu = ceil_div(tiles, model->cus);
   p.units[0] = tiles;
   p.units[1] = per_cu;
   p.units[2] = K / bk;
@@ -1099,7 +1110,7 @@ int32_t hxm_rank_tile_candidates(int64_t M, int64_t N, int64_t K, int32_t ab_dty
   struct Key {
     int abst;
     double lb;
-    int64_t spans;
+    double spans;
     std::tuple<int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t> cfg;
   };
   std::vector<Key> keys(n);
@@ -1108,9 +1119,12 @@ int32_t hxm_rank_tile_candidates(int64_t M, int64_t N, int64_t K, int32_t ab_dty
     const hxm_gemm_config& c = cands[i];
     hxm_tile_prediction p;
     const int32_t a = hxm_predict_tile_time(M, N, K, &c, ab_dtype, out_dtype, model, &p);
-    int64_t spans = 0;
-    if (c.bm > 0 && c.bn > 0 && c.bk > 0)
-      spans = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ((K + c.bk - 1) / c.bk);
+    // span_count (hmx_search.py:221-232), the tiebreak after the modeled
+    // bound: in double, so no extent overflows it (exact below 2^53).
+    double spans = 0.0;
+    if (c.bm > 0 && c.bn > 0 && c.bk > 0 && M > 0 && N > 0 && K > 0)
+      spans = static_cast<double>(ceil_div(M, c.bm)) * static_cast<double>(ceil_div(N, c.bn)) *
+              static_cast<double>(ceil_div(K, c.bk));
     keys[i] = Key{a != HXM_ABSTAIN_NONE ? 1 : 0, a != HXM_ABSTAIN_NONE ? 0.0 : p.lb_us, spans,
                   std::make_tuple(c.bm, c.bn, c.bk, c.waves_m, c.waves_n, c.stages, c.split_k)};
     idx[i] = i;

@@ -67,6 +67,9 @@ def span_count(m: int, n: int, k: int, tiles) -> int:
 def tile_ladder(extent: int) -> tuple:
     buf = (ctypes.c_int64 * 64)()
     n = lib.hxm_tile_ladder(int(extent), buf, 64)
+    if n < 0:
+        raise ValueError(f"extent {extent} is above 2^62: its padded power of two has no "
+                         "64-bit form")
     return tuple(int(buf[i]) for i in range(min(n, 64)))
 
 

@@ -513,7 +513,8 @@ const char* hxm_reason_string(int32_t reason);
 
 /* hmx_search.tile_ladder (hmx_search.py:246-266): powers of two from 32 to
  * next_pow2(extent), plus extent itself when it is a power of two, sorted.
- * Writes up to cap values; returns the full count. */
+ * Writes up to cap values; returns the full count, or -1 for an extent
+ * above 2^62, whose padded power of two (2^63) no int64 holds. */
 int32_t hxm_tile_ladder(int64_t extent, int64_t* out, int32_t cap);
 
 /* hmx_search.tile_verdict (hmx_search.py:269-292), the reference's engine

@@ -180,6 +180,22 @@ def test_each_abstain_class():
     assert S.manifest_abstains(None) == S.ABSTAIN_MANIFEST
 
 
+def test_extents_past_int64_tile_counts():
+    """The reference's Python integers are unbounded; the C restatement's
+    extents are int64.  Shapes whose tile count passes int64 have no cell
+    (HBM-bound by heat, so only the count refuses them), the largest count
+    that fits is priced, and the ranking's span tiebreak takes any extent."""
+    c = S.gemm_configs(I8)[0]  # 256 x 256 x 128
+    big = 1 << 40               # (2^32 tiles)^2 = 2^64 > 2^63
+    assert S.predict_tile_time(big, big, 128, c, dtype=I8).abstain == S.ABSTAIN_NO_CELL
+    fits = S.predict_tile_time(1 << 38, 1 << 38, 128, c, dtype=I8)   # 2^60 tiles
+    assert fits.abstain is None and fits.units[0] == 1 << 60
+    huge = (2 ** 62, 2 ** 62, 2 ** 62)
+    legal = S.gemm_configs(I8)[:4]
+    order = S.rank_tile_candidates(huge, legal, dtype=I8)
+    assert sorted(order, key=lambda x: x.as_tuple()) == sorted(legal, key=lambda x: x.as_tuple())
+
+
 @pytest.mark.parametrize("dtype,peak_ops_per_clk_cu", [(I8, 8192), (F16, 4096), (BF16, 4096)])
 def test_lower_bound_never_beats_the_published_peaks(dtype, peak_ops_per_clk_cu):
     """MI355X: 256 CUs at 2.4 GHz, dense int8 8192 and f16/bf16 4096 ops per

@@ -43,6 +43,24 @@ def test_ladder_shape():
     assert S.tile_ladder(16) == (16, 32)
 
 
+def test_ladder_and_verdict_at_the_int64_edge():
+    """The reference's Python integers are unbounded; the C restatement takes
+    int64.  Up to 2^62 the ladder is the reference's (every power of two from
+    32, 57 rungs at 2^62); above it the padded power of two, 2^63, has no
+    int64 form and the ladder is refused.  The verdict's block-size products
+    of powers of two near 2^62 are decided without forming them."""
+    top = 1 << 62
+    assert S.tile_ladder(top) == tuple(1 << e for e in range(5, 63))
+    assert S.tile_ladder(top - 1) == S.tile_ladder(top)
+    assert S.tile_ladder((1 << 61) + 1)[-1] == top
+    for bad in (top + 1, (1 << 63) - 1):
+        with pytest.raises(ValueError):
+            S.tile_ladder(bad)
+    for dims in [(top, top, top), (top, 32, 32), (32, top, 32), (32, 32, top), (1 << 40, 1, 1),
+                 (1 << 31, 1 << 31, 1), (1024, 1024, 1), (1024, 1, 1024), (2048, 512, 1)]:
+        assert S.tile_verdict(*dims) == _rule_verdict(*dims), dims
+
+
 def test_enumerator_matches_rules_on_the_twelve_shapes():
     verdicts = set()
     for m, n, k in TWELVE_SHAPES:

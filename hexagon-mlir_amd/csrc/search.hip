@@ -619,7 +619,11 @@ double hxm_quantile(const double* samples, int32_t n, double q) {
 int32_t hxm_calibration_iters(double perf_us, double target_us, int32_t lo, int32_t hi) {
   const double per_iter = std::max(perf_us, 1.0);
   const double it = target_us / per_iter;
-  const int64_t n = is_fin(it) ? static_cast<int64_t>(it) : hi;
+  // The quotient is clipped to +-2^62 before the (truncating) conversion: a
+  // double past int64 has no defined conversion, and lo / hi are 32-bit, so
+  // the clip changes no result of the clamp below.
+  const double clip = 4611686018427387904.0;
+  const int64_t n = is_fin(it) ? static_cast<int64_t>(std::min(std::max(it, -clip), clip)) : hi;
   return static_cast<int32_t>(std::max<int64_t>(lo, std::min<int64_t>(hi, n)));
 }
 
@@ -631,6 +635,7 @@ int32_t hxm_calibration_iters(double perf_us, double target_us, int32_t lo, int3
 int32_t hxm_champion_walk(const double* q20, const double* q50, const double* q80,
                           int32_t n, int32_t start, int32_t* outcome,
                           double* delta_out, double* gate_out) {
+  if (n < 0 || (n > 0 && (!q20 || !q50 || !q80))) return -2;
   return hxm::gated_walk(
       n, start, [&](int i) { return hxm_arm_quantiles{q20[i], q50[i], q80[i]}; }, outcome,
       nullptr, delta_out, gate_out);

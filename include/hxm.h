@@ -552,7 +552,8 @@ int32_t hxm_calibration_iters(double perf_us, double target_us, int32_t lo,
  * (q50_inc - q50_ch)/q50_inc > max(3*max(cv_ch, cv_inc), 15%) (strict: a tie
  * keeps the incumbent).  outcome[i] (may be NULL): -1 not compared, 0 kept,
  * 1 takeover; delta_out/gate_out (may be NULL) receive the fractions.
- * Returns the champion's index, -1 when start is not a measured row. */
+ * Returns the champion's index, -1 when start is not a measured row, -2 for
+ * n < 0 or a NULL q20/q50/q80 with n > 0. */
 int32_t hxm_champion_walk(const double* q20, const double* q50,
                           const double* q80, int32_t n, int32_t start,
                           int32_t* outcome, double* delta_out,

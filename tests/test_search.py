@@ -88,6 +88,9 @@ def test_calibration_box():
     assert S.calibration_iters(10.0) == 1000
     assert S.calibration_iters(2_600_000.0) == 5
     assert S.calibration_iters(0.0) == 1000
+    # quotients past int64 (the reference's Python int() has no such limit)
+    assert S.calibration_iters(1.0, target_us=1e300) == 1000
+    assert S.calibration_iters(1.0, target_us=-1e300) == 5
 
 
 def test_bench_quantiles_and_failures():
@@ -265,3 +268,15 @@ def test_tune_cache_file_contract(tmp_path):
         S.tune_cache_load(str(bad))
     with pytest.raises(hxm.HxmError, match="cannot open"):
         S.tune_cache_load(str(tmp_path / "missing.txt"))
+
+
+def test_walk_and_round_refuse_missing_arrays():
+    """The C walk and round judge take caller arrays: a NULL array with rows
+    to read, or a negative row count, is refused (-2) rather than read."""
+    import ctypes
+    q = (ctypes.c_double * 2)(1.0, 2.0)
+    L = hxm.lib
+    assert L.hxm_champion_walk(None, q, q, 2, 0, None, None, None) == -2
+    assert L.hxm_champion_walk(q, q, q, -1, 0, None, None, None) == -2
+    assert L.hxm_champion_walk(q, q, q, 2, 0, None, None, None) == 0
+    assert L.hxm_judge_round(None, 2, 0, None, 0.0, None, None, None, None, None) == -2

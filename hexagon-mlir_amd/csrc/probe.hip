@@ -216,9 +216,12 @@ hxm_status hxm_probe_mfma(const void* a, int64_t a_bytes, const void* b, int64_t
   if (!a || !b || !aligned16(a) || !aligned16(b) || !sink)
     return fail(HXM_INVALID_ARG, "invalid-argument: probe_mfma needs 16-byte aligned operands "
                                  "and a sink");
-  if (mfma_per_wave <= 0 || mfma_per_wave % 32)
+  // At most 2^24 MFMAs per wave (about a third of a second per launch at the
+  // clock this load runs at), so one launch cannot hold the device for long.
+  if (mfma_per_wave <= 0 || mfma_per_wave % 32 || mfma_per_wave > (int64_t(1) << 24))
     return fail(HXM_INVALID_ARG, "invalid-argument: probe_mfma mfma_per_wave must be a positive "
-                                 "multiple of 32 (got %lld)", (long long)mfma_per_wave);
+                                 "multiple of 32, at most 2^24 (got %lld)",
+                (long long)mfma_per_wave);
   if (workgroups < 1 || workgroups > HXM_PROBE_SINK_WORDS)
     return fail(HXM_INVALID_ARG, "invalid-argument: probe_mfma workgroups in [1, %d]",
                 HXM_PROBE_SINK_WORDS);

@@ -478,7 +478,8 @@ hxm_status hxm_probe_read(const void* src, int64_t bytes, uint32_t* sink, void* 
 /* MFMA probe (measurement helper; no counterpart in the reference): the
  * practical ceiling of the MFMA-bound kernels.  `workgroups` workgroups of
  * four waves (one per SIMD, the GEMM kernels' occupancy: one per CU) each run
- * mfma_per_wave 32x32 MFMAs (a positive multiple of 32) of the GEMMs' shapes
+ * mfma_per_wave 32x32 MFMAs (a positive multiple of 32, at most 2^24: about
+ * a third of a second per launch) of the GEMMs' shapes
  * -- int8 x int8 (v_mfma_i32_32x32x32_i8), f16 x f16 or bf16 x bf16
  * (v_mfma_f32_32x32x16_*), or f16 x int8 (B converted to f16 as the W8A16
  * kernels do) -- on operand fragments read once from a[0, a_bytes) and

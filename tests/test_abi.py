@@ -154,6 +154,11 @@ def _span_refusals():
     assert resident(16, 2 ** 31 - 64, _lib.IMAGE_W8A16) == _lib.HXM_UNSUPPORTED_SHAPE
     assert resident(1 << 16, 1 << 16, _lib.IMAGE_W8A16) == _lib.HXM_NO_DEVICE  # a 4 GiB image
     assert resident(1 << 20, 1 << 20, _lib.IMAGE_W8A16) == _lib.HXM_UNSUPPORTED_SHAPE  # 1 TiB
+    # The MFMA probe's per-wave count is bounded (a launch stays short).
+    assert L.hxm_probe_mfma(16, 64, 16, 64, hxm.I8, hxm.I8, (1 << 24) + 32, 1, 16,
+                            None) == _lib.HXM_INVALID_ARG
+    assert L.hxm_probe_mfma(16, 64, 16, 64, hxm.I8, hxm.I8, 1 << 24, 1, 16,
+                            None) == _lib.HXM_NO_DEVICE
 
 
 @pytest.mark.skipif("_gpu_present()", reason="a GPU box counts its gfx950 devices; "

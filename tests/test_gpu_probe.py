@@ -69,3 +69,7 @@ def test_probe_mfma_refusals(dev):
     assert lib.hxm_probe_mfma(p, 8000 + 8, p, 8192, hxm.I8, hxm.I8, 32, 1, s, st) != 0
     assert lib.hxm_probe_mfma(p, 8192, p, 8192, hxm.I8, hxm.I8, 32, 0, s, st) != 0
     assert lib.hxm_probe_mfma(p, 8192, p, 8192, hxm.I8, hxm.I8, 32, 1, None, st) != 0
+    # past 2^24 MFMAs per wave a launch would hold the device for seconds
+    assert lib.hxm_probe_mfma(p, 8192, p, 8192, hxm.I8, hxm.I8, (1 << 24) + 32, 1, s,
+                              st) != 0
+    assert "2^24" in hxm.last_error()

@@ -1,12 +1,15 @@
-"""HIP graph capture of the memory-bound and FFN entries: the one-chunk and
-pipelined W8A16 GEMV kernels (full and small N), the row ops and the FFN's
-W8A16 GEMMs, captured once on a side stream, then replayed three times with
+"""HIP graph capture of the compute entries: the one-chunk and pipelined
+W8A16 GEMV kernels (full and small N), the row ops, the FFN's W8A16 GEMMs and
+the MFMA GEMMs (int8 dequant, an int8 K split through the stream's
+workspace, f16 on both kernels, f32 operands), captured once on a side
+stream after an eager call of each has grown the workspace, then replayed three times with
 eager work (inputs refreshed, outputs poisoned) and a synchronisation between
 replays; every replay must equal the eager result bit for bit (same kernels,
 same inputs), and the eager result itself matches the oracle elsewhere."""
 import pytest
 import torch
 
+import hxm
 import hxm.ops as ops
 
 pytestmark = pytest.mark.gpu
@@ -37,6 +40,33 @@ def test_replays_equal_the_eager_results(dev):
     Wgu, sgu = ops.swiglu_pack(Wg, Wu, sg, su)
     cases.append(("swiglu gate/up", lambda h: ops.gemm_w8a16_swiglu(xs, Wgu, sgu, 704, out=h),
                   torch.empty(256, 704, dtype=torch.float16, device=dev), xs))
+    # The MFMA GEMMs: int8 with the dequant epilogue on a resident B, an int8
+    # K split over a [K, N] B (pack and partial planes in the stream's
+    # workspace, grown by the eager call), f16 on the direct small-output
+    # kernel and on the LDS-staged one, and f32 operands (fp16 images in the
+    # workspace).
+    A8 = torch.randint(-127, 128, (300, 2048), generator=g, dtype=torch.int8).to(dev)
+    B8 = torch.randint(-127, 128, (2048, 200), generator=g, dtype=torch.int8).to(dev)
+    B8p = ops.prepack_weight(B8)
+    rs = (torch.rand(300, generator=g) * 0.02 + 0.001).to(dev)
+    cs = (torch.rand(200, generator=g) * 0.02 + 0.001).to(dev)
+    cases.append(("gemm_i8_dequant", lambda c: ops.gemm_i8_dequant(A8, B8p, rs, cs, out=c,
+                                                                    b_layout="nk"),
+                  torch.empty(300, 200, dtype=torch.float16, device=dev), A8))
+    split = hxm.GemmConfig(256, 256, 128, 2, 2, 2, 4)
+    cases.append(("gemm_i8 split 4", lambda c: ops.gemm_i8(A8, B8, out=c, config=split),
+                  torch.empty(300, 200, dtype=torch.int32, device=dev), A8))
+    a16, b16 = ((torch.rand(256, 256, generator=g) - 0.5).half().to(dev) for _ in range(2))
+    cases.append(("matmul f16 256^3", lambda c: ops.matmul(a16, b16, out=c),
+                  torch.empty(256, 256, dtype=torch.float16, device=dev), a16))
+    a2 = (torch.rand(384, 1024, generator=g) - 0.5).half().to(dev)
+    b2 = (torch.rand(1024, 640, generator=g) - 0.5).half().to(dev)
+    cases.append(("matmul f16 384x640x1024", lambda c: ops.matmul(a2, b2, out=c),
+                  torch.empty(384, 640, dtype=torch.float16, device=dev), a2))
+    a32 = torch.randn(200, 300, generator=g).to(dev)
+    b32 = torch.randn(300, 100, generator=g).to(dev)
+    cases.append(("matmul f32 operands", lambda c: ops.matmul(a32, b32, out=c),
+                  torch.empty(200, 100, dtype=torch.float32, device=dev), a32))
 
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
@@ -53,7 +83,7 @@ def test_replays_equal_the_eager_results(dev):
     for rep in range(3):
         for (_, _, out, inp), keep in zip(cases, saved):
             out.fill_(-7.0)                      # eager work between replays
-            inp.mul_(2.0).copy_(keep)            # touched and restored
+            inp.mul_(2).copy_(keep)              # touched and restored
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()

@@ -717,7 +717,8 @@ def cpu_model():
 
 
 def cpu_baselines(A, Bp, seconds):
-    """The C restatement (oracle/oracle.c) of every BASELINE config, timed on
+    """The C restatement (oracle/oracle.c) of every benchmark config (the five
+    workloads of `configs` in the JSON line), timed on
     the host cores: one build of it for this host (gcc -O3 -march=native
     -fopenmp, `make native` in oracle/; the checker's portable build when
     that fails), one thread count for every op (OMP_NUM_THREADS, else the
@@ -991,7 +992,7 @@ def _r(v, nd=4):
 
 
 def config_records(head, legs, cpu):
-    """One compact record per BASELINE config (the reference's per-test
+    """One compact record per benchmark config (the reference's per-test
     Test_Info {Name, Result, Perf, Units}, test/utils/dsp/include/
     test_report.h:35-70): q20 / q50 / q80 microseconds per launch, the rate
     at q50, its fraction of the nominal peak, the fraction of this library's

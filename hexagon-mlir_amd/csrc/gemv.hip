@@ -84,6 +84,27 @@ __global__ __launch_bounds__(256) void pack_w8a16_kernel(const int8_t* __restric
   *reinterpret_cast<v4i32*>(out + blk * 1024 + lane * 16) = v;
 }
 
+// The channel-group block a workgroup takes.  XCD_MAP: workgroups are
+// dispatched round-robin over the 8 XCDs, so ordinal b runs on XCD b % 8;
+// block x * (G / 8) + min(x, G % 8) + b / 8 (x = b % 8, G = gridDim.x, a
+// bijection for any G) gives each XCD one contiguous run of blocks, so the
+// XCD's resident workgroups read one contiguous eighth of the weight image.
+// A 45 MB read in 64 KiB pieces (one 16-channel group of K = 4096) took
+// 8.61 us with piece b on ordinal b (each XCD's pieces 512 KiB apart) and
+// 7.86 us with this order (one box, six passes).  The GEMV at N=11008,
+// K=4096 (three alternating passes, one box): M=1 8.95-9.05 against
+// 9.20-9.30 us in a stream, 8.84-8.97 against 8.99-9.05 us in a HIP graph;
+// M=16 (three groups per workgroup) 10.09-10.10 against 10.12-10.18 us;
+// M=4 (the pipelined kernel, one group) 9.75-9.78 against 9.63-9.68 us,
+// so that kernel keeps the plain order.
+template <bool XCD_MAP>
+__device__ __forceinline__ int gemv_block() {
+  const int b = blockIdx.x;
+  if constexpr (!XCD_MAP) return b;
+  const int G = gridDim.x, x = b & 7;
+  return x * (G >> 3) + min(x, G & 7) + (b >> 3);
+}
+
 // Wave 0, after every wave has written its partial 16x16 tiles to part:
 // the sum over the KW waves, the per-channel scale, one rounding to f16, the
 // store.  Lane l holds D[channel 4*(l/16) + v][m = l%16] of each group.
@@ -155,7 +176,7 @@ __global__ __launch_bounds__(256) void gemv_empty_k_kernel(GemvArgs g) {
 // load lands.  PACKED reads the resident image (1 KiB contiguous per wave
 // instruction); otherwise W is the plain [N, K] matrix (16 rows x 64 bytes
 // per instruction).
-template <int KW, int SPW, bool PACKED, int MR, int CB, bool LATE_SCALES>
+template <int KW, int SPW, bool PACKED, int MR, int CB, bool LATE_SCALES, bool XCD_MAP>
 __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
   constexpr int kChunkSlabs = KW * SPW;
   constexpr int kChunkK = kChunkSlabs * 64;
@@ -166,7 +187,8 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
   __shared__ v4f32 part[KW][CB][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * 16 * CB;
+  const int blk = gemv_block<XCD_MAP>();
+  const int n0 = blk * 16 * CB;
   const int m_base = blockIdx.y * 16;
   const int rows = min(MR, g.M - m_base);       // x rows of this M tile (host: <= MR)
   const int r16 = lane & 15;                    // W row (channel) for A; x row for B
@@ -197,7 +219,7 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
 #pragma unroll
   for (int b = 0; b < CB; ++b) {
     if constexpr (PACKED) {
-      const int grp = min(static_cast<int>(blockIdx.x) * CB + b, (g.N + 15) / 16 - 1);
+      const int grp = min(blk * CB + b, (g.N + 15) / 16 - 1);
       wsrc[b] = g.W + static_cast<int64_t>(grp) * slabs * 1024 + lane * 16;
     } else {
       const int n = n0 + 16 * b + r16;
@@ -313,7 +335,7 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_kernel(GemvArgs g) {
 // 11.4 us.  Two or four slabs per wave per chunk, all of K in one chunk, 2
 // or 4 channel groups per workgroup, 4 or 16 waves per workgroup: each
 // slower (10.5 to 14.6 us at M=16).
-template <int KW, int MR, int CB, bool LATE_SCALES>
+template <int KW, int MR, int CB, bool LATE_SCALES, bool XCD_MAP>
 __global__ __launch_bounds__(KW * 64) void gemv_w8a16_pipe_kernel(GemvArgs g) {
   constexpr int kChunkK = KW * 64;
   constexpr int kRowBytes = kChunkK * 2 + 16;   // padded x row in LDS
@@ -323,7 +345,8 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_pipe_kernel(GemvArgs g) {
   __shared__ v4f32 part[KW][CB][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * 16 * CB;
+  const int blk = gemv_block<XCD_MAP>();
+  const int n0 = blk * 16 * CB;
   const int m_base = blockIdx.y * 16;
   const int rows = min(MR, g.M - m_base);
   const int r16 = lane & 15;
@@ -345,7 +368,7 @@ __global__ __launch_bounds__(KW * 64) void gemv_w8a16_pipe_kernel(GemvArgs g) {
   __amdgpu_buffer_rsrc_t wr[CB];
 #pragma unroll
   for (int b = 0; b < CB; ++b) {
-    const int grp = min(static_cast<int>(blockIdx.x) * CB + b, groups - 1);
+    const int grp = min(blk * CB + b, groups - 1);
     wr[b] = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int8_t*>(g.W) + static_cast<int64_t>(grp) * slabs * 1024,
         static_cast<short>(0), slabs * 1024, 0x00020000);
@@ -536,25 +559,28 @@ hxm_status hxm_gemv_w8a16(const void* x, int64_t ldx, const int8_t* W, int64_t l
   // M <= 4 below kGemvPipeMinGroups): a 4096-wide K chunk (x rows fit LDS),
   // so at K <= 4096 each wave issues all its weight loads at once and makes
   // one memory round trip.  Otherwise the packed image at M > 1 takes the
-  // pipelined kernel, 512-wide chunks with the next chunk in flight.
+  // pipelined kernel, 512-wide chunks with the next chunk in flight.  The
+  // last template argument (XCD-contiguous channel groups, gemv_block) is
+  // on at M = 1 and with three groups per workgroup, where it measured
+  // faster, and off elsewhere.
   if (M <= 1) {
-    if (pk) gemv_w8a16_kernel<8, 8, true, 1, 1, true><<<grid(1), 512, 0, s>>>(g);
-    else gemv_w8a16_kernel<8, 8, false, 1, 1, true><<<grid(1), 512, 0, s>>>(g);
+    if (pk) gemv_w8a16_kernel<8, 8, true, 1, 1, true, true><<<grid(1), 512, 0, s>>>(g);
+    else gemv_w8a16_kernel<8, 8, false, 1, 1, true, true><<<grid(1), 512, 0, s>>>(g);
   } else if (M <= 4) {
     if (pk && (N + 15) / 16 >= kGemvPipeMinGroups)
-      gemv_w8a16_pipe_kernel<8, 4, 1, true><<<grid(1), 512, 0, s>>>(g);
+      gemv_w8a16_pipe_kernel<8, 4, 1, true, false><<<grid(1), 512, 0, s>>>(g);
     else if (pk)
-      gemv_w8a16_kernel<8, 8, true, 4, 1, true><<<grid(1), 512, 0, s>>>(g);
+      gemv_w8a16_kernel<8, 8, true, 4, 1, true, false><<<grid(1), 512, 0, s>>>(g);
     else
-      gemv_w8a16_kernel<8, 8, false, 4, 1, true><<<grid(1), 512, 0, s>>>(g);
+      gemv_w8a16_kernel<8, 8, false, 4, 1, true, false><<<grid(1), 512, 0, s>>>(g);
   } else {
     // 16 x rows: three channel groups per workgroup share each staged x
     // chunk (measured with the one-chunk kernel: 13.1 vs 14.7 us at
     // N=11008, K=4096), one group below kGemvCb3MinGroups.
-    if (pk && cb == 3) gemv_w8a16_pipe_kernel<8, 16, 3, false><<<grid(3), 512, 0, s>>>(g);
-    else if (pk) gemv_w8a16_pipe_kernel<8, 16, 1, false><<<grid(1), 512, 0, s>>>(g);
-    else if (cb == 3) gemv_w8a16_kernel<8, 4, false, 16, 3, false><<<grid(3), 512, 0, s>>>(g);
-    else gemv_w8a16_kernel<8, 4, false, 16, 1, false><<<grid(1), 512, 0, s>>>(g);
+    if (pk && cb == 3) gemv_w8a16_pipe_kernel<8, 16, 3, false, true><<<grid(3), 512, 0, s>>>(g);
+    else if (pk) gemv_w8a16_pipe_kernel<8, 16, 1, false, false><<<grid(1), 512, 0, s>>>(g);
+    else if (cb == 3) gemv_w8a16_kernel<8, 4, false, 16, 3, false, true><<<grid(3), 512, 0, s>>>(g);
+    else gemv_w8a16_kernel<8, 4, false, 16, 1, false, false><<<grid(1), 512, 0, s>>>(g);
   }
   return check_launch("gemv_w8a16");
 }

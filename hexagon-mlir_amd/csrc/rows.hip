@@ -174,7 +174,19 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int half = wv % S;  // this wave's share of the row
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * (kRowWaves / S) + wv / S;
+  // Softmax takes its row groups XCD-contiguously: workgroups are dispatched
+  // round-robin over the 8 XCDs, so ordinal b (on XCD x = b % 8) takes group
+  // x * (G / 8) + min(x, G % 8) + b / 8 of the G in the grid (a bijection),
+  // and each XCD streams one contiguous eighth of the rows.  Measured at
+  // 8192 x 4096 f16 (three alternating passes, one box): softmax 20.01-20.02
+  // against 20.16-20.22 us; RMSNorm 19.90-19.97 against 19.89-19.91 and
+  // LayerNorm 20.98-21.01 against 20.88-20.93, so those keep the plain order.
+  int blk = blockIdx.x;
+  if constexpr (OP == kSoftmax) {
+    const int G = gridDim.x, x = blk & 7;
+    blk = x * (G >> 3) + min(x, G & 7) + (blk >> 3);
+  }
+  const int64_t r = static_cast<int64_t>(blk) * (kRowWaves / S) + wv / S;
   if constexpr (S == 1) {
     if (r >= a.rows) return;  // whole wave leaves; no barriers below
   }

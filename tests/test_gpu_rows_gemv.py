@@ -300,3 +300,30 @@ def test_gemv_kernels_agree_bit_for_bit(dev):
     assert torch.equal(ops.gemv_w8a16(x[:1], W, sc), y1)           # plain layout
     for M in (4, 16):
         assert torch.equal(ops.gemv_w8a16(x[:M], Wp, sc)[:1], y1), f"M={M}"
+
+
+@pytest.mark.parametrize("r", range(8))
+@pytest.mark.parametrize("M", [1, 16])
+def test_gemv_group_order_covers_every_channel(dev, M, r):
+    """The XCD-contiguous order of the channel groups (M = 1, and M > 4 with
+    three groups per workgroup) maps the grid's G workgroups onto its G
+    blocks one to one for every G mod 8 = r: every channel of y is written
+    once, with its own row's dot product (y starts as NaN), packed and plain
+    weights."""
+    K = 128
+    blocks = 8 * 41 + r                       # grid size: M = 1 one group each, M = 16 three
+    N = 16 * blocks * (3 if M > 4 else 1) - 5  # the last group partial
+    print(f"gemv order M={M} N={N} grid={blocks}", flush=True)
+    g = torch.Generator().manual_seed(100 + 8 * M + r)
+    x = torch.randn(M, K, generator=g).half()
+    W = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sc = (torch.rand(N, generator=g) * 0.019 + 0.001).half()
+    ref = orc.f16_bits_to_f32(orc.gemv_w8a16(host_bits(x, "f16"), W.numpy(),
+                                             host_bits(sc, "f16")))
+    Wd = W.to(dev)
+    for Wx in (ops.prepack_w8a16(Wd), Wd):
+        y = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+        ops.gemv_w8a16(x.to(dev), Wx, sc.to(dev), out=y)
+        yc = y.float().cpu().numpy()
+        assert np.isfinite(yc).all()
+        np.testing.assert_allclose(yc, ref, rtol=1e-2, atol=1e-3)

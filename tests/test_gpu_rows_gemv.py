@@ -45,6 +45,22 @@ def test_softmax(dev, rows, cols, name):
     assert np.allclose(got.sum(axis=1), 1.0, atol=2e-2)
 
 
+@pytest.mark.parametrize("r", range(8))
+def test_softmax_row_order_covers_every_row(dev, r):
+    """Softmax takes its row groups XCD-contiguously: for every grid size
+    mod 8 = r (full f16 rows of 4096, one row per workgroup) each row is
+    written once, with its own softmax (y starts as NaN)."""
+    rows, cols = 8 * 9 + r, 4096
+    g = torch.Generator().manual_seed(300 + r)
+    x = (torch.randn(rows, cols, generator=g) * 2).half()
+    y = torch.full((rows, cols), float("nan"), dtype=torch.float16, device=dev)
+    ops.softmax(x.to(dev), out=y)
+    ref = orc.to_f32(orc.softmax_rows(host_bits(x, "f16"), "f16"), "f16")
+    got = y.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, ref, **tol("f16"))
+
+
 @pytest.mark.parametrize("rows,cols", ROW_SHAPES)
 @pytest.mark.parametrize("name", ["f16", "bf16", "f32"])
 def test_rmsnorm(dev, rows, cols, name):

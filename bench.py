@@ -1009,41 +1009,50 @@ def config_records(head, legs, cpu):
         return {"value": _r(v["value"], 4), "unit": v["unit"], "sample": v["sample"]} if v else None
 
     out = {}
+
+    def put(name, make):
+        """One config's record; a leg without the fields it needs is reported
+        as an error in its own record, never by losing the line."""
+        try:
+            out[name] = make()
+        except (KeyError, TypeError, ZeroDivisionError) as e:
+            out[name] = {"error": f"incomplete leg record: {e!r}"}
+
     f = legs.get("f16_matmul_256")
     if f and "error" not in f:
-        out["1_f16_matmul_256"] = {**base(f, "TFLOPS", "TFLOPS"),
-                                   "note": "launch-bound: time per launch replayed from a HIP "
-                                           "graph; no roofline fraction",
-                                   "cpu": cpu_of(1)}
+        put("1_f16_matmul_256", lambda: {
+            **base(f, "TFLOPS", "TFLOPS"),
+            "note": "launch-bound: time per launch replayed from a HIP graph; no roofline fraction",
+            "cpu": cpu_of(1)})
     ceil2 = legs.get("mfma_ceiling_int8_gemm_4096", {})
-    out["2_int8_gemm_4096_dequant"] = {**base(head, "TOPS", "TOPS", PEAK_INT8_TOPS),
-                                       "ceiling_frac": (_r(ceil2["q50_us"] / head["q50_us"])
-                                                        if "q50_us" in ceil2 else None),
-                                       "cpu": cpu_of(2)}
+    put("2_int8_gemm_4096_dequant", lambda: {
+        **base(head, "TOPS", "TOPS", PEAK_INT8_TOPS),
+        "ceiling_frac": _r(ceil2["q50_us"] / head["q50_us"]) if "q50_us" in ceil2 else None,
+        "cpu": cpu_of(2)})
     for M in (1, 4, 16):
         g = legs.get(f"w8a16_gemv_M{M}")
         if g:
-            out[f"3_w8a16_gemv_M{M}"] = {**base(g, "GB/s", "GB/s", PEAK_HBM_GBS),
-                                         "ceiling_frac": _r(g["ceiling_frac"]),
-                                         "graph_us": _r(g["graph_us"], 3),
-                                         "graph_frac": _r(g["graph_hbm_frac"]),
-                                         "cpu": cpu_of(f"3_M{M}")}
+            put(f"3_w8a16_gemv_M{M}", lambda g=g, M=M: {
+                **base(g, "GB/s", "GB/s", PEAK_HBM_GBS),
+                "ceiling_frac": _r(g["ceiling_frac"]), "graph_us": _r(g["graph_us"], 3),
+                "graph_frac": _r(g["graph_hbm_frac"]), "cpu": cpu_of(f"3_M{M}")})
     for name, key in (("softmax", "softmax_f16_8192x4096"), ("rmsnorm", "rmsnorm_f16_8192x4096")):
         g = legs.get(key)
         if g:
-            out[f"4_{key}"] = {**base(g, "GB/s", "GB/s", PEAK_HBM_GBS),
-                               "ceiling_frac": _r(g["ceiling_frac"]),
-                               "graph_us": _r(g["graph_us"], 3), "cpu": cpu_of(f"4_{name}")}
+            put(f"4_{key}", lambda g=g, name=name: {
+                **base(g, "GB/s", "GB/s", PEAK_HBM_GBS),
+                "ceiling_frac": _r(g["ceiling_frac"]), "graph_us": _r(g["graph_us"], 3),
+                "cpu": cpu_of(f"4_{name}")})
     g = legs.get("swiglu_ffn_2048x4096x11008")
     if g:
         ceil5 = legs.get("mfma_ceiling_swiglu_ffn_2048x4096x11008", {})
-        out["5_swiglu_ffn_2048x4096x11008"] = {
+        put("5_swiglu_ffn_2048x4096x11008", lambda: {
             **base(g, "TFLOPS", "TFLOPS", PEAK_F16_TFLOPS),
-            "ceiling_frac": (_r(ceil5["q50_us"] / g["q50_us"]) if "q50_us" in ceil5 else None),
+            "ceiling_frac": _r(ceil5["q50_us"] / g["q50_us"]) if "q50_us" in ceil5 else None,
             "stages_us": {k: _r(v, 2) for k, v in g["stages_us"].items()},
             "graph_us": _r(g["graph_us"], 2),
             "sclk_mhz": g["sclk_under_load"]["median_mhz"] if g.get("sclk_under_load") else None,
-            "tuned": g["tuned"], "cpu": cpu_of(5)}
+            "tuned": g["tuned"], "cpu": cpu_of(5)})
     return out
 
 

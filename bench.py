@@ -935,8 +935,12 @@ def main() -> int:
     log("int8 gemm+dequant 4096^3:", json.dumps(head))
     clk = sclk_under_load(c, c.last_step)
     log("sclk under load:", json.dumps(clk))
-    cpu_common, cpu = (None, {}) if args.no_cpu_baseline else cpu_baselines(A, Bp,
-                                                                           args.cpu_seconds)
+    cpu_common, cpu = None, {}
+    if not args.no_cpu_baseline:
+        try:
+            cpu_common, cpu = cpu_baselines(A, Bp, args.cpu_seconds)
+        except Exception as e:  # the CPU baseline is reported, not required for the line
+            log(f"cpu_baselines failed: {e!r}")
     log("cpu baselines", json.dumps([cpu_common, {str(k): v for k, v in cpu.items()}]))
 
     f16l, f16c = legs.get("f16_matmul_4096", {}), legs.get("mfma_ceiling_f16_matmul_4096", {})

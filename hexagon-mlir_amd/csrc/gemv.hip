@@ -20,7 +20,10 @@
 //     the K order inside an instruction is the same permutation for both
 //     operands, so the sum is the plain dot product;
 //   * the KW partial 16x16 tiles meet in LDS; wave 0 applies the per-channel
-//     scale and writes f16.
+//     scale and writes f16;
+//   * at M = 1 and with three channel groups per workgroup, the groups go to
+//     workgroups XCD-contiguously (gemv_block), so each XCD streams one
+//     contiguous eighth of the weight image.
 #include "device_util.h"
 #include "hxm_internal.h"
 
